@@ -1,0 +1,157 @@
+/*
+ * qwen_hip.h -- C ABI of the MI355X (gfx950) Qwen3-MoE decode engine.
+ *
+ * This is the drop-in boundary for the reference's compute backend.  The
+ * reference binds its backends through a Rust trait (src/backend.rs:14-23):
+ *
+ *     pub trait Backend {
+ *         fn matvec(&mut self, model: &Gguf, name: &str, expert: Option<usize>,
+ *                   x: &[f32]) -> Result<Vec<f32>>;
+ *         fn stats(&self) -> &Stats;
+ *     }
+ *
+ * and drives the token loop through `Model::forward` (src/model.rs:209-302).
+ * Each entry point below names the reference interface it replaces.
+ *
+ * Conventions (all entry points):
+ *   - return 0 on success, nonzero on failure; qh_last_error() then returns a
+ *     message owned by the context (the anyhow message of the reference);
+ *   - plain host pointers and sizes; caller-owned host buffers; the context
+ *     owns every device allocation;
+ *   - one context per host thread, calls block until host-visible outputs are
+ *     ready (`&mut self` + blocking poll in the reference);
+ *   - no silent CPU fallback: without a usable gfx950 device qh_create fails.
+ */
+#ifndef QWEN_HIP_H
+#define QWEN_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct qh_ctx qh_ctx;
+
+/* == backend::Stats (src/backend.rs:7-13). */
+typedef struct {
+    uint64_t matvecs;        /* matvecs performed (a fused token step counts the
+                                reference's 3 + 1 + 1 + 3*top per layer + 1)   */
+    uint64_t uploaded_bytes; /* host->device bytes (weights at load, inputs)  */
+    uint64_t cache_hits;     /* always 0: all weights stay resident in HBM    */
+    double matvec_ms;        /* wall time spent in matvec / forward calls     */
+} qh_stats_t;
+
+/* == model::Config (src/model.rs:5-19). */
+typedef struct {
+    uint64_t hidden, layers, heads, kvheads, head_dim, experts, top, intermediate,
+        vocab, max_context;
+    float eps, theta;
+} qh_config_t;
+
+/* Creates a context on HIP device `device` (one HIP stream per context).
+ * Replaces `Vulkan::new` (src/backend.rs:95-161) / `Compute::backend`
+ * (src/main.rs:42-60).  Fails if the device is not gfx950. */
+int qh_create(int device, qh_ctx **out);
+void qh_destroy(qh_ctx *ctx);
+/* Message of the last failure on this context (or of qh_create when ctx is
+ * NULL). */
+const char *qh_last_error(const qh_ctx *ctx);
+
+/* Parses and validates a GGUF image held in host memory and uploads every
+ * tensor to HBM once (no LRU cache, no buffer splitting).  Replaces
+ * `Gguf::open` (src/gguf.rs:102-195) + `Model::new` (src/model.rs:173-201)
+ * with the same checks and error behaviour; `context` is the `--ctx` limit.
+ * A new load invalidates the previous model (src/backend.rs:357-361). */
+int qh_load_model(qh_ctx *ctx, const void *gguf_image, size_t len, size_t context);
+/* Same, reading the file at `path`. */
+int qh_load_model_file(qh_ctx *ctx, const char *path, size_t context);
+int qh_model_config(const qh_ctx *ctx, qh_config_t *out);
+/* == Gguf::tensor (src/gguf.rs:196-200): GGML kind, rank and dims of a
+ * loaded tensor (dims[0] = columns); "missing tensor {name}" otherwise. */
+int qh_tensor_info(const qh_ctx *ctx, const char *name, uint32_t *kind, size_t *rank,
+                   uint64_t dims[3]);
+/* Sum of tensor payload bytes (src/main.rs:128 packed_weight_bytes). */
+int qh_packed_weight_bytes(const qh_ctx *ctx, uint64_t *out);
+
+/* == Backend::matvec (src/backend.rs:14-23, resolution as `matrix`
+ * src/backend.rs:57-75): y[rows] = W x for tensor `name`, expert slab
+ * `expert` (-1 = None).  Errors: missing tensor, rank mismatch, expert out
+ * of bounds, cols != len(x). */
+int qh_matvec(qh_ctx *ctx, const char *name, int64_t expert, const float *x, size_t cols,
+              float *y, size_t rows);
+/* == Backend::stats (src/backend.rs:22). */
+int qh_stats(const qh_ctx *ctx, qh_stats_t *out);
+
+/* == Vulkan::packed_matvec test surface (src/backend.rs:173-182): packed
+ * GGUF rows given directly.  kind is the GGML type id (0 F32, 1 F16, 2 Q4_0,
+ * 8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K). */
+int qh_packed_matvec(qh_ctx *ctx, const void *data, size_t len, uint32_t kind, size_t rows,
+                     size_t cols, const float *x, float *y);
+
+/* == quant::decode (src/quant.rs:81-84) on the device, for `rows` packed
+ * rows: out[rows*cols].  Bit-exact with the reference decoder. */
+int qh_dequant(qh_ctx *ctx, const void *data, size_t len, uint32_t kind, size_t rows, size_t cols,
+               float *out);
+
+/* == ops::route (src/ops.rs:45-56): top `top` expert ids (descending, total
+ * order, lower index on ties) and softmax over the chosen logits. */
+int qh_route(qh_ctx *ctx, const float *logits, size_t n, size_t top, uint32_t *ids, float *w);
+
+/* == Sampler::sample with temperature 0 (src/sampling.rs:26-35). */
+int qh_argmax(qh_ctx *ctx, const float *logits, size_t n, uint32_t *out);
+
+/* == ops::attention (src/ops.rs:57-98); k/v time-major [t][kvheads][d],
+ * klen = t*kvheads*d floats. */
+int qh_attention(qh_ctx *ctx, const float *q, const float *k, const float *v, size_t klen,
+                 size_t heads, size_t kvheads, size_t d, float *out);
+
+/* == Model::forward (src/model.rs:209-216): one causal token step on the
+ * device (embedding, every layer, KV append, final norm, vocab projection,
+ * finite check).  logits (vocab floats) and argmax may be NULL.  On error the
+ * KV cache and position are reset, as the reference rolls back. */
+int qh_forward(qh_ctx *ctx, uint32_t token, float *logits, uint32_t *argmax);
+/* Sequential prefill of `n_prompt` tokens followed by `n_new` greedy tokens,
+ * all chained on the device with no per-token host round trip (the
+ * src/main.rs:250-282 loop with temperature 0).  out_tokens receives the
+ * n_new generated ids; logits_last (vocab floats, nullable) the logits that
+ * produced the last generated token. */
+int qh_generate(qh_ctx *ctx, const uint32_t *prompt, size_t n_prompt, size_t n_new,
+                uint32_t *out_tokens, float *logits_last);
+/* == Model::reset (src/model.rs:202-208). */
+int qh_reset(qh_ctx *ctx);
+/* == Model::position (src/model.rs:170). */
+int qh_position(const qh_ctx *ctx, size_t *out);
+
+/* One decoder layer (the loop body src/model.rs:227-287) applied to x[hidden]
+ * in place at position `pos`, with this layer's KV history replaced by
+ * kprev/vprev (time-major, `pos` positions).  ids/w (nullable) receive the
+ * routed experts.  Resets the model position to 0 afterwards. */
+int qh_layer_forward(qh_ctx *ctx, size_t layer, float *x, size_t pos, const float *kprev,
+                     const float *vprev, uint32_t *ids, float *w);
+
+/* Benchmark surface: `warmup` untimed then `steps` timed greedy decode steps
+ * continuing from the current position, timed with HIP events on the
+ * context's stream.  ms_total receives the timed milliseconds. */
+int qh_bench_decode(qh_ctx *ctx, size_t warmup, size_t steps, double *ms_total);
+
+/* Per-kernel-class timing of `steps` decode steps launched one kernel at a
+ * time with HIP events between kernels on the context's stream (continuing
+ * from the current position).  ms_by_class[QH_NUM_KERNEL_CLASSES] receives
+ * the mean GPU milliseconds per token of each class, in this order:
+ * embed, rms_qkv, qk_norm_rope, attention, oproj, router, gateup, down,
+ * final (norm + vocab + argmax). */
+#define QH_NUM_KERNEL_CLASSES 9
+int qh_profile_step(qh_ctx *ctx, size_t steps, double *ms_by_class, size_t nclass);
+
+/* Benchmark surface for single matvecs with device-resident inputs: uploads
+ * `copies` copies of the packed matrix (so successive launches stream
+ * distinct HBM and do not hit the 256 MB MALL), then times `iters` launches
+ * rotating over the copies.  ms_per_launch receives the mean launch time. */
+int qh_bench_matvec(qh_ctx *ctx, const void *data, size_t len, uint32_t kind, size_t rows,
+                    size_t cols, size_t copies, size_t iters, double *ms_per_launch);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

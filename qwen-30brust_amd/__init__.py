@@ -1,0 +1,272 @@
+"""MI355X (gfx950) Qwen3-MoE decode engine: Python host mirror of the
+reference's backend interface over the engine's C ABI (include/qwen_hip.h).
+
+The reference exposes (src/backend.rs:14-23, src/model.rs:163-302):
+
+    trait Backend { fn matvec(&mut self, model, name, expert, x) -> Vec<f32>;
+                    fn stats(&self) -> &Stats; }
+    Model::new(gguf, context) / forward(token, backend) / reset() / position
+
+Here the same surface is `HipBackend.matvec(name, expert, x)` /
+`HipBackend.stats()` and `Model(image_or_path, context)` with
+`.forward(token)`, `.reset()`, `.position`, all running on the GPU through
+libqwen_hip.so.  There is no CPU fallback: without the built library or a
+gfx950 device every entry raises.
+
+Import with importlib (the package directory name contains a hyphen):
+    qh = importlib.import_module("qwen-30brust_amd")
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "libqwen_hip.so")
+
+KINDS = {"F32": 0, "F16": 1, "Q4_0": 2, "Q8_0": 8, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+
+
+class EngineError(RuntimeError):
+    """A failure reported by the engine (the reference's anyhow error)."""
+
+
+class _Stats(C.Structure):
+    _fields_ = [("matvecs", C.c_uint64), ("uploaded_bytes", C.c_uint64),
+                ("cache_hits", C.c_uint64), ("matvec_ms", C.c_double)]
+
+
+class _Config(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("hidden", "layers", "heads", "kvheads", "head_dim",
+                                          "experts", "top", "intermediate", "vocab",
+                                          "max_context")] + \
+               [("eps", C.c_float), ("theta", C.c_float)]
+
+
+_SIGS = {
+    "qh_create": (C.c_int, [C.c_int, C.POINTER(C.c_void_p)]),
+    "qh_destroy": (None, [C.c_void_p]),
+    "qh_last_error": (C.c_char_p, [C.c_void_p]),
+    "qh_load_model": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t]),
+    "qh_load_model_file": (C.c_int, [C.c_void_p, C.c_char_p, C.c_size_t]),
+    "qh_model_config": (C.c_int, [C.c_void_p, C.POINTER(_Config)]),
+    "qh_packed_weight_bytes": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint64)]),
+    "qh_tensor_info": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_uint32), C.POINTER(C.c_size_t),
+                                 C.POINTER(C.c_uint64 * 3)]),
+    "qh_matvec": (C.c_int, [C.c_void_p, C.c_char_p, C.c_int64, C.c_void_p, C.c_size_t,
+                            C.c_void_p, C.c_size_t]),
+    "qh_stats": (C.c_int, [C.c_void_p, C.POINTER(_Stats)]),
+    "qh_packed_matvec": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint32, C.c_size_t,
+                                   C.c_size_t, C.c_void_p, C.c_void_p]),
+    "qh_dequant": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint32, C.c_size_t,
+                             C.c_size_t, C.c_void_p]),
+    "qh_route": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p,
+                           C.c_void_p]),
+    "qh_argmax": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.POINTER(C.c_uint32)]),
+    "qh_attention": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
+                               C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p]),
+    "qh_forward": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.POINTER(C.c_uint32)]),
+    "qh_generate": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p,
+                              C.c_void_p]),
+    "qh_reset": (C.c_int, [C.c_void_p]),
+    "qh_position": (C.c_int, [C.c_void_p, C.POINTER(C.c_size_t)]),
+    "qh_layer_forward": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p,
+                                   C.c_void_p, C.c_void_p, C.c_void_p]),
+    "qh_bench_decode": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(C.c_double)]),
+    "qh_profile_step": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]),
+    "qh_bench_matvec": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint32, C.c_size_t,
+                                  C.c_size_t, C.c_size_t, C.c_size_t, C.POINTER(C.c_double)]),
+}
+
+_lib = None
+
+
+def lib():
+    """Loads libqwen_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise EngineError(f"{LIB_PATH} is missing: build it with `python -c "
+                              f"'import __graft_entry__ as g; g.build()'` (no CPU fallback)")
+        l = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(l, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = l
+    return _lib
+
+
+def _ptr(a):
+    return a.ctypes.data if a is not None and a.size else None
+
+
+def _f32(x):
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+class Device:
+    """One engine context (one HIP stream) on a gfx950 device."""
+
+    def __init__(self, device=0):
+        h = C.c_void_p()
+        if lib().qh_create(device, C.byref(h)) != 0:
+            raise EngineError(lib().qh_last_error(None).decode())
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().qh_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def _check(self, rc):
+        if rc != 0:
+            raise EngineError(lib().qh_last_error(self.h).decode())
+
+    # ---- raw test surfaces -------------------------------------------------
+    def packed_matvec(self, data, kind, rows, cols, x):
+        """== Vulkan::packed_matvec (src/backend.rs:173-182)."""
+        d = np.ascontiguousarray(np.frombuffer(data, np.uint8) if isinstance(data, (bytes, bytearray)) else data, np.uint8)
+        x = _f32(x)
+        y = np.empty(max(rows, 1), np.float32)
+        self._check(lib().qh_packed_matvec(self.h, _ptr(d), d.size, kind, rows, cols, _ptr(x), _ptr(y)))
+        return y[:rows]
+
+    def dequant(self, data, kind, rows, cols):
+        """== quant::decode (src/quant.rs:81-84) for `rows` packed rows."""
+        d = np.ascontiguousarray(np.frombuffer(data, np.uint8) if isinstance(data, (bytes, bytearray)) else data, np.uint8)
+        out = np.empty(max(rows * cols, 1), np.float32)
+        self._check(lib().qh_dequant(self.h, _ptr(d), d.size, kind, rows, cols, _ptr(out)))
+        return out[: rows * cols].reshape(rows, cols)
+
+    def route(self, logits, top):
+        """== ops::route (src/ops.rs:45-56)."""
+        lg = _f32(logits)
+        ids = np.zeros(max(top, 1), np.uint32)
+        w = np.zeros(max(top, 1), np.float32)
+        self._check(lib().qh_route(self.h, _ptr(lg), lg.size, top, _ptr(ids), _ptr(w)))
+        return ids[:top], w[:top]
+
+    def argmax(self, logits):
+        """== Sampler::sample, temperature 0 (src/sampling.rs:26-35)."""
+        lg = _f32(logits)
+        out = C.c_uint32()
+        self._check(lib().qh_argmax(self.h, _ptr(lg), lg.size, C.byref(out)))
+        return out.value
+
+    def attention(self, q, k, v, heads, kvheads, d):
+        """== ops::attention (src/ops.rs:57-98), time-major k/v."""
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        if k.size != v.size or q.size != heads * d:
+            raise EngineError("attention shape mismatch")
+        out = np.empty(heads * d, np.float32)
+        self._check(lib().qh_attention(self.h, _ptr(q), _ptr(k), _ptr(v), k.size, heads, kvheads, d, _ptr(out)))
+        return out
+
+    def bench_matvec(self, data, kind, rows, cols, copies, iters):
+        d = np.ascontiguousarray(data, np.uint8)
+        ms = C.c_double()
+        self._check(lib().qh_bench_matvec(self.h, _ptr(d), d.size, kind, rows, cols, copies, iters, C.byref(ms)))
+        return ms.value
+
+
+class Model:
+    """== model::Model on the GPU: `Model(image_or_path, context)`."""
+
+    def __init__(self, source, context, device=None):
+        self.dev = device if device is not None else Device(0)
+        if isinstance(source, (str, os.PathLike)):
+            self.dev._check(lib().qh_load_model_file(self.dev.h, os.fspath(source).encode(), context))
+        else:
+            buf = np.frombuffer(source, np.uint8) if not isinstance(source, np.ndarray) else source
+            buf = np.ascontiguousarray(buf, np.uint8)
+            self.dev._check(lib().qh_load_model(self.dev.h, _ptr(buf), buf.size, context))
+        c = _Config()
+        self.dev._check(lib().qh_model_config(self.dev.h, C.byref(c)))
+        self.config = {n: getattr(c, n) for n, _ in _Config._fields_}
+        self.context = context
+
+    @property
+    def position(self):
+        p = C.c_size_t()
+        lib().qh_position(self.dev.h, C.byref(p))
+        return p.value
+
+    def packed_weight_bytes(self):
+        v = C.c_uint64()
+        self.dev._check(lib().qh_packed_weight_bytes(self.dev.h, C.byref(v)))
+        return v.value
+
+    def tensor(self, name):
+        """== Gguf::tensor: {"kind", "dims"} of a loaded tensor."""
+        kind, rank, dims = C.c_uint32(), C.c_size_t(), (C.c_uint64 * 3)()
+        self.dev._check(lib().qh_tensor_info(self.dev.h, name.encode(), C.byref(kind), C.byref(rank), C.byref(dims)))
+        return {"kind": kind.value, "dims": list(dims)[: rank.value]}
+
+    def reset(self):
+        self.dev._check(lib().qh_reset(self.dev.h))
+
+    def forward(self, token, want_logits=True):
+        """== Model::forward: returns the logits (and keeps the argmax)."""
+        lg = np.empty(self.config["vocab"], np.float32) if want_logits else None
+        am = C.c_uint32()
+        self.dev._check(lib().qh_forward(self.dev.h, token, _ptr(lg), C.byref(am)))
+        self.last_argmax = am.value
+        return lg
+
+    def generate(self, prompt, n_new, want_logits=False):
+        """Sequential prefill of `prompt` then `n_new` greedy tokens on device."""
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(max(n_new, 1), np.uint32)
+        lg = np.empty(self.config["vocab"], np.float32) if want_logits else None
+        self.dev._check(lib().qh_generate(self.dev.h, _ptr(p), p.size, n_new, _ptr(out), _ptr(lg)))
+        return (out[:n_new], lg) if want_logits else out[:n_new]
+
+    def layer_forward(self, layer, x, pos, kprev, vprev):
+        x = np.array(x, np.float32)
+        top = self.config["top"]
+        ids = np.zeros(top, np.uint32)
+        w = np.zeros(top, np.float32)
+        kp = _f32(kprev) if pos else None
+        vp = _f32(vprev) if pos else None
+        self.dev._check(lib().qh_layer_forward(self.dev.h, layer, _ptr(x), pos, _ptr(kp), _ptr(vp), _ptr(ids), _ptr(w)))
+        return x, ids, w
+
+    KERNEL_CLASSES = ["embed", "rms_qkv", "qk_norm_rope", "attention", "oproj", "router",
+                      "gateup", "down", "final"]
+
+    def profile_step(self, steps):
+        """Mean GPU ms per token of each kernel class (events between kernels)."""
+        out = np.zeros(len(self.KERNEL_CLASSES), np.float64)
+        self.dev._check(lib().qh_profile_step(self.dev.h, steps, _ptr(out), out.size))
+        return dict(zip(self.KERNEL_CLASSES, out.tolist()))
+
+    def bench_decode(self, warmup, steps):
+        ms = C.c_double()
+        self.dev._check(lib().qh_bench_decode(self.dev.h, warmup, steps, C.byref(ms)))
+        return ms.value
+
+
+class HipBackend:
+    """== backend::Backend for a loaded Model: matvec(name, expert, x) and
+    stats() (src/backend.rs:14-23)."""
+
+    def __init__(self, model):
+        self.model = model
+
+    def matvec(self, name, expert, x):
+        x = _f32(x)
+        dims = self.model.tensor(name)["dims"]
+        rows = dims[1] if len(dims) > 1 else 1
+        y = np.empty(rows, np.float32)
+        dev = self.model.dev
+        dev._check(lib().qh_matvec(dev.h, name.encode(), -1 if expert is None else expert,
+                                   _ptr(x), x.size, _ptr(y), rows))
+        return y
+
+    def stats(self):
+        s = _Stats()
+        lib().qh_stats(self.model.dev.h, C.byref(s))
+        return {n: getattr(s, n) for n, _ in _Stats._fields_}

@@ -1,0 +1,978 @@
+// Host side of the decode engine: model upload, the captured token-step
+// graph, and the C ABI declared in include/qwen_hip.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fcntl.h>
+#include <map>
+#include <memory>
+#include <string>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+#include <vector>
+
+#include "../../include/qwen_hip.h"
+#include "gguf.hpp"
+#include "kernels.hpp"
+#include "qh_rows.hpp"
+
+namespace qh {
+// Kernels (kernels.hip).
+__global__ void k_repack(const uint8_t*, uint8_t*, uint32_t, uint32_t, size_t, size_t, size_t);
+__global__ void k_dequant(DevMat, size_t, size_t, float*);
+template <int R> __global__ void k_matvec(DevMat, const float*, float*, int);
+__global__ void k_route(const float*, uint32_t, uint32_t, uint32_t*, float*, uint32_t*);
+__global__ void k_argmax(const float*, uint32_t, int32_t*, uint32_t*, uint32_t*, uint32_t*, uint32_t*);
+__global__ void k_attention_api(AttnArgs, uint32_t);
+__global__ void k_embed(DevMat, Acts, ModelDims);
+template <int R> __global__ void k_rms_qkv(LayerW, Acts, ModelDims);
+__global__ void k_qk_norm_rope(LayerW, Acts, ModelDims);
+__global__ void k_attention(AttnArgs, Acts, ModelDims);
+template <int R> __global__ void k_oproj(LayerW, Acts, ModelDims);
+template <int R> __global__ void k_router(LayerW, Acts, ModelDims);
+template <int P> __global__ void k_gateup(LayerW, Acts, ModelDims);
+template <int R> __global__ void k_down(LayerW, Acts, ModelDims);
+template <int R> __global__ void k_final(DevMat, const float*, Acts, ModelDims);
+}  // namespace qh
+
+using namespace qh;
+
+#define HIP_OK(expr)                                                                          \
+    do {                                                                                      \
+        hipError_t e_ = (expr);                                                               \
+        if (e_ != hipSuccess) throw Error(std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+namespace {
+
+constexpr uint32_t kMaxGrid = 2048;  // grid-stride cap for matvec-shaped kernels
+
+uint32_t pad32h(uint64_t n) { return (uint32_t)((n + 31) / 32 * 32); }
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t n = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    DevBuf(DevBuf&& o) noexcept : p(o.p), n(o.n) { o.p = nullptr; o.n = 0; }
+    DevBuf& operator=(DevBuf&& o) noexcept {
+        if (this != &o) { release(); p = o.p; n = o.n; o.p = nullptr; o.n = 0; }
+        return *this;
+    }
+    ~DevBuf() { release(); }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+    void alloc(size_t bytes) {
+        release();
+        HIP_OK(hipMalloc(&p, std::max<size_t>(bytes, 256)));
+        n = bytes;
+    }
+    // Grows (never shrinks) to at least `bytes`.
+    void reserve(size_t bytes) {
+        if (p && n >= bytes) return;
+        alloc(bytes);
+    }
+    template <class T> T* as() const { return reinterpret_cast<T*>(p); }
+};
+
+struct HostPinned {
+    void* p = nullptr;
+    size_t n = 0;
+    ~HostPinned() { if (p) (void)hipHostFree(p); }
+    void reserve(size_t bytes) {
+        if (p && n >= bytes) return;
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        HIP_OK(hipHostMalloc(&p, bytes));
+        n = bytes;
+    }
+};
+
+struct ModelTensor {
+    uint32_t kind = 0;
+    std::vector<uint64_t> dims;
+    DevBuf buf;
+    DevMat mat{};   // rank >= 2 (per-expert view for rank 3 via expert_stride)
+    DevBuf f32;     // rank 1: decoded f32 vector
+};
+
+DevMat make_mat(const uint8_t* w, uint32_t kind, uint64_t rows, uint64_t cols, uint64_t experts) {
+    DevMat m{};
+    m.w = w;
+    m.kind = kind;
+    m.rows = (uint32_t)rows;
+    m.cols = (uint32_t)cols;
+    m.drb = (uint32_t)dev_row_bytes(kind, cols);
+    m.geo = row_geo(kind, cols);
+    m.expert_stride = experts ? (size_t)rows * m.drb : 0;
+    return m;
+}
+
+uint32_t blocks_for(uint64_t waves) {
+    uint64_t b = (waves + kWaves - 1) / kWaves;
+    return (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(b, kMaxGrid));
+}
+uint64_t groups_host(uint64_t rows, uint64_t cols, int R) {
+    int L = lanes_per_row((uint32_t)cols);
+    uint64_t per = (uint64_t)R * (64 / L);
+    return (rows + per - 1) / per;
+}
+
+}  // namespace
+
+struct qh_ctx {
+    int device = 0;
+    hipStream_t s = nullptr;
+    std::string err;
+    qh_stats_t stats{};
+
+    // model
+    bool loaded = false;
+    Config cfg{};
+    ModelDims dm{};
+    uint64_t packed = 0;
+    std::map<std::string, ModelTensor> tensors;
+    std::vector<LayerW> layers;
+    std::vector<AttnArgs> attn;
+    DevMat emb{}, out{};
+    const float* onorm = nullptr;
+    size_t context = 0, pos = 0;
+
+    // activations / caches
+    DevBuf acts_buf, kv, rope_buf;
+    Acts acts{};
+    uint32_t max_chunks = 0, tc = 32;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+
+    // launch geometry of the step kernels
+    uint32_t g_embed = 1, g_qkv = 1, g_qkn = 1, g_o = 1, g_router = 1, g_gu = 1, g_down = 1, g_final = 1;
+    size_t lds_h = 0, lds_attn = 0, lds_o = 0, lds_router = 0, lds_down = 0;
+
+    // scratch for the API surfaces
+    DevBuf sa, sb, sc, sd;
+    HostPinned pin;
+
+    ~qh_ctx() { drop_model(); if (s) (void)hipStreamDestroy(s); }
+
+    void drop_model() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        exec = nullptr;
+        graph = nullptr;
+        tensors.clear();
+        layers.clear();
+        attn.clear();
+        acts_buf.release();
+        kv.release();
+        rope_buf.release();
+        loaded = false;
+        pos = 0;
+    }
+};
+
+namespace {
+
+thread_local std::string g_create_err;
+
+template <class F> int guarded(qh_ctx* c, F f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception& e) {
+        if (c) c->err = e.what();
+        return 1;
+    }
+}
+
+void sync(qh_ctx* c) { HIP_OK(hipStreamSynchronize(c->s)); }
+
+// Uploads `rows` packed GGUF rows (src) into device rows at dst, repacking on
+// the device through a staging buffer.
+void upload_rows(qh_ctx* c, const uint8_t* src, uint8_t* dst, uint32_t kind, uint64_t cols,
+                 uint64_t rows) {
+    const size_t src_rb = gguf_row_bytes(kind, cols), dst_rb = dev_row_bytes(kind, cols);
+    const size_t stage = 256u << 20;
+    const uint64_t per = std::max<uint64_t>(1, stage / std::max<size_t>(src_rb, 1));
+    c->sa.reserve(std::min<uint64_t>(rows, per) * src_rb);
+    HIP_OK(hipMemsetAsync(dst, 0, rows * dst_rb, c->s));
+    for (uint64_t r = 0; r < rows; r += per) {
+        uint64_t n = std::min(per, rows - r);
+        HIP_OK(hipMemcpyAsync(c->sa.p, src + r * src_rb, n * src_rb, hipMemcpyHostToDevice, c->s));
+        uint64_t total = n * src_rb;
+        uint32_t grid = (uint32_t)std::min<uint64_t>((total + kBlock - 1) / kBlock, 65535);
+        hipLaunchKernelGGL(k_repack, dim3(grid), dim3(kBlock), 0, c->s, c->sa.as<const uint8_t>(),
+                           dst + r * dst_rb, kind, (uint32_t)cols, (size_t)n, src_rb, dst_rb);
+        HIP_OK(hipGetLastError());
+        HIP_OK(hipStreamSynchronize(c->s));  // staging buffer reused
+    }
+    c->stats.uploaded_bytes += rows * src_rb;
+}
+
+void launch_matvec(qh_ctx* c, const DevMat& m, const float* x, float* y, int R = 4) {
+    const uint32_t np = pad32h(m.cols);
+    const bool lds = np * 4 <= 65536;
+    const size_t smem = lds ? np * 4 : 0;
+    const uint32_t grid = blocks_for(groups_host(m.rows, m.cols, R));
+    switch (R) {
+    case 1: hipLaunchKernelGGL(k_matvec<1>, dim3(grid), dim3(kBlock), smem, c->s, m, x, y, (int)lds); break;
+    case 2: hipLaunchKernelGGL(k_matvec<2>, dim3(grid), dim3(kBlock), smem, c->s, m, x, y, (int)lds); break;
+    case 8: hipLaunchKernelGGL(k_matvec<8>, dim3(grid), dim3(kBlock), smem, c->s, m, x, y, (int)lds); break;
+    default: hipLaunchKernelGGL(k_matvec<4>, dim3(grid), dim3(kBlock), smem, c->s, m, x, y, (int)lds); break;
+    }
+    HIP_OK(hipGetLastError());
+}
+
+// Row-parallel R heuristic: enough waves to cover the GPU, more rows per wave
+// for tall matrices.
+int pick_r(uint64_t rows, uint64_t cols) {
+    for (int R : {8, 4, 2}) {
+        if (groups_host(rows, cols, R) >= 2048) return R;
+    }
+    return 1;
+}
+
+// Upload host vector x (n floats) zero-padded to pad32.
+const float* upload_x(qh_ctx* c, DevBuf& b, const float* x, size_t n) {
+    size_t np = pad32h(n);
+    b.reserve(np * 4);
+    HIP_OK(hipMemsetAsync(b.p, 0, np * 4, c->s));
+    if (n) HIP_OK(hipMemcpyAsync(b.p, x, n * 4, hipMemcpyHostToDevice, c->s));
+    c->stats.uploaded_bytes += n * 4;
+    return b.as<const float>();
+}
+
+// ---------------------------------------------------------------- model --
+void build_rope(qh_ctx* c) {
+    // (cos, sin) of angle = pos * theta^(-2i/d), computed as src/ops.rs:20-21
+    // does (f32 powf, sin_cos), for every position of the context.
+    const uint32_t d = c->dm.head_dim, half = d / 2;
+    std::vector<float> tab((size_t)c->context * half * 2);
+    std::vector<float> freq(half);
+    for (uint32_t i = 0; i < half; i++) {
+        volatile float e = -2.f * (float)i;
+        e = e / (float)d;
+        freq[i] = powf(c->cfg.theta, e);
+    }
+    for (size_t p = 0; p < c->context; p++)
+        for (uint32_t i = 0; i < half; i++) {
+            volatile float angle = (float)p * freq[i];
+            tab[(p * half + i) * 2] = cosf(angle);
+            tab[(p * half + i) * 2 + 1] = sinf(angle);
+        }
+    c->rope_buf.alloc(tab.size() * 4);
+    HIP_OK(hipMemcpy(c->rope_buf.p, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
+}
+
+void alloc_acts(qh_ctx* c) {
+    const ModelDims& d = c->dm;
+    const uint64_t hp = pad32h(d.hidden), qd = pad32h((uint64_t)d.heads * d.head_dim),
+                   kvd = pad32h((uint64_t)d.kvheads * d.head_dim), fp = pad32h(d.ff);
+    if (c->max_chunks * c->tc < c->context) throw Error("attention tile not chosen");
+    Acts& a = c->acts;
+    std::vector<std::pair<size_t, void**>> parts = {
+        {hp * 4, (void**)&a.x},
+        {hp * 4, (void**)&a.xn},
+        {qd * 4, (void**)&a.q},
+        {kvd * 4, (void**)&a.k},
+        {kvd * 4, (void**)&a.v},
+        {qd * 4, (void**)&a.attn},
+        {pad32h(d.experts) * 4, (void**)&a.logits_r},
+        {pad32h(d.top) * 4, (void**)&a.ids},
+        {pad32h(d.top) * 4, (void**)&a.wts},
+        {(uint64_t)d.top * fp * 4, (void**)&a.h},
+        {pad32h(d.vocab) * 4, (void**)&a.logits},
+        {(uint64_t)d.heads * c->max_chunks * (d.head_dim + 2) * 4, (void**)&a.part},
+        {pad32h(d.kvheads) * 4, (void**)&a.attn_cnt},
+        {kMaxGrid * 4, (void**)&a.fin_key},
+        {kMaxGrid * 4, (void**)&a.fin_idx},
+        {pad32h(c->context + 2) * 4, (void**)&a.tokens},
+        {256, (void**)&a.st},
+    };
+    size_t total = 0;
+    for (auto& p : parts) total += (p.first + 255) / 256 * 256;
+    c->acts_buf.alloc(total);
+    HIP_OK(hipMemset(c->acts_buf.p, 0, total));
+    size_t off = 0;
+    for (auto& p : parts) {
+        *p.second = c->acts_buf.as<uint8_t>() + off;
+        off += (p.first + 255) / 256 * 256;
+    }
+    const size_t kv_layer = (size_t)d.kvheads * c->context * d.head_dim;
+    c->kv.alloc(kv_layer * 2 * 4 * c->cfg.layers);
+    HIP_OK(hipMemset(c->kv.p, 0, c->kv.n));
+    build_rope(c);
+    a.rope = c->rope_buf.as<const float2>();
+}
+
+// Attention key tile: the largest power of two <= 64 whose LDS footprint
+// fits; fixes the chunk count (and partial buffer) of the model's context.
+void choose_attn_tile(qh_ctx* c) {
+    const ModelDims& d = c->dm;
+    const uint32_t G = d.heads / d.kvheads, hd = d.head_dim;
+    auto attn_lds = [&](uint32_t tc) { return (size_t)(G * hd + tc * (hd + 1) + tc * hd + G * tc + 2 * G) * 4; };
+    c->tc = 64;
+    while (c->tc > 1 && attn_lds(c->tc) > 60 * 1024) c->tc /= 2;
+    if (attn_lds(c->tc) > 64 * 1024) throw Error("attention shape exceeds the LDS budget");
+    c->lds_attn = attn_lds(c->tc);
+    c->max_chunks = (uint32_t)((c->context + c->tc - 1) / c->tc);
+}
+
+void choose_geometry(qh_ctx* c) {
+    const ModelDims& d = c->dm;
+    const LayerW& L = c->layers[0];
+    c->g_embed = (uint32_t)std::min<uint64_t>((d.hidden + kBlock - 1) / kBlock, 1024);
+    c->lds_h = (size_t)pad32h(d.hidden) * 4;
+    c->g_qkv = blocks_for(groups_host(L.q.rows, L.q.cols, 2) + groups_host(L.k.rows, L.k.cols, 2) +
+                          groups_host(L.v.rows, L.v.cols, 2));
+    c->g_qkn = d.heads + 2 * d.kvheads;
+    c->g_o = blocks_for(groups_host(L.o.rows, L.o.cols, 2));
+    c->lds_o = (size_t)pad32h((uint64_t)d.heads * d.head_dim) * 4;
+    c->g_router = blocks_for(groups_host(L.router.rows, L.router.cols, 1));
+    c->lds_router = c->lds_h + (size_t)d.top * 4;
+    {
+        int Lw = lanes_per_row(d.hidden), S = 64 / Lw;
+        uint64_t per = 2 * S;
+        c->g_gu = blocks_for((uint64_t)d.top * ((d.ff + per - 1) / per));
+    }
+    c->g_down = blocks_for((d.hidden + 1) / 2);
+    c->lds_down = ((size_t)d.top * pad32h(d.ff) + 2 * d.top) * 4;
+    c->g_final = blocks_for(groups_host(c->out.rows, c->out.cols, 4));
+    const size_t lds_cap = 64 * 1024;
+    if (c->lds_h > lds_cap || c->lds_o > lds_cap || c->lds_router > lds_cap)
+        throw Error("hidden size exceeds the LDS budget of the device kernels");
+    if (c->lds_down > lds_cap) throw Error("expert_used_count * expert FFN exceeds the LDS budget");
+}
+
+// Enqueues one layer's kernels.
+void enqueue_layer(qh_ctx* c, size_t l) {
+    const ModelDims& d = c->dm;
+    const LayerW& L = c->layers[l];
+    hipLaunchKernelGGL(k_rms_qkv<2>, dim3(c->g_qkv), dim3(kBlock), c->lds_h, c->s, L, c->acts, d);
+    hipLaunchKernelGGL(k_qk_norm_rope, dim3(c->g_qkn), dim3(kBlock), 0, c->s, L, c->acts, d);
+    hipLaunchKernelGGL(k_attention, dim3(d.kvheads, c->max_chunks), dim3(kBlock), c->lds_attn, c->s, c->attn[l], c->acts, d);
+    hipLaunchKernelGGL(k_oproj<2>, dim3(c->g_o), dim3(kBlock), c->lds_o, c->s, L, c->acts, d);
+    hipLaunchKernelGGL(k_router<1>, dim3(c->g_router), dim3(kBlock), c->lds_router, c->s, L, c->acts, d);
+    hipLaunchKernelGGL(k_gateup<2>, dim3(c->g_gu), dim3(kBlock), c->lds_h, c->s, L, c->acts, d);
+    hipLaunchKernelGGL(k_down<2>, dim3(c->g_down), dim3(kBlock), c->lds_down, c->s, L, c->acts, d);
+}
+
+void enqueue_step(qh_ctx* c) {
+    hipLaunchKernelGGL(k_embed, dim3(c->g_embed), dim3(kBlock), 0, c->s, c->emb, c->acts, c->dm);
+    for (size_t l = 0; l < c->layers.size(); l++) enqueue_layer(c, l);
+    hipLaunchKernelGGL(k_final<4>, dim3(c->g_final), dim3(kBlock), c->lds_h, c->s, c->out, c->onorm, c->acts, c->dm);
+}
+
+void capture_graph(qh_ctx* c) {
+    HIP_OK(hipStreamBeginCapture(c->s, hipStreamCaptureModeThreadLocal));
+    enqueue_step(c);
+    hipError_t e = hipStreamEndCapture(c->s, &c->graph);
+    if (e != hipSuccess) throw Error(std::string("graph capture: ") + hipGetErrorString(e));
+    HIP_OK(hipGraphInstantiate(&c->exec, c->graph, nullptr, nullptr, 0));
+}
+
+void load_image(qh_ctx* c, const uint8_t* data, size_t len, size_t context) {
+    Gguf g = parse_gguf(data, len);
+    Config cfg = config_from_gguf(g);
+    validate_tensors(cfg, g);
+    if (!(context > 0 && context <= cfg.max_context))
+        throw Error("context must be in 1..=" + std::to_string(cfg.max_context));
+    if (cfg.head_dim > 512) throw Error("head_dim above 512 is not supported by the device kernels");
+    if (cfg.top > 1024) throw Error("expert_used_count above 1024 is not supported");
+    c->drop_model();
+    c->cfg = cfg;
+    c->context = context;
+    c->packed = g.packed_bytes();
+    ModelDims& d = c->dm;
+    d.hidden = (uint32_t)cfg.hidden; d.heads = (uint32_t)cfg.heads; d.kvheads = (uint32_t)cfg.kvheads;
+    d.head_dim = (uint32_t)cfg.head_dim; d.experts = (uint32_t)cfg.experts; d.top = (uint32_t)cfg.top;
+    d.ff = (uint32_t)cfg.intermediate; d.vocab = (uint32_t)cfg.vocab; d.ctx = (uint32_t)context;
+    d.eps = cfg.eps;
+    // every tensor to HBM once, repacked into the device row layout
+    for (auto& kv : g.tensors) {
+        const Tensor& t = kv.second;
+        ModelTensor mt;
+        mt.kind = t.kind;
+        mt.dims = t.dims;
+        uint64_t cols = t.dims[0], rows = 1, experts = 0;
+        for (size_t k = 1; k < t.dims.size(); k++) rows *= t.dims[k];
+        if (t.dims.size() == 3) experts = t.dims[2];
+        const size_t drb = dev_row_bytes(t.kind, cols);
+        mt.buf.alloc(rows * drb + 64);
+        upload_rows(c, data + t.offset, mt.buf.as<uint8_t>(), t.kind, cols, rows);
+        if (t.dims.size() == 1) {
+            DevMat m = make_mat(mt.buf.as<uint8_t>(), t.kind, 1, cols, 0);
+            mt.f32.alloc(pad32h(cols) * 4);
+            HIP_OK(hipMemsetAsync(mt.f32.p, 0, pad32h(cols) * 4, c->s));
+            hipLaunchKernelGGL(k_dequant, dim3((uint32_t)std::min<uint64_t>((cols + 255) / 256, 1024)), dim3(kBlock), 0,
+                               c->s, m, (size_t)0, (size_t)1, mt.f32.as<float>());
+            HIP_OK(hipGetLastError());
+        } else {
+            mt.mat = make_mat(mt.buf.as<uint8_t>(), t.kind, t.dims[1], cols, experts);
+        }
+        c->tensors.emplace(kv.first, std::move(mt));
+    }
+    sync(c);
+    auto mat = [&](const std::string& n) { return c->tensors.at(n).mat; };
+    auto vec = [&](const std::string& n) { return c->tensors.at(n).f32.as<const float>(); };
+    c->emb = mat("token_embd.weight");
+    c->out = c->tensors.count("output.weight") ? mat("output.weight") : c->emb;
+    c->onorm = vec("output_norm.weight");
+    choose_attn_tile(c);
+    alloc_acts(c);
+    const size_t kv_layer = (size_t)d.kvheads * context * d.head_dim;
+    for (uint64_t i = 0; i < cfg.layers; i++) {
+        std::string p = "blk." + std::to_string(i) + ".";
+        LayerW L{};
+        L.q = mat(p + "attn_q.weight");
+        L.k = mat(p + "attn_k.weight");
+        L.v = mat(p + "attn_v.weight");
+        L.o = mat(p + "attn_output.weight");
+        L.router = mat(p + "ffn_gate_inp.weight");
+        L.gate = mat(p + "ffn_gate_exps.weight");
+        L.up = mat(p + "ffn_up_exps.weight");
+        L.down = mat(p + "ffn_down_exps.weight");
+        L.attn_norm = vec(p + "attn_norm.weight");
+        L.q_norm = vec(p + "attn_q_norm.weight");
+        L.k_norm = vec(p + "attn_k_norm.weight");
+        L.ffn_norm = vec(p + "ffn_norm.weight");
+        L.kcache = c->kv.as<float>() + (2 * i) * kv_layer;
+        L.vcache = c->kv.as<float>() + (2 * i + 1) * kv_layer;
+        c->layers.push_back(L);
+    }
+    choose_geometry(c);
+    for (uint64_t i = 0; i < cfg.layers; i++) {
+        AttnArgs a{};
+        a.q = c->acts.q;
+        a.k = c->layers[i].kcache;
+        a.v = c->layers[i].vcache;
+        a.sh = (size_t)context * d.head_dim;
+        a.st = d.head_dim;
+        a.heads = d.heads;
+        a.kvheads = d.kvheads;
+        a.d = d.head_dim;
+        a.tc = c->tc;
+        a.max_chunks = c->max_chunks;
+        a.part = c->acts.part;
+        a.counter = c->acts.attn_cnt;
+        a.out = c->acts.attn;
+        a.err = &c->acts.st->err;
+        c->attn.push_back(a);
+    }
+    capture_graph(c);
+    c->loaded = true;
+    c->pos = 0;
+}
+
+void need_model(qh_ctx* c) {
+    if (!c->loaded) throw Error("no model loaded");
+}
+
+// Writes the device step state from the host mirror.
+void put_state(qh_ctx* c, uint32_t pos, uint32_t n_given) {
+    DevState st{};
+    st.pos = pos;
+    st.n_given = n_given;
+    HIP_OK(hipMemcpyAsync(c->acts.st, &st, sizeof st, hipMemcpyHostToDevice, c->s));
+}
+
+DevState get_state(qh_ctx* c) {
+    DevState st{};
+    HIP_OK(hipMemcpyAsync(&st, c->acts.st, sizeof st, hipMemcpyDeviceToHost, c->s));
+    sync(c);
+    return st;
+}
+
+void reset_model(qh_ctx* c) {
+    c->pos = 0;
+    put_state(c, 0, 0);
+    sync(c);
+}
+
+[[noreturn]] void fail_step(qh_ctx* c, uint32_t err) {
+    reset_model(c);
+    if (err & kErrToken) throw Error("token outside vocabulary");
+    if (err & kErrRouter) throw Error("invalid MoE router");
+    if (err & kErrLogits) throw Error("nonfinite model output");
+    if (err & kErrContext) throw Error("context limit " + std::to_string(c->context) + " reached");
+    throw Error("device step failed");
+}
+
+uint64_t matvecs_per_token(const qh_ctx* c) { return c->cfg.layers * (5 + 3 * c->cfg.top) + 1; }
+
+double now_ms() {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+}  // namespace
+
+// ===================================================================== C ABI ==
+extern "C" {
+
+int qh_create(int device, qh_ctx** out) {
+    try {
+        int n = 0;
+        HIP_OK(hipGetDeviceCount(&n));
+        if (device < 0 || device >= n) throw Error("HIP device " + std::to_string(device) + " not present");
+        hipDeviceProp_t p;
+        HIP_OK(hipGetDeviceProperties(&p, device));
+        if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
+            throw Error(std::string("device is ") + p.gcnArchName + ", this engine is built for gfx950");
+        HIP_OK(hipSetDevice(device));
+        auto c = std::make_unique<qh_ctx>();
+        c->device = device;
+        HIP_OK(hipStreamCreateWithFlags(&c->s, hipStreamNonBlocking));
+        *out = c.release();
+        return 0;
+    } catch (const std::exception& e) {
+        g_create_err = e.what();
+        return 1;
+    }
+}
+
+void qh_destroy(qh_ctx* c) { delete c; }
+
+const char* qh_last_error(const qh_ctx* c) { return c ? c->err.c_str() : g_create_err.c_str(); }
+
+int qh_load_model(qh_ctx* c, const void* image, size_t len, size_t context) {
+    return guarded(c, [&] {
+        HIP_OK(hipSetDevice(c->device));
+        load_image(c, static_cast<const uint8_t*>(image), len, context);
+    });
+}
+
+int qh_load_model_file(qh_ctx* c, const char* path, size_t context) {
+    return guarded(c, [&] {
+        int fd = open(path, O_RDONLY);
+        if (fd < 0) throw Error(std::string("open ") + path);
+        struct stat sb;
+        if (fstat(fd, &sb) != 0) { close(fd); throw Error(std::string("stat ") + path); }
+        size_t len = (size_t)sb.st_size;
+        void* m = len ? mmap(nullptr, len, PROT_READ, MAP_PRIVATE, fd, 0) : nullptr;
+        close(fd);
+        if (len && m == MAP_FAILED) throw Error(std::string("mmap ") + path);
+        try {
+            HIP_OK(hipSetDevice(c->device));
+            load_image(c, static_cast<const uint8_t*>(m), len, context);
+        } catch (...) {
+            if (len) munmap(m, len);
+            throw;
+        }
+        if (len) munmap(m, len);
+    });
+}
+
+int qh_model_config(const qh_ctx* c, qh_config_t* out) {
+    return guarded(const_cast<qh_ctx*>(c), [&] {
+        need_model(const_cast<qh_ctx*>(c));
+        const Config& g = c->cfg;
+        *out = {g.hidden, g.layers, g.heads, g.kvheads, g.head_dim, g.experts, g.top, g.intermediate,
+                g.vocab, g.max_context, g.eps, g.theta};
+    });
+}
+
+int qh_tensor_info(const qh_ctx* c, const char* name, uint32_t* kind, size_t* rank, uint64_t dims[3]) {
+    return guarded(const_cast<qh_ctx*>(c), [&] {
+        need_model(const_cast<qh_ctx*>(c));
+        auto it = c->tensors.find(name);
+        if (it == c->tensors.end()) throw Error(std::string("missing tensor ") + name);
+        *kind = it->second.kind;
+        *rank = it->second.dims.size();
+        for (size_t k = 0; k < 3; k++) dims[k] = k < it->second.dims.size() ? it->second.dims[k] : 0;
+    });
+}
+
+int qh_packed_weight_bytes(const qh_ctx* c, uint64_t* out) {
+    return guarded(const_cast<qh_ctx*>(c), [&] {
+        need_model(const_cast<qh_ctx*>(c));
+        *out = c->packed;
+    });
+}
+
+int qh_matvec(qh_ctx* c, const char* name, int64_t expert, const float* x, size_t cols, float* y,
+              size_t rows) {
+    return guarded(c, [&] {
+        double t0 = now_ms();
+        need_model(c);
+        auto it = c->tensors.find(name);
+        if (it == c->tensors.end()) throw Error(std::string("missing tensor ") + name);
+        const ModelTensor& t = it->second;
+        if (t.dims.size() != (expert >= 0 ? 3u : 2u)) throw Error(std::string("matrix rank mismatch: ") + name);
+        if (expert >= 0 && (uint64_t)expert >= t.dims[2]) throw Error("expert out of bounds");
+        if (cols != t.dims[0]) throw Error(std::string("matvec shape mismatch ") + name);
+        if (rows < t.dims[1]) throw Error("output buffer too small");
+        DevMat m = t.mat;
+        if (expert >= 0) m.w += (size_t)expert * m.expert_stride;
+        const float* xd = upload_x(c, c->sb, x, cols);
+        c->sc.reserve((size_t)m.rows * 4);
+        launch_matvec(c, m, xd, c->sc.as<float>(), pick_r(m.rows, m.cols));
+        HIP_OK(hipMemcpyAsync(y, c->sc.p, (size_t)m.rows * 4, hipMemcpyDeviceToHost, c->s));
+        sync(c);
+        c->stats.matvecs += 1;
+        c->stats.matvec_ms += now_ms() - t0;
+    });
+}
+
+int qh_stats(const qh_ctx* c, qh_stats_t* out) {
+    *out = c->stats;
+    return 0;
+}
+
+int qh_packed_matvec(qh_ctx* c, const void* data, size_t len, uint32_t kind, size_t rows, size_t cols,
+                     const float* x, float* y) {
+    return guarded(c, [&] {
+        double t0 = now_ms();
+        size_t rb = row_bytes_checked(kind, cols);
+        if (!(rows > 0 && rows * rb == len)) throw Error("GPU matvec shape mismatch");
+        if (rows > 0xffffffffull) throw Error("matrix too tall");
+        const size_t drb = dev_row_bytes(kind, cols);
+        c->sd.reserve(rows * drb + 64);
+        upload_rows(c, static_cast<const uint8_t*>(data), c->sd.as<uint8_t>(), kind, cols, rows);
+        DevMat m = make_mat(c->sd.as<uint8_t>(), kind, rows, cols, 0);
+        const float* xd = upload_x(c, c->sb, x, cols);
+        c->sc.reserve(rows * 4);
+        launch_matvec(c, m, xd, c->sc.as<float>(), pick_r(rows, cols));
+        HIP_OK(hipMemcpyAsync(y, c->sc.p, rows * 4, hipMemcpyDeviceToHost, c->s));
+        sync(c);
+        c->stats.matvecs += 1;
+        c->stats.matvec_ms += now_ms() - t0;
+    });
+}
+
+int qh_dequant(qh_ctx* c, const void* data, size_t len, uint32_t kind, size_t rows, size_t cols, float* out) {
+    return guarded(c, [&] {
+        size_t rb = row_bytes_checked(kind, cols);
+        if (len < rows * rb) throw Error("truncated quantized row");
+        if (rows == 0) return;
+        const size_t drb = dev_row_bytes(kind, cols);
+        c->sd.reserve(rows * drb + 64);
+        upload_rows(c, static_cast<const uint8_t*>(data), c->sd.as<uint8_t>(), kind, cols, rows);
+        DevMat m = make_mat(c->sd.as<uint8_t>(), kind, rows, cols, 0);
+        c->sc.reserve(rows * cols * 4);
+        uint32_t grid = (uint32_t)std::min<uint64_t>((rows * cols + kBlock - 1) / kBlock, 65535);
+        hipLaunchKernelGGL(k_dequant, dim3(grid), dim3(kBlock), 0, c->s, m, (size_t)0, rows, c->sc.as<float>());
+        HIP_OK(hipGetLastError());
+        HIP_OK(hipMemcpyAsync(out, c->sc.p, rows * cols * 4, hipMemcpyDeviceToHost, c->s));
+        sync(c);
+    });
+}
+
+int qh_route(qh_ctx* c, const float* logits, size_t n, size_t top, uint32_t* ids, float* w) {
+    return guarded(c, [&] {
+        if (top == 0 || top > n) throw Error("invalid MoE router");
+        if (n > 0xffffffffull) throw Error("invalid MoE router");
+        const float* ld = upload_x(c, c->sb, logits, n);
+        c->sc.reserve(pad32h(top) * 8 + 256);
+        uint32_t* dids = c->sc.as<uint32_t>();
+        float* dw = reinterpret_cast<float*>(dids + pad32h(top));
+        uint32_t* derr = reinterpret_cast<uint32_t*>(dw + pad32h(top));
+        HIP_OK(hipMemsetAsync(derr, 0, 4, c->s));
+        hipLaunchKernelGGL(k_route, dim3(1), dim3(kBlock), top * 4, c->s, ld, (uint32_t)n, (uint32_t)top, dids, dw, derr);
+        HIP_OK(hipGetLastError());
+        uint32_t e = 0;
+        HIP_OK(hipMemcpyAsync(&e, derr, 4, hipMemcpyDeviceToHost, c->s));
+        sync(c);
+        if (e) throw Error("invalid MoE router");
+        HIP_OK(hipMemcpyAsync(ids, dids, top * 4, hipMemcpyDeviceToHost, c->s));
+        HIP_OK(hipMemcpyAsync(w, dw, top * 4, hipMemcpyDeviceToHost, c->s));
+        sync(c);
+    });
+}
+
+int qh_argmax(qh_ctx* c, const float* logits, size_t n, uint32_t* out) {
+    return guarded(c, [&] {
+        if (n == 0 || n > 0xffffffffull) throw Error("invalid logits");
+        const float* ld = upload_x(c, c->sb, logits, n);
+        uint32_t grid = (uint32_t)std::min<uint64_t>((n + kBlock * 8 - 1) / (kBlock * 8), 1024);
+        c->sc.reserve((2 * 1024 + 64) * 4);
+        int32_t* pk = c->sc.as<int32_t>();
+        uint32_t* pi = reinterpret_cast<uint32_t*>(pk + 1024);
+        uint32_t* misc = pi + 1024;  // [0] counter, [1] out, [2] err
+        HIP_OK(hipMemsetAsync(misc, 0, 16, c->s));
+        hipLaunchKernelGGL(k_argmax, dim3(grid), dim3(kBlock), 0, c->s, ld, (uint32_t)n, pk, pi, misc, misc + 1, misc + 2);
+        HIP_OK(hipGetLastError());
+        uint32_t h[3];
+        HIP_OK(hipMemcpyAsync(h, misc, 12, hipMemcpyDeviceToHost, c->s));
+        sync(c);
+        if (h[2]) throw Error("invalid logits");
+        *out = h[1];
+    });
+}
+
+int qh_attention(qh_ctx* c, const float* q, const float* k, const float* v, size_t klen, size_t heads,
+                 size_t kvheads, size_t d, float* out) {
+    return guarded(c, [&] {
+        if (!(kvheads > 0 && heads > 0 && d > 0 && heads % kvheads == 0 && klen % (kvheads * d) == 0))
+            throw Error("attention shape mismatch");
+        const size_t T = klen / (kvheads * d);
+        if (T == 0) throw Error("empty KV cache");
+        const uint32_t G = (uint32_t)(heads / kvheads);
+        auto lds = [&](uint32_t tc) { return (size_t)(G * d + tc * (d + 1) + tc * d + G * tc + 2 * G) * 4; };
+        uint32_t tc = 64;
+        while (tc > 1 && lds(tc) > 60 * 1024) tc /= 2;
+        if (lds(tc) > 64 * 1024) throw Error("attention shape exceeds the LDS budget");
+        const uint32_t nch = (uint32_t)((T + tc - 1) / tc);
+        const float* qd = upload_x(c, c->sa, q, heads * d);
+        c->sb.reserve(klen * 8 + 256);
+        HIP_OK(hipMemcpyAsync(c->sb.p, k, klen * 4, hipMemcpyHostToDevice, c->s));
+        HIP_OK(hipMemcpyAsync(c->sb.as<float>() + klen, v, klen * 4, hipMemcpyHostToDevice, c->s));
+        c->stats.uploaded_bytes += klen * 8;
+        const size_t part = heads * nch * (d + 2);
+        c->sc.reserve((part + heads * d + kvheads + 64) * 4);
+        float* dpart = c->sc.as<float>();
+        float* dout = dpart + part;
+        uint32_t* cnt = reinterpret_cast<uint32_t*>(dout + heads * d);
+        HIP_OK(hipMemsetAsync(cnt, 0, kvheads * 4, c->s));
+        AttnArgs a{};
+        a.q = qd;
+        a.k = c->sb.as<float>();
+        a.v = c->sb.as<float>() + klen;
+        a.sh = d;
+        a.st = kvheads * d;
+        a.heads = (uint32_t)heads;
+        a.kvheads = (uint32_t)kvheads;
+        a.d = (uint32_t)d;
+        a.tc = tc;
+        a.max_chunks = nch;
+        a.part = dpart;
+        a.counter = cnt;
+        a.out = dout;
+        a.err = nullptr;
+        hipLaunchKernelGGL(k_attention_api, dim3((uint32_t)kvheads, nch), dim3(kBlock), lds(tc), c->s, a, (uint32_t)T);
+        HIP_OK(hipGetLastError());
+        HIP_OK(hipMemcpyAsync(out, dout, heads * d * 4, hipMemcpyDeviceToHost, c->s));
+        sync(c);
+    });
+}
+
+int qh_forward(qh_ctx* c, uint32_t token, float* logits, uint32_t* argmax) {
+    return guarded(c, [&] {
+        double t0 = now_ms();
+        need_model(c);
+        if (!(c->pos < c->context)) {
+            reset_model(c);
+            throw Error("context limit " + std::to_string(c->context) + " reached");
+        }
+        if (!(token < c->cfg.vocab)) {
+            reset_model(c);
+            throw Error("token outside vocabulary");
+        }
+        HIP_OK(hipMemcpyAsync(c->acts.tokens + c->pos, &token, 4, hipMemcpyHostToDevice, c->s));
+        put_state(c, (uint32_t)c->pos, (uint32_t)c->pos + 1);
+        HIP_OK(hipGraphLaunch(c->exec, c->s));
+        if (logits)
+            HIP_OK(hipMemcpyAsync(logits, c->acts.logits, c->cfg.vocab * 4, hipMemcpyDeviceToHost, c->s));
+        DevState st = get_state(c);
+        if (st.err) fail_step(c, st.err);
+        c->pos += 1;
+        if (argmax) *argmax = st.argmax;
+        c->stats.matvecs += matvecs_per_token(c);
+        c->stats.matvec_ms += now_ms() - t0;
+    });
+}
+
+int qh_generate(qh_ctx* c, const uint32_t* prompt, size_t n_prompt, size_t n_new, uint32_t* out_tokens,
+                float* logits_last) {
+    return guarded(c, [&] {
+        double t0 = now_ms();
+        need_model(c);
+        if (n_prompt == 0) throw Error("empty prompt");
+        const size_t steps = n_prompt + (n_new ? n_new - 1 : 0);
+        if (c->pos + steps > c->context) throw Error("prompt + max-tokens exceed --ctx");
+        for (size_t i = 0; i < n_prompt; i++)
+            if (prompt[i] >= c->cfg.vocab) throw Error("token outside vocabulary");
+        HIP_OK(hipMemcpyAsync(c->acts.tokens + c->pos, prompt, n_prompt * 4, hipMemcpyHostToDevice, c->s));
+        put_state(c, (uint32_t)c->pos, (uint32_t)(c->pos + n_prompt));
+        for (size_t i = 0; i < steps; i++) HIP_OK(hipGraphLaunch(c->exec, c->s));
+        DevState st = get_state(c);
+        if (st.err) fail_step(c, st.err);
+        if (n_new)
+            HIP_OK(hipMemcpyAsync(out_tokens, c->acts.tokens + c->pos + n_prompt, n_new * 4, hipMemcpyDeviceToHost, c->s));
+        if (logits_last)
+            HIP_OK(hipMemcpyAsync(logits_last, c->acts.logits, c->cfg.vocab * 4, hipMemcpyDeviceToHost, c->s));
+        sync(c);
+        c->pos += steps;
+        c->stats.matvecs += matvecs_per_token(c) * steps;
+        c->stats.matvec_ms += now_ms() - t0;
+    });
+}
+
+int qh_reset(qh_ctx* c) {
+    return guarded(c, [&] {
+        need_model(c);
+        reset_model(c);
+    });
+}
+
+int qh_position(const qh_ctx* c, size_t* out) {
+    *out = c->pos;
+    return 0;
+}
+
+int qh_layer_forward(qh_ctx* c, size_t layer, float* x, size_t pos, const float* kprev, const float* vprev,
+                     uint32_t* ids, float* w) {
+    return guarded(c, [&] {
+        need_model(c);
+        if (layer >= c->layers.size()) throw Error("layer out of range");
+        if (pos >= c->context) throw Error("context limit " + std::to_string(c->context) + " reached");
+        const ModelDims& d = c->dm;
+        const LayerW& L = c->layers[layer];
+        HIP_OK(hipMemcpyAsync(c->acts.x, x, d.hidden * 4, hipMemcpyHostToDevice, c->s));
+        if (pos) {
+            // time-major host history -> head-major device cache
+            const size_t kvd = (size_t)d.kvheads * d.head_dim;
+            std::vector<float> hk(pos * kvd), hv(pos * kvd);
+            for (size_t t = 0; t < pos; t++)
+                for (uint32_t h = 0; h < d.kvheads; h++) {
+                    std::memcpy(&hk[(h * pos + t) * d.head_dim], kprev + t * kvd + h * d.head_dim, d.head_dim * 4);
+                    std::memcpy(&hv[(h * pos + t) * d.head_dim], vprev + t * kvd + h * d.head_dim, d.head_dim * 4);
+                }
+            for (uint32_t h = 0; h < d.kvheads; h++) {
+                HIP_OK(hipMemcpyAsync(L.kcache + (size_t)h * c->context * d.head_dim, &hk[h * pos * d.head_dim],
+                                      pos * d.head_dim * 4, hipMemcpyHostToDevice, c->s));
+                HIP_OK(hipMemcpyAsync(L.vcache + (size_t)h * c->context * d.head_dim, &hv[h * pos * d.head_dim],
+                                      pos * d.head_dim * 4, hipMemcpyHostToDevice, c->s));
+            }
+            c->stats.uploaded_bytes += 2 * pos * kvd * 4;
+            sync(c);  // host staging vectors go out of scope
+        }
+        put_state(c, (uint32_t)pos, (uint32_t)pos + 1);
+        enqueue_layer(c, layer);
+        HIP_OK(hipGetLastError());
+        HIP_OK(hipMemcpyAsync(x, c->acts.x, d.hidden * 4, hipMemcpyDeviceToHost, c->s));
+        if (ids) HIP_OK(hipMemcpyAsync(ids, c->acts.ids, d.top * 4, hipMemcpyDeviceToHost, c->s));
+        if (w) HIP_OK(hipMemcpyAsync(w, c->acts.wts, d.top * 4, hipMemcpyDeviceToHost, c->s));
+        DevState st = get_state(c);
+        reset_model(c);
+        if (st.err) fail_step(c, st.err);
+    });
+}
+
+int qh_bench_decode(qh_ctx* c, size_t warmup, size_t steps, double* ms_total) {
+    return guarded(c, [&] {
+        need_model(c);
+        if (c->pos == 0) throw Error("bench_decode continues a sequence: run a prompt first");
+        if (c->pos + warmup + steps > c->context) throw Error("prompt + max-tokens exceed --ctx");
+        put_state(c, (uint32_t)c->pos, (uint32_t)c->pos);
+        for (size_t i = 0; i < warmup; i++) HIP_OK(hipGraphLaunch(c->exec, c->s));
+        hipEvent_t e0, e1;
+        HIP_OK(hipEventCreate(&e0));
+        HIP_OK(hipEventCreate(&e1));
+        HIP_OK(hipEventRecord(e0, c->s));
+        for (size_t i = 0; i < steps; i++) HIP_OK(hipGraphLaunch(c->exec, c->s));
+        HIP_OK(hipEventRecord(e1, c->s));
+        HIP_OK(hipEventSynchronize(e1));
+        float ms = 0;
+        HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        DevState st = get_state(c);
+        if (st.err) fail_step(c, st.err);
+        c->pos += warmup + steps;
+        c->stats.matvecs += matvecs_per_token(c) * (warmup + steps);
+        *ms_total = ms;
+    });
+}
+
+int qh_profile_step(qh_ctx* c, size_t steps, double* ms_by_class, size_t nclass) {
+    return guarded(c, [&] {
+        need_model(c);
+        if (nclass < QH_NUM_KERNEL_CLASSES) throw Error("ms_by_class needs QH_NUM_KERNEL_CLASSES entries");
+        if (c->pos == 0) throw Error("profile_step continues a sequence: run a prompt first");
+        if (c->pos + steps > c->context) throw Error("prompt + max-tokens exceed --ctx");
+        const size_t L = c->layers.size();
+        std::vector<hipEvent_t> ev(2 + 7 * L + 1);
+        for (auto& e : ev) HIP_OK(hipEventCreate(&e));
+        std::vector<double> acc(QH_NUM_KERNEL_CLASSES, 0.0);
+        put_state(c, (uint32_t)c->pos, (uint32_t)c->pos);
+        const ModelDims& d = c->dm;
+        for (size_t s = 0; s < steps; s++) {
+            size_t k = 0;
+            HIP_OK(hipEventRecord(ev[k++], c->s));
+            hipLaunchKernelGGL(k_embed, dim3(c->g_embed), dim3(kBlock), 0, c->s, c->emb, c->acts, d);
+            HIP_OK(hipEventRecord(ev[k++], c->s));
+            for (size_t l = 0; l < L; l++) {
+                const LayerW& W = c->layers[l];
+                hipLaunchKernelGGL(k_rms_qkv<2>, dim3(c->g_qkv), dim3(kBlock), c->lds_h, c->s, W, c->acts, d);
+                HIP_OK(hipEventRecord(ev[k++], c->s));
+                hipLaunchKernelGGL(k_qk_norm_rope, dim3(c->g_qkn), dim3(kBlock), 0, c->s, W, c->acts, d);
+                HIP_OK(hipEventRecord(ev[k++], c->s));
+                hipLaunchKernelGGL(k_attention, dim3(d.kvheads, c->max_chunks), dim3(kBlock), c->lds_attn, c->s, c->attn[l], c->acts, d);
+                HIP_OK(hipEventRecord(ev[k++], c->s));
+                hipLaunchKernelGGL(k_oproj<2>, dim3(c->g_o), dim3(kBlock), c->lds_o, c->s, W, c->acts, d);
+                HIP_OK(hipEventRecord(ev[k++], c->s));
+                hipLaunchKernelGGL(k_router<1>, dim3(c->g_router), dim3(kBlock), c->lds_router, c->s, W, c->acts, d);
+                HIP_OK(hipEventRecord(ev[k++], c->s));
+                hipLaunchKernelGGL(k_gateup<2>, dim3(c->g_gu), dim3(kBlock), c->lds_h, c->s, W, c->acts, d);
+                HIP_OK(hipEventRecord(ev[k++], c->s));
+                hipLaunchKernelGGL(k_down<2>, dim3(c->g_down), dim3(kBlock), c->lds_down, c->s, W, c->acts, d);
+                HIP_OK(hipEventRecord(ev[k++], c->s));
+            }
+            hipLaunchKernelGGL(k_final<4>, dim3(c->g_final), dim3(kBlock), c->lds_h, c->s, c->out, c->onorm, c->acts, d);
+            HIP_OK(hipEventRecord(ev[k++], c->s));
+            HIP_OK(hipGetLastError());
+            HIP_OK(hipEventSynchronize(ev[k - 1]));
+            auto el = [&](size_t a) {
+                float ms = 0;
+                HIP_OK(hipEventElapsedTime(&ms, ev[a], ev[a + 1]));
+                return (double)ms;
+            };
+            acc[0] += el(0);
+            for (size_t l = 0; l < L; l++)
+                for (size_t j = 0; j < 7; j++) acc[1 + j] += el(1 + 7 * l + j);
+            acc[8] += el(1 + 7 * L);
+        }
+        for (auto& e : ev) (void)hipEventDestroy(e);
+        DevState st = get_state(c);
+        if (st.err) fail_step(c, st.err);
+        c->pos += steps;
+        for (size_t j = 0; j < QH_NUM_KERNEL_CLASSES; j++) ms_by_class[j] = acc[j] / (double)steps;
+    });
+}
+
+int qh_bench_matvec(qh_ctx* c, const void* data, size_t len, uint32_t kind, size_t rows, size_t cols,
+                    size_t copies, size_t iters, double* ms_per_launch) {
+    return guarded(c, [&] {
+        size_t rb = row_bytes_checked(kind, cols);
+        if (!(rows > 0 && rows * rb == len)) throw Error("GPU matvec shape mismatch");
+        if (copies == 0 || iters == 0) throw Error("copies and iters must be positive");
+        const size_t drb = dev_row_bytes(kind, cols), one = rows * drb;
+        DevBuf w;
+        w.alloc(one * copies + 64);
+        upload_rows(c, static_cast<const uint8_t*>(data), w.as<uint8_t>(), kind, cols, rows);
+        for (size_t i = 1; i < copies; i++)
+            HIP_OK(hipMemcpyAsync(w.as<uint8_t>() + i * one, w.p, one, hipMemcpyDeviceToDevice, c->s));
+        DevBuf xb, yb;
+        xb.alloc(pad32h(cols) * 4);
+        HIP_OK(hipMemsetAsync(xb.p, 0, pad32h(cols) * 4, c->s));
+        yb.alloc(rows * 4);
+        const int R = pick_r(rows, cols);
+        for (size_t i = 0; i < std::min<size_t>(copies, 8); i++)
+            launch_matvec(c, make_mat(w.as<uint8_t>() + i * one, kind, rows, cols, 0), xb.as<float>(), yb.as<float>(), R);
+        hipEvent_t e0, e1;
+        HIP_OK(hipEventCreate(&e0));
+        HIP_OK(hipEventCreate(&e1));
+        HIP_OK(hipEventRecord(e0, c->s));
+        for (size_t i = 0; i < iters; i++)
+            launch_matvec(c, make_mat(w.as<uint8_t>() + (i % copies) * one, kind, rows, cols, 0), xb.as<float>(),
+                          yb.as<float>(), R);
+        HIP_OK(hipEventRecord(e1, c->s));
+        HIP_OK(hipEventSynchronize(e1));
+        float ms = 0;
+        HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        *ms_per_launch = ms / (double)iters;
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,90 @@
+// Kernel argument blocks and launch helpers shared by kernels.hip and the
+// engine.  Every kernel here is hand-written for gfx950 (wave64, 256-thread
+// workgroups = 4 waves).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "qh_format.hpp"
+
+namespace qh {
+
+constexpr int kBlock = 256;  // threads per workgroup (4 wavefronts)
+constexpr int kWaves = kBlock / 64;
+
+// One packed matrix (or a stack of expert matrices) resident in HBM.
+struct DevMat {
+    const uint8_t* w;   // device row layout
+    uint32_t kind;
+    uint32_t rows, cols;
+    uint32_t drb;       // device row stride (bytes)
+    RowGeo geo;
+    size_t expert_stride;  // bytes between experts (rows * drb); 0 for 2-D
+};
+
+// Device-resident step state of one sequence.
+struct DevState {
+    uint32_t pos;      // position of the token being processed
+    uint32_t n_given;  // tokens[0, n_given) come from the caller; later ones from argmax
+    uint32_t err;      // error bits (kErr*)
+    uint32_t argmax;   // greedy id of the last completed step
+    uint32_t cnt_router, cnt_final, pad0, pad1;
+};
+
+enum : uint32_t {
+    kErrRouter = 1u,   // non-finite router logits (src/ops.rs:46-49)
+    kErrLogits = 2u,   // non-finite output logits (src/model.rs:296-299)
+    kErrToken = 4u,    // token outside vocabulary (src/model.rs:222)
+    kErrContext = 8u,  // position beyond the allocated context
+};
+
+struct LayerW {
+    DevMat q, k, v, o, router, gate, up, down;
+    const float* attn_norm;
+    const float* q_norm;
+    const float* k_norm;
+    const float* ffn_norm;
+    float* kcache;  // [kvheads][ctx][d]
+    float* vcache;
+};
+
+struct ModelDims {
+    uint32_t hidden, heads, kvheads, head_dim, experts, top, ff, vocab, ctx;
+    float eps;
+};
+
+// Scratch activations of one step.
+struct Acts {
+    float* x;        // [H] residual stream
+    float* xn;       // [H] normalised input of the expert FFN
+    float* q;        // [heads*d]
+    float* k;        // [kvheads*d]
+    float* v;        // [kvheads*d]
+    float* attn;     // [heads*d]
+    float* logits_r; // [experts]
+    uint32_t* ids;   // [top]
+    float* wts;      // [top]
+    float* h;        // [top*ff]
+    float* logits;   // [vocab]
+    float* part;     // attention partials [heads][max_chunks][d+2]
+    uint32_t* attn_cnt;   // [kvheads] last-block counters
+    uint32_t* fin_key;    // [max final blocks] argmax partial keys
+    uint32_t* fin_idx;    // [max final blocks]
+    uint32_t* tokens;     // [ctx+1]
+    const float2* rope;   // [ctx][d/2] (cos, sin)
+    DevState* st;
+};
+
+// Arguments of the split-T attention kernels (see kernels.hip).
+struct AttnArgs {
+    const float* q;
+    const float* k;
+    const float* v;
+    size_t sh, st;      // element (t, g, j) at k[g*sh + t*st + j]
+    uint32_t heads, kvheads, d, tc, max_chunks;
+    float* part;        // [heads][max_chunks][d+2]
+    uint32_t* counter;  // [kvheads]
+    float* out;         // [heads*d]
+    uint32_t* err;      // nullable: error bits (kErrContext on a chunk overflow)
+};
+
+}  // namespace qh
