@@ -37,20 +37,18 @@ def tensor_bytes(model, name, rows_slice=None):
 
 
 def algorithmic_bytes(model, pos_avg):
-    """Bytes each kernel class must move per decode token (weights read once,
-    activation vectors in/out, KV history of the average position)."""
+    """Bytes each kernel class must move per decode token: weights read once,
+    activation vectors in/out, and the KV history at the average position."""
     c = model.config
-    H, L, top, ff = c["hidden"], c["layers"], c["top"], c["intermediate"]
+    H, L, top, ff, E = c["hidden"], c["layers"], c["top"], c["intermediate"], c["experts"]
     qd, kvd = c["heads"] * c["head_dim"], c["kvheads"] * c["head_dim"]
     b = dict.fromkeys(model.KERNEL_CLASSES, 0.0)
-    b["embed"] = tensor_bytes(model, "token_embd.weight", 1) + 4 * H
+    b["qkv"] = tensor_bytes(model, "token_embd.weight", 1)
     for i in range(L):
         p = f"blk.{i}."
-        b["rms_qkv"] += sum(tensor_bytes(model, p + n) for n in ("attn_q.weight", "attn_k.weight", "attn_v.weight")) + 4 * H + 4 * (qd + 2 * kvd)
-        b["qk_norm_rope"] += 4 * 2 * (qd + 2 * kvd)
-        b["attention"] += 2 * 4 * kvd * (pos_avg + 1) + 8 * qd
-        b["oproj"] += tensor_bytes(model, p + "attn_output.weight") + 4 * qd + 8 * H
-        b["router"] += tensor_bytes(model, p + "ffn_gate_inp.weight") + 8 * H + 4 * c["experts"]
+        b["qkv"] += sum(tensor_bytes(model, p + n) for n in ("attn_q.weight", "attn_k.weight", "attn_v.weight")) + 4 * H + 4 * (qd + 2 * kvd)
+        b["attention"] += 2 * 4 * kvd * (pos_avg + 1) + 4 * (qd + 2 * kvd) + 4 * qd
+        b["oproj"] += tensor_bytes(model, p + "attn_output.weight") + tensor_bytes(model, p + "ffn_gate_inp.weight") + 4 * qd + 8 * H
         b["gateup"] += top * (tensor_bytes(model, p + "ffn_gate_exps.weight", ff) +
                               tensor_bytes(model, p + "ffn_up_exps.weight", ff)) + 4 * H + 4 * top * ff
         b["down"] += top * tensor_bytes(model, p + "ffn_down_exps.weight", H) + 4 * top * ff + 8 * H
@@ -59,7 +57,7 @@ def algorithmic_bytes(model, pos_avg):
         model.tensor(out)
     except Exception:
         out = "token_embd.weight"
-    b["final"] = tensor_bytes(model, out) + 4 * H + 4 * c["vocab"]
+    b["vocab"] = tensor_bytes(model, out) + 4 * H + 4 * c["vocab"]
     return b
 
 
@@ -165,13 +163,13 @@ def main():
         gbs = bytes_cls[k] / (v * 1e-3) / 1e9 if v > 0 else 0.0
         classes[k] = {"ms_per_token": round(v, 4), "bytes_per_token": int(bytes_cls[k]), "GB_s": round(gbs, 1)}
     dom = max(breakdown, key=breakdown.get)
-    launches = 1 if dom in ("embed", "final") else args.layers
+    launches = 1 if dom in ("vocab", "finish") else args.layers
     per_launch_bytes = bytes_cls[dom] / launches
     per_launch_ms = breakdown[dom] / launches
     achieved = per_launch_bytes / (per_launch_ms * 1e-3) / 1e9
     log(f"dominant kernel class {dom}: {per_launch_ms*1e3:.1f} us/launch, {achieved:.0f} GB/s")
 
-    w_active = sum(bytes_cls[k] for k in ("embed", "rms_qkv", "oproj", "router", "gateup", "down", "final"))
+    w_active = sum(bytes_cls[k] for k in ("qkv", "oproj", "gateup", "down", "vocab"))
     matvec = [] if args.no_matvec else matvec_cases(engine, synth, dev)
     cpu = None if args.no_cpu else cpu_baseline(img, spec, threads)
 

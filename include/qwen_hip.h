@@ -139,9 +139,12 @@ int qh_bench_decode(qh_ctx *ctx, size_t warmup, size_t steps, double *ms_total);
  * time with HIP events between kernels on the context's stream (continuing
  * from the current position).  ms_by_class[QH_NUM_KERNEL_CLASSES] receives
  * the mean GPU milliseconds per token of each class, in this order:
- * embed, rms_qkv, qk_norm_rope, attention, oproj, router, gateup, down,
- * final (norm + vocab + argmax). */
-#define QH_NUM_KERNEL_CLASSES 9
+ * qkv (norm + q/k/v projections), attention (Q/K norm, RoPE, KV append,
+ * attention), oproj (output projection, residual, router partials), gateup
+ * (router top-k, gate/up projections, SwiGLU), down (down projections,
+ * combine, residual), vocab (final norm, vocab projection), finish
+ * (argmax, next token). */
+#define QH_NUM_KERNEL_CLASSES 7
 int qh_profile_step(qh_ctx *ctx, size_t steps, double *ms_by_class, size_t nclass);
 
 /* Benchmark surface for single matvecs with device-resident inputs: uploads

@@ -234,8 +234,7 @@ class Model:
         self.dev._check(lib().qh_layer_forward(self.dev.h, layer, _ptr(x), pos, _ptr(kp), _ptr(vp), _ptr(ids), _ptr(w)))
         return x, ids, w
 
-    KERNEL_CLASSES = ["embed", "rms_qkv", "qk_norm_rope", "attention", "oproj", "router",
-                      "gateup", "down", "final"]
+    KERNEL_CLASSES = ["qkv", "attention", "oproj", "gateup", "down", "vocab", "finish"]
 
     def profile_step(self, steps):
         """Mean GPU ms per token of each kernel class (events between kernels)."""

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -20,6 +21,7 @@
 #include "gguf.hpp"
 #include "kernels.hpp"
 #include "qh_rows.hpp"
+#include "qh_tile.hpp"
 
 namespace qh {
 // Kernels (kernels.hip).
@@ -29,15 +31,16 @@ template <int R> __global__ void k_matvec(DevMat, const float*, float*, int);
 __global__ void k_route(const float*, uint32_t, uint32_t, uint32_t*, float*, uint32_t*);
 __global__ void k_argmax(const float*, uint32_t, int32_t*, uint32_t*, uint32_t*, uint32_t*, uint32_t*);
 __global__ void k_attention_api(AttnArgs, uint32_t);
-__global__ void k_embed(DevMat, Acts, ModelDims);
-template <int R> __global__ void k_rms_qkv(LayerW, Acts, ModelDims);
-__global__ void k_qk_norm_rope(LayerW, Acts, ModelDims);
-__global__ void k_attention(AttnArgs, Acts, ModelDims);
-template <int R> __global__ void k_oproj(LayerW, Acts, ModelDims);
-template <int R> __global__ void k_router(LayerW, Acts, ModelDims);
-template <int P> __global__ void k_gateup(LayerW, Acts, ModelDims);
-template <int R> __global__ void k_down(LayerW, Acts, ModelDims);
-template <int R> __global__ void k_final(DevMat, const float*, Acts, ModelDims);
+// Token-step kernels (step.hip).
+// Template argument C: held chunk slots per lane (tile_slots), 0 = general.
+template <int C> __global__ void k_qkv(LayerW, DevMat, Acts, ModelDims, int);
+__global__ void k_attn(LayerW, AttnArgs, Acts, ModelDims);
+__global__ void k_attn128(LayerW, AttnArgs, Acts, ModelDims);
+template <int C> __global__ void k_oproj(LayerW, Acts, ModelDims);
+template <int C> __global__ void k_gateup(LayerW, Acts, ModelDims, uint32_t);
+template <int C> __global__ void k_down(LayerW, Acts, ModelDims);
+template <int C> __global__ void k_vocab(DevMat, const float*, Acts, ModelDims);
+__global__ void k_finish(Acts, ModelDims, uint32_t);
 }  // namespace qh
 
 using namespace qh;
@@ -50,7 +53,9 @@ using namespace qh;
 
 namespace {
 
-constexpr uint32_t kMaxGrid = 2048;  // grid-stride cap for matvec-shaped kernels
+constexpr uint32_t kMaxGrid = 2048;     // grid-stride cap for matvec-shaped kernels
+constexpr uint32_t kRouterParts = 64;   // most k_oproj workgroups (router partial rows)
+constexpr int kWideBlock = 512;         // k_oproj and k_gateup workgroup size
 
 uint32_t pad32h(uint64_t n) { return (uint32_t)((n + 31) / 32 * 32); }
 
@@ -151,12 +156,17 @@ struct qh_ctx {
     DevBuf acts_buf, kv, rope_buf;
     Acts acts{};
     uint32_t max_chunks = 0, tc = 32;
+    bool attn128 = false;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    bool use_graph = true;  // QH_NO_GRAPH=1: launch the step's kernels directly (profilers)
 
-    // launch geometry of the step kernels
-    uint32_t g_embed = 1, g_qkv = 1, g_qkn = 1, g_o = 1, g_router = 1, g_gu = 1, g_down = 1, g_final = 1;
-    size_t lds_h = 0, lds_attn = 0, lds_o = 0, lds_router = 0, lds_down = 0;
+    // launch geometry of the step kernels; per layer the held chunk slots
+    // (0 qkv, 1 oproj, 2 gateup, 3 down) and for the vocab projection
+    uint32_t g_qkv = 1, g_o = 1, g_gu = 1, g_down = 1, g_vocab = 1;
+    std::vector<std::array<int, 4>> slots;
+    int vocab_slots = 0;
+    size_t lds_h = 0, lds_attn = 0, lds_o = 0, lds_gu = 0, lds_down = 0;
 
     // scratch for the API surfaces
     DevBuf sa, sb, sc, sd;
@@ -277,15 +287,14 @@ void alloc_acts(qh_ctx* c) {
     const ModelDims& d = c->dm;
     const uint64_t hp = pad32h(d.hidden), qd = pad32h((uint64_t)d.heads * d.head_dim),
                    kvd = pad32h((uint64_t)d.kvheads * d.head_dim), fp = pad32h(d.ff);
-    if (c->max_chunks * c->tc < c->context) throw Error("attention tile not chosen");
     Acts& a = c->acts;
     std::vector<std::pair<size_t, void**>> parts = {
         {hp * 4, (void**)&a.x},
-        {hp * 4, (void**)&a.xn},
         {qd * 4, (void**)&a.q},
         {kvd * 4, (void**)&a.k},
         {kvd * 4, (void**)&a.v},
         {qd * 4, (void**)&a.attn},
+        {(uint64_t)kRouterParts * (d.experts + 1) * 4, (void**)&a.rpart},
         {pad32h(d.experts) * 4, (void**)&a.logits_r},
         {pad32h(d.top) * 4, (void**)&a.ids},
         {pad32h(d.top) * 4, (void**)&a.wts},
@@ -314,70 +323,133 @@ void alloc_acts(qh_ctx* c) {
     a.rope = c->rope_buf.as<const float2>();
 }
 
-// Attention key tile: the largest power of two <= 64 whose LDS footprint
-// fits; fixes the chunk count (and partial buffer) of the model's context.
+// Attention geometry: up to 32 chunk workgroups per KV head (at least 32
+// keys each), 32-key LDS tiles.  Fixes the partial buffer of the context.
+constexpr uint32_t kAttnTile = 32, kAttnMaxChunks = 32;
 void choose_attn_tile(qh_ctx* c) {
     const ModelDims& d = c->dm;
-    const uint32_t G = d.heads / d.kvheads, hd = d.head_dim;
-    auto attn_lds = [&](uint32_t tc) { return (size_t)(G * hd + tc * (hd + 1) + tc * hd + G * tc + 2 * G) * 4; };
-    c->tc = 64;
-    while (c->tc > 1 && attn_lds(c->tc) > 60 * 1024) c->tc /= 2;
-    if (attn_lds(c->tc) > 64 * 1024) throw Error("attention shape exceeds the LDS budget");
-    c->lds_attn = attn_lds(c->tc);
-    c->max_chunks = (uint32_t)((c->context + c->tc - 1) / c->tc);
+    const uint32_t G = d.heads / d.kvheads, hd = d.head_dim, T = kAttnTile;
+    // head_dim 128 with up to 8 query heads per KV head: the register-slice
+    // kernel (k_attn128); otherwise the general LDS-tiled one
+    c->attn128 = hd == 128 && G >= 1 && G <= 8;
+    if (c->attn128)
+        c->lds_attn = (size_t)(8 * 160 + 160 + 128 + T * 128 + 8 * 36 + 8 + 16) * 4;
+    else
+        c->lds_attn = (size_t)(G * hd + 2 * hd + T * (hd + 1) + T * hd + G * T + G * hd + 3 * G) * 4;
+    if (c->lds_attn > 64 * 1024) throw Error("attention shape exceeds the LDS budget");
+    if (G > hd) throw Error("more query heads per KV head than head_dim is not supported");
+    c->tc = T;
+    c->max_chunks = (uint32_t)std::min<size_t>(kAttnMaxChunks, (c->context + 31) / 32);
 }
 
 void choose_geometry(qh_ctx* c) {
     const ModelDims& d = c->dm;
     const LayerW& L = c->layers[0];
-    c->g_embed = (uint32_t)std::min<uint64_t>((d.hidden + kBlock - 1) / kBlock, 1024);
-    c->lds_h = (size_t)pad32h(d.hidden) * 4;
-    c->g_qkv = blocks_for(groups_host(L.q.rows, L.q.cols, 2) + groups_host(L.k.rows, L.k.cols, 2) +
-                          groups_host(L.v.rows, L.v.cols, 2));
-    c->g_qkn = d.heads + 2 * d.kvheads;
-    c->g_o = blocks_for(groups_host(L.o.rows, L.o.cols, 2));
-    c->lds_o = (size_t)pad32h((uint64_t)d.heads * d.head_dim) * 4;
-    c->g_router = blocks_for(groups_host(L.router.rows, L.router.cols, 1));
-    c->lds_router = c->lds_h + (size_t)d.top * 4;
-    {
-        int Lw = lanes_per_row(d.hidden), S = 64 / Lw;
-        uint64_t per = 2 * S;
-        c->g_gu = blocks_for((uint64_t)d.top * ((d.ff + per - 1) / per));
+    const size_t lds_cap = 64 * 1024;
+    c->slots.clear();
+    for (const LayerW& W : c->layers) {
+        // held tiles need one block-quantised format per launch role
+        const bool qkv_q = is_quant(W.q.kind) && is_quant(W.k.kind) && is_quant(W.v.kind);
+        const bool gu_q = W.gate.kind == W.up.kind;
+        c->slots.push_back({qkv_q ? tile_slots(W.q.kind, W.q.cols) : 0, tile_slots(W.o.kind, W.o.cols),
+                            gu_q ? tile_slots(W.gate.kind, W.gate.cols) : 0, is_quant(W.down.kind) ? 1 : 0});
     }
+    c->vocab_slots = tile_slots(c->out.kind, c->out.cols);
+    c->lds_h = (size_t)pad32h(d.hidden) * 4;
+    // k_qkv: one workgroup per 4 row groups (2 rows each), per matrix
+    auto wgs = [](const DevMat& m) { return (groups_host(m.rows, m.cols, 2) + kWaves - 1) / kWaves; };
+    const uint64_t gq = wgs(L.q) + wgs(L.k) + wgs(L.v);
+    if (gq > 65535) throw Error("attention projections too large for one launch");
+    c->g_qkv = (uint32_t)gq;
+    c->g_o = std::min<uint32_t>(kRouterParts, d.hidden);
+    c->lds_o = ((size_t)pad32h((uint64_t)d.heads * d.head_dim) + 2 * ((d.hidden + c->g_o - 1) / c->g_o)) * 4;
+    {
+        // k_gateup: per routed slot, enough workgroups that each wave owns one
+        // group of 2 row pairs
+        const uint64_t per_wg = (uint64_t)(kWideBlock / 64) * 2 * (64 / lanes_per_row(d.hidden));
+        uint64_t wps = (d.ff + per_wg - 1) / per_wg;
+        wps = std::max<uint64_t>(1, std::min<uint64_t>(wps, kMaxGrid / std::max<uint32_t>(1, d.top)));
+        c->g_gu = (uint32_t)(d.top * wps);
+    }
+    // k_gateup folds the router partials of at most 64 workgroups for at most
+    // 255 experts (two 128-expert passes of four threads each)
+    if (d.experts + 1 > 256) throw Error("more than 255 experts is not supported by the routing kernel");
+    if (c->g_o > 64) throw Error("too many router partial rows");
+    c->lds_gu = ((size_t)pad32h(d.hidden) + d.experts + 1 + 2 * d.top + 4) * 4;
     c->g_down = blocks_for((d.hidden + 1) / 2);
     c->lds_down = ((size_t)d.top * pad32h(d.ff) + 2 * d.top) * 4;
-    c->g_final = blocks_for(groups_host(c->out.rows, c->out.cols, 4));
-    const size_t lds_cap = 64 * 1024;
-    if (c->lds_h > lds_cap || c->lds_o > lds_cap || c->lds_router > lds_cap)
+    c->g_vocab = blocks_for(groups_host(c->out.rows, c->out.cols, 2));
+    if (c->lds_h > lds_cap || c->lds_o > lds_cap || c->lds_gu > lds_cap)
         throw Error("hidden size exceeds the LDS budget of the device kernels");
     if (c->lds_down > lds_cap) throw Error("expert_used_count * expert FFN exceeds the LDS budget");
 }
 
-// Enqueues one layer's kernels.
-void enqueue_layer(qh_ctx* c, size_t l) {
+// Launches kern<C> for the held chunk slots C in {0, 1, 2}.
+#define QH_LAUNCH_SLOTS(kern, C, ...)                                    \
+    switch (C) {                                                         \
+    case 1: hipLaunchKernelGGL(kern<1>, __VA_ARGS__); break;             \
+    case 2: hipLaunchKernelGGL(kern<2>, __VA_ARGS__); break;             \
+    default: hipLaunchKernelGGL(kern<0>, __VA_ARGS__); break;            \
+    }
+
+// Enqueues kernel k (0 qkv, 1 attention, 2 oproj, 3 gateup, 4 down) of
+// layer l (first: the layer also embeds tokens[pos]).
+void enqueue_kernel(qh_ctx* c, size_t l, bool first, int k) {
     const ModelDims& d = c->dm;
     const LayerW& L = c->layers[l];
-    hipLaunchKernelGGL(k_rms_qkv<2>, dim3(c->g_qkv), dim3(kBlock), c->lds_h, c->s, L, c->acts, d);
-    hipLaunchKernelGGL(k_qk_norm_rope, dim3(c->g_qkn), dim3(kBlock), 0, c->s, L, c->acts, d);
-    hipLaunchKernelGGL(k_attention, dim3(d.kvheads, c->max_chunks), dim3(kBlock), c->lds_attn, c->s, c->attn[l], c->acts, d);
-    hipLaunchKernelGGL(k_oproj<2>, dim3(c->g_o), dim3(kBlock), c->lds_o, c->s, L, c->acts, d);
-    hipLaunchKernelGGL(k_router<1>, dim3(c->g_router), dim3(kBlock), c->lds_router, c->s, L, c->acts, d);
-    hipLaunchKernelGGL(k_gateup<2>, dim3(c->g_gu), dim3(kBlock), c->lds_h, c->s, L, c->acts, d);
-    hipLaunchKernelGGL(k_down<2>, dim3(c->g_down), dim3(kBlock), c->lds_down, c->s, L, c->acts, d);
+    const auto& sl = c->slots[l];
+    switch (k) {
+    case 0: QH_LAUNCH_SLOTS(k_qkv, sl[0], dim3(c->g_qkv), dim3(kBlock), c->lds_h, c->s, L, c->emb, c->acts, d, (int)first); break;
+    case 1:
+        if (c->attn128)
+            hipLaunchKernelGGL(k_attn128, dim3(d.kvheads, c->max_chunks), dim3(kBlock), c->lds_attn, c->s, L, c->attn[l], c->acts, d);
+        else
+            hipLaunchKernelGGL(k_attn, dim3(d.kvheads, c->max_chunks), dim3(kBlock), c->lds_attn, c->s, L, c->attn[l], c->acts, d);
+        break;
+    case 2: QH_LAUNCH_SLOTS(k_oproj, sl[1], dim3(c->g_o), dim3(kWideBlock), c->lds_o, c->s, L, c->acts, d); break;
+    case 3: QH_LAUNCH_SLOTS(k_gateup, sl[2], dim3(c->g_gu), dim3(kWideBlock), c->lds_gu, c->s, L, c->acts, d, c->g_o); break;
+    default:
+        if (sl[3]) hipLaunchKernelGGL(k_down<1>, dim3(c->g_down), dim3(kBlock), c->lds_down, c->s, L, c->acts, d);
+        else hipLaunchKernelGGL(k_down<0>, dim3(c->g_down), dim3(kBlock), c->lds_down, c->s, L, c->acts, d);
+        break;
+    }
+}
+
+void enqueue_vocab(qh_ctx* c) {
+    QH_LAUNCH_SLOTS(k_vocab, c->vocab_slots, dim3(c->g_vocab), dim3(kBlock), c->lds_h, c->s, c->out, c->onorm, c->acts, c->dm);
+}
+
+void enqueue_layer(qh_ctx* c, size_t l, bool first) {
+    for (int k = 0; k < 5; k++) enqueue_kernel(c, l, first, k);
+}
+
+void enqueue_tail(qh_ctx* c) {
+    enqueue_vocab(c);
+    hipLaunchKernelGGL(k_finish, dim3(1), dim3(kBlock), 0, c->s, c->acts, c->dm, c->g_vocab);
 }
 
 void enqueue_step(qh_ctx* c) {
-    hipLaunchKernelGGL(k_embed, dim3(c->g_embed), dim3(kBlock), 0, c->s, c->emb, c->acts, c->dm);
-    for (size_t l = 0; l < c->layers.size(); l++) enqueue_layer(c, l);
-    hipLaunchKernelGGL(k_final<4>, dim3(c->g_final), dim3(kBlock), c->lds_h, c->s, c->out, c->onorm, c->acts, c->dm);
+    for (size_t l = 0; l < c->layers.size(); l++) enqueue_layer(c, l, l == 0);
+    enqueue_tail(c);
 }
 
 void capture_graph(qh_ctx* c) {
+    if (!c->use_graph) return;
     HIP_OK(hipStreamBeginCapture(c->s, hipStreamCaptureModeThreadLocal));
     enqueue_step(c);
     hipError_t e = hipStreamEndCapture(c->s, &c->graph);
     if (e != hipSuccess) throw Error(std::string("graph capture: ") + hipGetErrorString(e));
     HIP_OK(hipGraphInstantiate(&c->exec, c->graph, nullptr, nullptr, 0));
+}
+
+// One token step: the captured graph, or the same kernels launched directly.
+void launch_step(qh_ctx* c) {
+    if (c->use_graph) {
+        HIP_OK(hipGraphLaunch(c->exec, c->s));
+    } else {
+        enqueue_step(c);
+        HIP_OK(hipGetLastError());
+    }
 }
 
 void load_image(qh_ctx* c, const uint8_t* data, size_t len, size_t context) {
@@ -530,6 +602,8 @@ int qh_create(int device, qh_ctx** out) {
         HIP_OK(hipSetDevice(device));
         auto c = std::make_unique<qh_ctx>();
         c->device = device;
+        const char* ng = std::getenv("QH_NO_GRAPH");
+        c->use_graph = !(ng && ng[0] == '1');
         HIP_OK(hipStreamCreateWithFlags(&c->s, hipStreamNonBlocking));
         *out = c.release();
         return 0;
@@ -768,7 +842,7 @@ int qh_forward(qh_ctx* c, uint32_t token, float* logits, uint32_t* argmax) {
         }
         HIP_OK(hipMemcpyAsync(c->acts.tokens + c->pos, &token, 4, hipMemcpyHostToDevice, c->s));
         put_state(c, (uint32_t)c->pos, (uint32_t)c->pos + 1);
-        HIP_OK(hipGraphLaunch(c->exec, c->s));
+        launch_step(c);
         if (logits)
             HIP_OK(hipMemcpyAsync(logits, c->acts.logits, c->cfg.vocab * 4, hipMemcpyDeviceToHost, c->s));
         DevState st = get_state(c);
@@ -792,7 +866,7 @@ int qh_generate(qh_ctx* c, const uint32_t* prompt, size_t n_prompt, size_t n_new
             if (prompt[i] >= c->cfg.vocab) throw Error("token outside vocabulary");
         HIP_OK(hipMemcpyAsync(c->acts.tokens + c->pos, prompt, n_prompt * 4, hipMemcpyHostToDevice, c->s));
         put_state(c, (uint32_t)c->pos, (uint32_t)(c->pos + n_prompt));
-        for (size_t i = 0; i < steps; i++) HIP_OK(hipGraphLaunch(c->exec, c->s));
+        for (size_t i = 0; i < steps; i++) launch_step(c);
         DevState st = get_state(c);
         if (st.err) fail_step(c, st.err);
         if (n_new)
@@ -846,7 +920,7 @@ int qh_layer_forward(qh_ctx* c, size_t layer, float* x, size_t pos, const float*
             sync(c);  // host staging vectors go out of scope
         }
         put_state(c, (uint32_t)pos, (uint32_t)pos + 1);
-        enqueue_layer(c, layer);
+        enqueue_layer(c, layer, false);
         HIP_OK(hipGetLastError());
         HIP_OK(hipMemcpyAsync(x, c->acts.x, d.hidden * 4, hipMemcpyDeviceToHost, c->s));
         if (ids) HIP_OK(hipMemcpyAsync(ids, c->acts.ids, d.top * 4, hipMemcpyDeviceToHost, c->s));
@@ -863,12 +937,12 @@ int qh_bench_decode(qh_ctx* c, size_t warmup, size_t steps, double* ms_total) {
         if (c->pos == 0) throw Error("bench_decode continues a sequence: run a prompt first");
         if (c->pos + warmup + steps > c->context) throw Error("prompt + max-tokens exceed --ctx");
         put_state(c, (uint32_t)c->pos, (uint32_t)c->pos);
-        for (size_t i = 0; i < warmup; i++) HIP_OK(hipGraphLaunch(c->exec, c->s));
+        for (size_t i = 0; i < warmup; i++) launch_step(c);
         hipEvent_t e0, e1;
         HIP_OK(hipEventCreate(&e0));
         HIP_OK(hipEventCreate(&e1));
         HIP_OK(hipEventRecord(e0, c->s));
-        for (size_t i = 0; i < steps; i++) HIP_OK(hipGraphLaunch(c->exec, c->s));
+        for (size_t i = 0; i < steps; i++) launch_step(c);
         HIP_OK(hipEventRecord(e1, c->s));
         HIP_OK(hipEventSynchronize(e1));
         float ms = 0;
@@ -890,34 +964,22 @@ int qh_profile_step(qh_ctx* c, size_t steps, double* ms_by_class, size_t nclass)
         if (c->pos == 0) throw Error("profile_step continues a sequence: run a prompt first");
         if (c->pos + steps > c->context) throw Error("prompt + max-tokens exceed --ctx");
         const size_t L = c->layers.size();
-        std::vector<hipEvent_t> ev(2 + 7 * L + 1);
+        std::vector<hipEvent_t> ev(1 + 5 * L + 2);
         for (auto& e : ev) HIP_OK(hipEventCreate(&e));
         std::vector<double> acc(QH_NUM_KERNEL_CLASSES, 0.0);
         put_state(c, (uint32_t)c->pos, (uint32_t)c->pos);
-        const ModelDims& d = c->dm;
         for (size_t s = 0; s < steps; s++) {
             size_t k = 0;
             HIP_OK(hipEventRecord(ev[k++], c->s));
-            hipLaunchKernelGGL(k_embed, dim3(c->g_embed), dim3(kBlock), 0, c->s, c->emb, c->acts, d);
-            HIP_OK(hipEventRecord(ev[k++], c->s));
             for (size_t l = 0; l < L; l++) {
-                const LayerW& W = c->layers[l];
-                hipLaunchKernelGGL(k_rms_qkv<2>, dim3(c->g_qkv), dim3(kBlock), c->lds_h, c->s, W, c->acts, d);
-                HIP_OK(hipEventRecord(ev[k++], c->s));
-                hipLaunchKernelGGL(k_qk_norm_rope, dim3(c->g_qkn), dim3(kBlock), 0, c->s, W, c->acts, d);
-                HIP_OK(hipEventRecord(ev[k++], c->s));
-                hipLaunchKernelGGL(k_attention, dim3(d.kvheads, c->max_chunks), dim3(kBlock), c->lds_attn, c->s, c->attn[l], c->acts, d);
-                HIP_OK(hipEventRecord(ev[k++], c->s));
-                hipLaunchKernelGGL(k_oproj<2>, dim3(c->g_o), dim3(kBlock), c->lds_o, c->s, W, c->acts, d);
-                HIP_OK(hipEventRecord(ev[k++], c->s));
-                hipLaunchKernelGGL(k_router<1>, dim3(c->g_router), dim3(kBlock), c->lds_router, c->s, W, c->acts, d);
-                HIP_OK(hipEventRecord(ev[k++], c->s));
-                hipLaunchKernelGGL(k_gateup<2>, dim3(c->g_gu), dim3(kBlock), c->lds_h, c->s, W, c->acts, d);
-                HIP_OK(hipEventRecord(ev[k++], c->s));
-                hipLaunchKernelGGL(k_down<2>, dim3(c->g_down), dim3(kBlock), c->lds_down, c->s, W, c->acts, d);
-                HIP_OK(hipEventRecord(ev[k++], c->s));
+                for (int kk = 0; kk < 5; kk++) {
+                    enqueue_kernel(c, l, l == 0, kk);
+                    HIP_OK(hipEventRecord(ev[k++], c->s));
+                }
             }
-            hipLaunchKernelGGL(k_final<4>, dim3(c->g_final), dim3(kBlock), c->lds_h, c->s, c->out, c->onorm, c->acts, d);
+            enqueue_vocab(c);
+            HIP_OK(hipEventRecord(ev[k++], c->s));
+            hipLaunchKernelGGL(k_finish, dim3(1), dim3(kBlock), 0, c->s, c->acts, c->dm, c->g_vocab);
             HIP_OK(hipEventRecord(ev[k++], c->s));
             HIP_OK(hipGetLastError());
             HIP_OK(hipEventSynchronize(ev[k - 1]));
@@ -926,10 +988,10 @@ int qh_profile_step(qh_ctx* c, size_t steps, double* ms_by_class, size_t nclass)
                 HIP_OK(hipEventElapsedTime(&ms, ev[a], ev[a + 1]));
                 return (double)ms;
             };
-            acc[0] += el(0);
             for (size_t l = 0; l < L; l++)
-                for (size_t j = 0; j < 7; j++) acc[1 + j] += el(1 + 7 * l + j);
-            acc[8] += el(1 + 7 * L);
+                for (size_t j = 0; j < 5; j++) acc[j] += el(5 * l + j);
+            acc[5] += el(5 * L);
+            acc[6] += el(5 * L + 1);
         }
         for (auto& e : ev) (void)hipEventDestroy(e);
         DevState st = get_state(c);

@@ -27,7 +27,7 @@ struct DevState {
     uint32_t n_given;  // tokens[0, n_given) come from the caller; later ones from argmax
     uint32_t err;      // error bits (kErr*)
     uint32_t argmax;   // greedy id of the last completed step
-    uint32_t cnt_router, cnt_final, pad0, pad1;
+    uint32_t pad[4];
 };
 
 enum : uint32_t {
@@ -54,23 +54,23 @@ struct ModelDims {
 
 // Scratch activations of one step.
 struct Acts {
-    float* x;        // [H] residual stream
-    float* xn;       // [H] normalised input of the expert FFN
-    float* q;        // [heads*d]
-    float* k;        // [kvheads*d]
-    float* v;        // [kvheads*d]
-    float* attn;     // [heads*d]
-    float* logits_r; // [experts]
-    uint32_t* ids;   // [top]
-    float* wts;      // [top]
-    float* h;        // [top*ff]
-    float* logits;   // [vocab]
-    float* part;     // attention partials [heads][max_chunks][d+2]
-    uint32_t* attn_cnt;   // [kvheads] last-block counters
-    uint32_t* fin_key;    // [max final blocks] argmax partial keys
-    uint32_t* fin_idx;    // [max final blocks]
-    uint32_t* tokens;     // [ctx+1]
-    const float2* rope;   // [ctx][d/2] (cos, sin)
+    float* x;          // [H] residual stream
+    float* q;          // [heads*d]   raw q projection
+    float* k;          // [kvheads*d] raw k projection
+    float* v;          // [kvheads*d] raw v projection
+    float* attn;       // [heads*d] attention output
+    float* rpart;      // [router parts][experts+1] router partial dots + sum of squares
+    float* logits_r;   // [experts] router logits of the last layer run (diagnostics)
+    uint32_t* ids;     // [top] routed experts of the current layer
+    float* wts;        // [top] their renormalised weights
+    float* h;          // [top][pad32(ff)] SwiGLU outputs
+    float* logits;     // [vocab]
+    float* part;       // attention partials [heads][max_chunks][d+2]
+    uint32_t* attn_cnt;  // [kvheads] last-arrival counters of the attention combine
+    uint32_t* fin_key;   // [final blocks] vocab argmax partial keys
+    uint32_t* fin_idx;   // [final blocks]
+    uint32_t* tokens;    // [ctx+2]
+    const float2* rope;  // [ctx][d/2] (cos, sin)
     DevState* st;
 };
 

@@ -1,0 +1,203 @@
+// Workgroup-level building blocks shared by the API kernels (kernels.hip)
+// and the token-step kernels (step.hip): reductions, RMSNorm into LDS, the
+// matvec row-group drivers, top-k ranking and argmax merging.
+#pragma once
+#include "kernels.hpp"
+#include "qh_rows.hpp"
+
+namespace qh {
+
+// Phase marks of the token-step kernels: QH_MARK(kernel, phase) records the
+// wall clock of thread 0 of each workgroup when a translation unit that
+// defines QH_PHASE_TRACE (and qh_phase_mark) includes the kernels; otherwise
+// it compiles to nothing.
+#ifdef QH_PHASE_TRACE
+__device__ void qh_phase_mark(int kernel, int phase);
+#define QH_MARK(k, p) ::qh::qh_phase_mark((k), (p))
+#else
+#define QH_MARK(k, p) ((void)0)
+#endif
+
+// ------------------------------------------------------------------ helpers --
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < kWaves; i++) s += red[i];
+    __syncthreads();
+    return s;
+}
+
+// xs[i] = x[i] * (scale * w[i]) with scale = 1/sqrt(mean(x^2) + eps)
+// (src/ops.rs:3-15), zero-padded to npad; ends with a barrier.
+__device__ __forceinline__ void rms_to_lds(const float* x, const float* w, uint32_t n, uint32_t npad, float eps,
+                           float* xs, float* red) {
+    float ss = 0.f;
+    for (uint32_t i = threadIdx.x; i < n; i += kBlock) {
+        float v = x[i];
+        ss = fmaf(v, v, ss);
+    }
+    const float tot = block_sum(ss, red);
+    const float scale = 1.0f / sqrtf(tot / (float)n + eps);
+    for (uint32_t i = threadIdx.x; i < npad; i += kBlock) xs[i] = i < n ? x[i] * (scale * w[i]) : 0.f;
+    __syncthreads();
+}
+
+__device__ __forceinline__ void stage_lds(const float* x, uint32_t n, uint32_t npad, float* xs) {
+    for (uint32_t i = threadIdx.x; i < npad; i += kBlock) xs[i] = i < n ? x[i] : 0.f;
+    __syncthreads();
+}
+
+__device__ __forceinline__ uint32_t pad32(uint32_t n) { return (n + 31) / 32 * 32; }
+
+// True for exactly one workgroup: the last one of `expected` to arrive.
+// Performs release before and acquire after the counter update.
+__device__ __forceinline__ bool last_arrival(uint32_t* counter, uint32_t expected) {
+    __shared__ uint32_t last;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t old = atomicAdd(counter, 1u);
+        last = (old == expected - 1) ? 1u : 0u;
+        if (last) atomicExch(counter, 0u);
+    }
+    __syncthreads();
+    if (last) __threadfence();
+    return last != 0;
+}
+
+// Row groups of a matrix processed R*S rows at a time by a wave.
+struct Groups {
+    int L, S;
+    uint32_t per, n;
+};
+__device__ __forceinline__ Groups groups_of(uint32_t rows, uint32_t cols, int R) {
+    Groups g;
+    g.L = lanes_per_row(cols);
+    g.S = 64 / g.L;
+    g.per = (uint32_t)(R * g.S);
+    g.n = (rows + g.per - 1) / g.per;
+    return g;
+}
+
+// One group of rows of matrix m against x in LDS; epi(row, value) is called
+// by the lane holding each row's result.
+template <uint32_t KIND, int R, typename Epi>
+__device__ __forceinline__ void mv_group(const DevMat& m, const uint8_t* base, const Groups& gp,
+                                         uint32_t grp, const float* xs, Epi epi) {
+    const uint32_t lane = threadIdx.x & 63, sub = lane / gp.L, cl = lane % gp.L;
+    const uint32_t r0 = grp * gp.per + sub;
+    float acc[R];
+    rows_dot<KIND, R>(
+        [&](int k) -> const uint8_t* {
+            uint32_t r = r0 + k * gp.S;
+            return r < m.rows ? base + (size_t)r * m.drb : nullptr;
+        },
+        m.geo, xs, m.cols, gp.L, cl, acc);
+#pragma unroll
+    for (int k = 0; k < R; k++) acc[k] = seg_sum(acc[k], gp.L);
+    if (cl == 0) {
+#pragma unroll
+        for (int k = 0; k < R; k++) {
+            uint32_t r = r0 + k * gp.S;
+            if (r < m.rows) epi(r, acc[k]);
+        }
+    }
+}
+
+// All groups of one matrix, spread over every wave of the grid.
+template <int R, typename Epi>
+__device__ __forceinline__ void mv_all(const DevMat& m, const uint8_t* base, const float* xs, Epi epi) {
+    const Groups gp = groups_of(m.rows, m.cols, R);
+    const uint32_t gw = blockIdx.x * kWaves + (threadIdx.x >> 6), nw = gridDim.x * kWaves;
+    QH_DISPATCH_KIND(m.kind, {
+        for (uint32_t grp = gw; grp < gp.n; grp += nw) mv_group<K_, R>(m, base, gp, grp, xs, epi);
+    });
+}
+
+// Router top-k (src/ops.rs:45-56) inside one workgroup: rank every logit by
+// total order with index tie-break, keep ranks < top, then a sequential
+// softmax over the chosen logits in rank order.  Non-finite input sets
+// kErrRouter and leaves ids/w untouched.
+__device__ __forceinline__ void route_block(const float* logits, uint32_t n, uint32_t top, uint32_t* ids, float* w,
+                            uint32_t* err, float* sw) {
+    __shared__ uint32_t bad;
+    if (threadIdx.x == 0) bad = 0;
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < n; i += kBlock) {
+        const float v = logits[i];
+        if (!finite_f(v)) bad = 1;
+        const int32_t key = total_key(v);
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < n; j++) {
+            const int32_t kj = total_key(logits[j]);
+            rank += (kj > key) || (kj == key && j < i);
+        }
+        if (rank < top) {
+            ids[rank] = i;
+            sw[rank] = v;
+        }
+    }
+    __syncthreads();
+    if (bad) {
+        if (threadIdx.x == 0) atomicOr(err, kErrRouter);
+        return;
+    }
+    if (threadIdx.x == 0) {
+#pragma clang fp contract(off)
+        float mx = -INFINITY;
+        for (uint32_t i = 0; i < top; i++) mx = fmaxf(mx, sw[i]);
+        float sum = 0.f;
+        for (uint32_t i = 0; i < top; i++) {
+            sw[i] = expf(sw[i] - mx);
+            sum += sw[i];
+        }
+        for (uint32_t i = 0; i < top; i++) w[i] = sw[i] / sum;
+    }
+}
+
+// (key, index) merge for argmax under total order, lowest index on ties.
+__device__ __forceinline__ void best_merge(int32_t& k, uint32_t& i, int32_t k2, uint32_t i2) {
+    if (k2 > k || (k2 == k && i2 < i)) {
+        k = k2;
+        i = i2;
+    }
+}
+template <int CTRL>
+__device__ __forceinline__ void best_step(int32_t& k, uint32_t& i) {
+    best_merge(k, i, dpp_i<CTRL>(k), (uint32_t)dpp_i<CTRL>((int32_t)i));
+}
+// Wave-wide best; result valid in every lane (all lanes active).
+__device__ __forceinline__ void wave_best(int32_t& k, uint32_t& i) {
+    best_step<kDppXor1>(k, i);
+    best_step<kDppXor2>(k, i);
+    best_step<kDppHalfMirror>(k, i);
+    best_step<kDppMirror>(k, i);
+    int32_t bk = __builtin_amdgcn_readlane(k, 0);
+    uint32_t bi = (uint32_t)__builtin_amdgcn_readlane((int32_t)i, 0);
+#pragma unroll
+    for (int r = 16; r < 64; r += 16)
+        best_merge(bk, bi, __builtin_amdgcn_readlane(k, r), (uint32_t)__builtin_amdgcn_readlane((int32_t)i, r));
+    k = bk;
+    i = bi;
+}
+// Block-wide best; result valid in every thread.
+__device__ __forceinline__ void block_best(int32_t& k, uint32_t& i) {
+    __shared__ int32_t sk[kWaves];
+    __shared__ uint32_t si[kWaves];
+    wave_best(k, i);
+    if ((threadIdx.x & 63) == 0) {
+        sk[threadIdx.x >> 6] = k;
+        si[threadIdx.x >> 6] = i;
+    }
+    __syncthreads();
+    k = sk[0];
+    i = si[0];
+    for (int w = 1; w < kWaves; w++) best_merge(k, i, sk[w], si[w]);
+    __syncthreads();
+}
+
+}  // namespace qh

@@ -47,13 +47,37 @@ __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
     return *reinterpret_cast<const uint16_t*>(p);
 }
 
+// Hides a value from the optimiser's known-bits analysis, so that byte k of a
+// pre-masked word still converts with one v_cvt_f32_ubyte<k> instead of a
+// bitfield extract plus convert.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // Four bytes of `w` as floats, multiplied into x[0..4) and accumulated.
 __device__ __forceinline__ float dot4u8(uint32_t w, const float* x, float acc) {
+    w = opaque(w);
     acc = fmaf(x[0], (float)(w & 0xffu), acc);
     acc = fmaf(x[1], (float)((w >> 8) & 0xffu), acc);
     acc = fmaf(x[2], (float)((w >> 16) & 0xffu), acc);
     acc = fmaf(x[3], (float)(w >> 24), acc);
     return acc;
+}
+
+// 6-bit (scale, min) of the sub-block pair (2p, 2p+1), p in 0..3, from the
+// 12 scale bytes in s0 (bytes 0-3), s1 (4-7), s2 (8-11), branch-free
+// (src/quant.rs:25-34).  Returns byte 0 = value of sub-block 2p, byte 1 =
+// value of 2p+1.
+__device__ __forceinline__ void kscale_pair(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t p,
+                                            uint32_t& sc, uint32_t& m) {
+    const uint32_t sh = (p & 1) * 16;
+    const uint32_t Y = (s0 >> sh) & 0xffffu, Z = (s1 >> sh) & 0xffffu, W = (s2 >> sh) & 0xffffu;
+    const uint32_t scA = Y & 0x3f3fu, mA = Z & 0x3f3fu;
+    const uint32_t scB = (W & 0x0f0fu) | ((Y >> 2) & 0x3030u);
+    const uint32_t mB = ((W >> 4) & 0x0f0fu) | ((Z >> 2) & 0x3030u);
+    sc = p < 2 ? scA : scB;
+    m = p < 2 ? mA : mB;
 }
 
 template <uint32_t KIND> struct Fmt;
@@ -72,10 +96,10 @@ template <> struct Fmt<Q4_K> {
     }
     static __device__ __forceinline__ float dot(const Raw& r, uint32_t c, const float* xa,
                                                 const float* xb, float sa, float sb) {
-        uint32_t ga = ((c & 7) >> 1) * 2;
-        uint32_t sca, ma, scb, mb;
-        kscale(r.h.y, r.h.z, r.h.w, ga, sca, ma);
-        kscale(r.h.y, r.h.z, r.h.w, ga + 1, scb, mb);
+        uint32_t scp, mp;
+        kscale_pair(r.h.y, r.h.z, r.h.w, (c & 7) >> 1, scp, mp);
+        const float sca = (float)(scp & 0xffu), scb = (float)(scp >> 8), ma = (float)(mp & 0xffu),
+                    mb = (float)(mp >> 8);
         float d = h2f(r.h.x & 0xffff), dm = h2f(r.h.x >> 16);
         uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
         float pa = 0.f, pb = 0.f;
@@ -84,7 +108,7 @@ template <> struct Fmt<Q4_K> {
             pa = dot4u8(w[k] & 0x0f0f0f0fu, xa + 4 * k, pa);
             pb = dot4u8((w[k] >> 4) & 0x0f0f0f0fu, xb + 4 * k, pb);
         }
-        return d * ((float)sca * pa + (float)scb * pb) - dm * ((float)ma * sa + (float)mb * sb);
+        return d * (sca * pa + scb * pb) - dm * (ma * sa + mb * sb);
     }
 };
 
@@ -100,10 +124,11 @@ template <> struct Fmt<Q5_K> {
     }
     static __device__ __forceinline__ float dot(const Raw& r, uint32_t c, const float* xa,
                                                 const float* xb, float sa, float sb) {
-        uint32_t ga = ((c & 7) >> 1) * 2;
-        uint32_t sca, ma, scb, mb;
-        kscale(r.h.y, r.h.z, r.h.w, ga, sca, ma);
-        kscale(r.h.y, r.h.z, r.h.w, ga + 1, scb, mb);
+        const uint32_t ga = ((c & 7) >> 1) * 2;
+        uint32_t scp, mp;
+        kscale_pair(r.h.y, r.h.z, r.h.w, (c & 7) >> 1, scp, mp);
+        const float sca = (float)(scp & 0xffu), scb = (float)(scp >> 8), ma = (float)(mp & 0xffu),
+                    mb = (float)(mp >> 8);
         float d = h2f(r.h.x & 0xffff), dm = h2f(r.h.x >> 16);
         uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
         uint32_t hb[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
@@ -115,13 +140,13 @@ template <> struct Fmt<Q5_K> {
             pa = dot4u8(qa, xa + 4 * k, pa);
             pb = dot4u8(qb, xb + 4 * k, pb);
         }
-        return d * ((float)sca * pa + (float)scb * pb) - dm * ((float)ma * sa + (float)mb * sb);
+        return d * (sca * pa + scb * pb) - dm * (ma * sa + mb * sb);
     }
 };
 
 // -------------------------------------------------------------------- Q6_K --
 template <> struct Fmt<Q6_K> {
-    struct Raw { uint4 ql, qh, sc; uint32_t d; };
+    struct Raw { uint4 ql, qh; uint32_t sc, d; };
     static __device__ __forceinline__ uint32_t xoff_a(uint32_t c) {
         uint32_t j = c & 7;
         return (c >> 3) * 256 + (j >> 2) * 128 + ((j & 3) >> 1) * 32 + (j & 1) * 16;
@@ -129,23 +154,27 @@ template <> struct Fmt<Q6_K> {
     static __device__ __forceinline__ uint32_t xoff_b(uint32_t c) { return xoff_a(c) + 64; }
     static __device__ __forceinline__ Raw load(const uint8_t* row, const RowGeo& g, uint32_t c) {
         uint32_t b = c >> 3, j = c & 7;
+        // scales of this chunk: sc[(j>>2)*8 + qa*2 + (j&1)] (quarter qa) and +4
+        // (quarter qa+2); the 8 bytes of half j>>2 arrive as one 8-byte load
+        const uint2 s8 = *reinterpret_cast<const uint2*>(row + g.off_c + b * 16 + (j >> 2) * 8);
+        const uint32_t sh = (((j & 3) >> 1) * 2 + (j & 1)) * 8;
+        const uint32_t sc = ((s8.x >> sh) & 0xffu) | (((s8.y >> sh) & 0xffu) << 8);
         return {ld16(row + g.off_a + b * 128 + j * 16),
-                ld16(row + g.off_b + b * 64 + (j >> 2) * 32 + (j & 1) * 16),
-                ld16(row + g.off_c + b * 16), ld_u16(row + g.off_d + b * 2)};
+                ld16(row + g.off_b + b * 64 + (j >> 2) * 32 + (j & 1) * 16), sc,
+                ld_u16(row + g.off_d + b * 2)};
     }
     static __device__ __forceinline__ float dot(const Raw& r, uint32_t c, const float* xa,
                                                 const float* xb, float sa, float sb) {
         uint32_t j = c & 7, qa = (j & 3) >> 1;
-        uint32_t ia = (j >> 2) * 8 + qa * 2 + (j & 1);
-        float sca = (float)(int8_t)byte_of(r.sc, ia), scb = (float)(int8_t)byte_of(r.sc, ia + 4);
+        float sca = (float)(int8_t)(r.sc & 0xffu), scb = (float)(int8_t)(r.sc >> 8);
         float d = h2f(r.d);
         uint32_t l[4] = {r.ql.x, r.ql.y, r.ql.z, r.ql.w};
         uint32_t h[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
         float pa = 0.f, pb = 0.f;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            uint32_t ua = (l[k] & 0x0f0f0f0fu) | (((h[k] >> (2 * qa)) & 0x03030303u) << 4);
-            uint32_t ub = ((l[k] >> 4) & 0x0f0f0f0fu) | (((h[k] >> (2 * qa + 4)) & 0x03030303u) << 4);
+            uint32_t ua = (l[k] & 0x0f0f0f0fu) | ((h[k] << (4 - 2 * qa)) & 0x30303030u);
+            uint32_t ub = ((l[k] >> 4) & 0x0f0f0f0fu) | ((h[k] >> (2 * qa)) & 0x30303030u);
             pa = dot4u8(ua, xa + 4 * k, pa);
             pb = dot4u8(ub, xb + 4 * k, pb);
         }
@@ -315,20 +344,45 @@ __device__ __forceinline__ float dequant_value(const uint8_t* row, uint32_t kind
 }
 
 // ------------------------------------------------------------ reductions --
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+// Cross-lane reductions on the DPP crossbar (VALU latency) rather than
+// ds_bpermute (an LDS round trip per step).  Within a row of 16 lanes an xor
+// butterfly (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror) leaves every lane with its group's result; the four rows are
+// then combined through v_readlane.  Every lane of the wave must be active.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+template <int CTRL>
+__device__ __forceinline__ int32_t dpp_i(int32_t v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
 }
-// Sum over aligned segments of `width` lanes (width a power of two <= 64).
+__device__ __forceinline__ float lane_f(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Sum over aligned segments of `width` lanes (a power of two <= 64); every
+// lane of a segment receives the segment's sum.
 __device__ __forceinline__ float seg_sum(float v, int width) {
-    for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    if (width >= 2) v += dpp_f<kDppXor1>(v);
+    if (width >= 4) v += dpp_f<kDppXor2>(v);
+    if (width >= 8) v += dpp_f<kDppHalfMirror>(v);
+    if (width >= 16) v += dpp_f<kDppMirror>(v);
+    if (width >= 32) {
+        const float a = lane_f(v, 0) + lane_f(v, 16), b = lane_f(v, 32) + lane_f(v, 48);
+        v = width == 64 ? a + b : ((threadIdx.x & 32) ? b : a);
+    }
     return v;
+}
+__device__ __forceinline__ float wave_sum(float v) { return seg_sum(v, 64); }
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kDppMirror>(v));
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
 // Total-order key of an f32 (Rust f32::total_cmp): larger key = larger value.

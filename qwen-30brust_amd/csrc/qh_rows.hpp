@@ -103,4 +103,17 @@ __device__ __forceinline__ void rows_dot(RowSel rowsel, const RowGeo& g, const f
     default: break;                                                                   \
     }
 
+// The same over the block-quantised kinds only (compact register tiles).
+#define QH_DISPATCH_QUANT(kind, ...)                                                  \
+    switch (kind) {                                                                   \
+    case ::qh::Q4_0: { constexpr uint32_t K_ = ::qh::Q4_0; __VA_ARGS__; } break;      \
+    case ::qh::Q8_0: { constexpr uint32_t K_ = ::qh::Q8_0; __VA_ARGS__; } break;      \
+    case ::qh::Q4_K: { constexpr uint32_t K_ = ::qh::Q4_K; __VA_ARGS__; } break;      \
+    case ::qh::Q5_K: { constexpr uint32_t K_ = ::qh::Q5_K; __VA_ARGS__; } break;      \
+    case ::qh::Q6_K: { constexpr uint32_t K_ = ::qh::Q6_K; __VA_ARGS__; } break;      \
+    default: break;                                                                   \
+    }
+
+QH_HD bool is_quant(uint32_t kind) { return kind == Q4_0 || kind == Q8_0 || kind == Q4_K || kind == Q5_K || kind == Q6_K; }
+
 }  // namespace qh
