@@ -81,6 +81,19 @@ def matvec_cases(engine, synth, dev):
     return out
 
 
+def measured_traffic(kernel_class):
+    """HBM bytes per launch of a step kernel class (reads + writes), from the
+    committed rocprofv3 PMC summary (FETCH_SIZE / WRITE_SIZE passes scaled by
+    a copy of known size); None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_decode_30b.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)["per_launch"][kernel_class]
+        return int(d["read_bytes"] + d["write_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(img, spec, threads_nt):
     """The oracle (C restatement of the reference CPU backend) on this host:
     faithful single-thread per-element decode, as backend.rs:41-48.  Sample:
@@ -123,6 +136,9 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-matvec", action="store_true")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="also run one device-to-device copy of this many MiB (a known-size "
+                         "kernel that calibrates HBM byte counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -132,6 +148,15 @@ def main():
         sys.exit(2)
     engine = importlib.import_module("qwen-30brust_amd")
     synth = importlib.import_module("qwen-30brust_amd.synth")
+    if args.copy_mb > 0:
+        import torch
+        n = args.copy_mb << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {n} bytes device to device")
+        del src, dst
 
     ctx = args.prompt + args.warmup + args.steps + args.profile_steps + 8
     spec = synth.qwen30b(layers=args.layers, context=max(4096, ctx))
@@ -192,7 +217,9 @@ def main():
                    "weights": "Q4_K/Q6_K/F32 (Q4_K_M mix), activations and KV FP32",
                    "positions": [pos_start, pos_start + args.warmup + args.steps]},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(dom), "algorithmic_bytes_per_launch": int(per_launch_bytes),
+                     "launch_us": round(per_launch_ms * 1e3, 2)},
         "weights_roofline": {"active_weight_bytes_per_token": int(w_active),
                              "GB_s": round(w_active * tok_s / 1e9, 1),
                              "frac": round(w_active * tok_s / 1e9 / HBM_PEAK_GBS, 4)},
