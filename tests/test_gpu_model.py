@@ -163,3 +163,31 @@ def test_layer_30b_shapes_at_pos_1024(dev, more_bits):
     assert np.array_equal(ids_g, ids_r), margin
     assert np.allclose(w_g, w_r, rtol=1e-5, atol=1e-6)
     assert rel_err(xg, xr) <= REL
+
+
+def test_greedy_30b_token_loop_matches_oracle(dev):
+    """Config 4 token loop: the random-init 48-layer Qwen3-30B-A3B Q4_K_M
+    model, a 32-token uniform random prompt, then 64 greedy tokens chained on
+    the device; the ids must equal the oracle's greedy loop.  The oracle's
+    top-1/top-2 logit margin per step is printed so a flip can be attributed
+    to a near-tie."""
+    threads = min(16, os.cpu_count() or 1)
+    spec = synth.qwen30b(context=256)
+    img = synth.build_image(spec, threads=threads)
+    g = oracle.Gguf(img)
+    om = oracle.Model(g, spec.context, threads=threads)
+    m = engine.Model(img, spec.context, device=dev)
+    prompt = np.random.default_rng(4).integers(0, spec.vocab, 32).astype(np.uint32)
+    got = m.generate(prompt, 64)
+    for t in prompt:
+        ref = om.forward(int(t))
+    ref_ids, margins = [], []
+    for i in range(64):
+        s = np.partition(ref, -2)[-2:]
+        margins.append(float(s[1] - s[0]))
+        ref_ids.append(oracle.greedy(ref))
+        if i + 1 < 64:
+            ref = om.forward(ref_ids[-1])
+        print(f"step {i}: oracle {ref_ids[-1]} device {int(got[i])} margin {margins[-1]:.3e}", flush=True)
+    print(f"smallest top-1/top-2 margin {min(margins):.3e}")
+    assert list(got) == ref_ids
