@@ -158,7 +158,8 @@ def main():
         log(f"calibration copy: {n} bytes device to device")
         del src, dst
 
-    ctx = args.prompt + args.warmup + args.steps + args.profile_steps + 8
+    alt_warmup, alt_steps = 4, 32
+    ctx = args.prompt + args.warmup + args.steps + args.profile_steps + alt_warmup + alt_steps + 8
     spec = synth.qwen30b(layers=args.layers, context=max(4096, ctx))
     threads = min(16, os.cpu_count() or 1)
     t0 = time.time()
@@ -180,19 +181,33 @@ def main():
     tok_s = 1000.0 / ms_per_step
     log(f"decode: {ms_per_step:.3f} ms/token, {tok_s:.1f} tok/s")
 
+    persistent = model.persistent
     pos_mid = pos_start + args.warmup + args.steps
+    # the per-phase kernels: timed as a second line, and profiled one kernel
+    # class at a time (HIP events between direct launches)
+    model.persistent = False
+    ms_alt = model.bench_decode(alt_warmup, alt_steps) / alt_steps
+    log(f"per-phase kernels: {ms_alt:.3f} ms/token, {1000.0/ms_alt:.1f} tok/s")
     breakdown = model.profile_step(args.profile_steps)
+    model.persistent = persistent
     bytes_cls = algorithmic_bytes(model, pos_mid + args.profile_steps / 2)
     classes = {}
     for k, v in breakdown.items():
         gbs = bytes_cls[k] / (v * 1e-3) / 1e9 if v > 0 else 0.0
         classes[k] = {"ms_per_token": round(v, 4), "bytes_per_token": int(bytes_cls[k]), "GB_s": round(gbs, 1)}
-    dom = max(breakdown, key=breakdown.get)
-    launches = 1 if dom in ("vocab", "finish") else args.layers
-    per_launch_bytes = bytes_cls[dom] / launches
-    per_launch_ms = breakdown[dom] / launches
+    if persistent:
+        # one k_decode launch (plus the 1-WG embedding kernel) per token: its
+        # algorithmic bytes are the whole token's (weights + KV + activations)
+        dom = "decode_step"
+        per_launch_bytes = sum(bytes_cls.values())
+        per_launch_ms = ms_per_step
+    else:
+        dom = max(breakdown, key=breakdown.get)
+        launches = 1 if dom in ("vocab", "finish") else args.layers
+        per_launch_bytes = bytes_cls[dom] / launches
+        per_launch_ms = breakdown[dom] / launches
     achieved = per_launch_bytes / (per_launch_ms * 1e-3) / 1e9
-    log(f"dominant kernel class {dom}: {per_launch_ms*1e3:.1f} us/launch, {achieved:.0f} GB/s")
+    log(f"dominant kernel {dom}: {per_launch_ms*1e3:.1f} us/launch, {achieved:.0f} GB/s")
 
     w_active = sum(bytes_cls[k] for k in ("qkv", "oproj", "gateup", "down", "vocab"))
     matvec = [] if args.no_matvec else matvec_cases(engine, synth, dev)
@@ -223,7 +238,9 @@ def main():
         "weights_roofline": {"active_weight_bytes_per_token": int(w_active),
                              "GB_s": round(w_active * tok_s / 1e9, 1),
                              "frac": round(w_active * tok_s / 1e9 / HBM_PEAK_GBS, 4)},
-        "step_breakdown": classes,
+        "step": "persistent k_decode (one launch per token)" if persistent else "per-phase kernels",
+        "per_phase_kernels": {"ms_per_token": round(ms_alt, 4), "tok_s": round(1000.0 / ms_alt, 2),
+                              "breakdown": classes},
         "matvec": matvec,
         "cpu_baseline": cpu,
     }

@@ -130,6 +130,17 @@ int qh_position(const qh_ctx *ctx, size_t *out);
 int qh_layer_forward(qh_ctx *ctx, size_t layer, float *x, size_t pos, const float *kprev,
                      const float *vprev, uint32_t *ids, float *w);
 
+/* Token-step implementation (no counterpart in the reference, whose step is
+ * host-driven): *out = 1 when qh_forward / qh_generate / qh_layer_forward run
+ * the persistent single-launch step (one workgroup per CU, phases handed over
+ * through memory), 0 when they run the per-phase kernels.  The persistent
+ * step covers the Q4_K_M formats at Qwen3-MoE shapes; other models always
+ * use the per-phase kernels. */
+int qh_persistent(const qh_ctx *ctx, int *out);
+/* Selects the implementation for the loaded model (enable = 0: per-phase
+ * kernels).  Enabling fails when the model is not covered. */
+int qh_set_persistent(qh_ctx *ctx, int enable);
+
 /* Benchmark surface: `warmup` untimed then `steps` timed greedy decode steps
  * continuing from the current position, timed with HIP events on the
  * context's stream.  ms_total receives the timed milliseconds. */

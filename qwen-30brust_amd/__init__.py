@@ -73,6 +73,8 @@ _SIGS = {
     "qh_layer_forward": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p,
                                    C.c_void_p, C.c_void_p, C.c_void_p]),
     "qh_bench_decode": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(C.c_double)]),
+    "qh_persistent": (C.c_int, [C.c_void_p, C.POINTER(C.c_int)]),
+    "qh_set_persistent": (C.c_int, [C.c_void_p, C.c_int]),
     "qh_profile_step": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]),
     "qh_bench_matvec": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint32, C.c_size_t,
                                   C.c_size_t, C.c_size_t, C.c_size_t, C.POINTER(C.c_double)]),
@@ -241,6 +243,18 @@ class Model:
         out = np.zeros(len(self.KERNEL_CLASSES), np.float64)
         self.dev._check(lib().qh_profile_step(self.dev.h, steps, _ptr(out), out.size))
         return dict(zip(self.KERNEL_CLASSES, out.tolist()))
+
+    @property
+    def persistent(self):
+        """True when the token step runs as one persistent launch (k_decode)
+        rather than the per-phase kernels."""
+        v = C.c_int()
+        self.dev._check(lib().qh_persistent(self.dev.h, C.byref(v)))
+        return bool(v.value)
+
+    @persistent.setter
+    def persistent(self, enable):
+        self.dev._check(lib().qh_set_persistent(self.dev.h, 1 if enable else 0))
 
     def bench_decode(self, warmup, steps):
         ms = C.c_double()

@@ -41,6 +41,9 @@ template <int C> __global__ void k_gateup(LayerW, Acts, ModelDims, uint32_t);
 template <int C> __global__ void k_down(LayerW, Acts, ModelDims);
 template <int C> __global__ void k_vocab(DevMat, const float*, Acts, ModelDims);
 __global__ void k_finish(Acts, ModelDims, uint32_t);
+// Persistent token step (decode.hip).
+__global__ void k_embed(DevMat, Acts, ModelDims);
+__global__ void k_decode(DecodeArgs);
 }  // namespace qh
 
 using namespace qh;
@@ -161,6 +164,14 @@ struct qh_ctx {
     hipGraphExec_t exec = nullptr;
     bool use_graph = true;  // QH_NO_GRAPH=1: launch the step's kernels directly (profilers)
 
+    // persistent token step (k_decode): one cooperative launch per token
+    bool persist_ok = false;  // the model's formats and shapes are covered
+    bool persist = false;     // and it is enabled (QH_NO_PERSIST=1 or qh_set_persistent(0) disable it)
+    uint32_t nwg = 0;         // workgroups of k_decode (one per CU)
+    uint32_t flag_base = 0;   // phase flags reached by the last launch
+    DevBuf layers_dev, sync_buf;
+    DecodeArgs dargs{};
+
     // launch geometry of the step kernels; per layer the held chunk slots
     // (0 qkv, 1 oproj, 2 gateup, 3 down) and for the vocab projection
     uint32_t g_qkv = 1, g_o = 1, g_gu = 1, g_down = 1, g_vocab = 1;
@@ -183,6 +194,9 @@ struct qh_ctx {
         layers.clear();
         attn.clear();
         acts_buf.release();
+        layers_dev.release();
+        sync_buf.release();
+        persist_ok = persist = false;
         kv.release();
         rope_buf.release();
         loaded = false;
@@ -442,8 +456,87 @@ void capture_graph(qh_ctx* c) {
     HIP_OK(hipGraphInstantiate(&c->exec, c->graph, nullptr, nullptr, 0));
 }
 
+// Whether k_decode covers this model: the Q4_K_M formats (q/k/o/gate/up
+// Q4_K; v/down/vocab Q4_K or Q6_K; F32 router) and the row splits of its
+// phases over one 512-thread workgroup per CU.
+bool persist_supported(const qh_ctx* c, uint32_t nwg) {
+    const ModelDims& d = c->dm;
+    const uint32_t G = d.heads / d.kvheads, NWV = nwg * 8;
+    auto km = [](uint32_t k) { return k == Q4_K || k == Q6_K; };
+    if (!(d.head_dim == 128 && G >= 1 && G <= 8 && d.heads * 128 <= 4096 && d.kvheads * 32 <= nwg)) return false;
+    if (!(d.hidden % 256 == 0 && d.hidden <= 2048 && d.hidden <= 8 * nwg)) return false;
+    if (!(d.experts <= 128 && d.experts + 1 <= nwg && d.top >= 1 && d.top <= 8)) return false;
+    if (!(d.ff % 256 == 0 && (uint64_t)d.top * d.ff <= 3ull * NWV && d.top * (d.ff / 32) <= 192 &&
+          d.top * pad32h(d.ff) <= 8192))
+        return false;
+    if (!km(c->out.kind) || c->out.cols != d.hidden || c->max_chunks > 32 || nwg > kMaxGrid || nwg > 512) return false;
+    for (const LayerW& L : c->layers) {
+        if (!(L.q.kind == Q4_K && L.k.kind == Q4_K && L.o.kind == Q4_K && L.gate.kind == Q4_K &&
+              L.up.kind == Q4_K && km(L.v.kind) && km(L.down.kind) && L.router.kind == F32))
+            return false;
+        if ((uint64_t)L.q.rows + L.k.rows + L.v.rows > 3ull * NWV) return false;
+    }
+    return true;
+}
+
+void setup_persist(qh_ctx* c) {
+    hipDeviceProp_t p;
+    HIP_OK(hipGetDeviceProperties(&p, c->device));
+    int per_cu = 0;
+    HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(k_decode), 512, 0));
+    const uint32_t nwg = (uint32_t)p.multiProcessorCount;
+    c->persist_ok = per_cu >= 1 && persist_supported(c, nwg);
+    const char* np = std::getenv("QH_NO_PERSIST");
+    c->persist = c->persist_ok && !(np && np[0] == '1');
+    if (!c->persist_ok) return;
+    c->nwg = nwg;
+    const ModelDims& d = c->dm;
+    c->layers_dev.alloc(c->layers.size() * sizeof(LayerW));
+    HIP_OK(hipMemcpy(c->layers_dev.p, c->layers.data(), c->layers.size() * sizeof(LayerW), hipMemcpyHostToDevice));
+    // flags [nwg][32] | abort | rlog [E+1] | rpart [nwg][E+1]
+    const size_t flags_b = (size_t)nwg * 32 * 4, rlog_b = (size_t)(d.experts + 1) * 4;
+    const size_t total = flags_b + 256 + (rlog_b + 255) / 256 * 256 + (size_t)nwg * (d.experts + 1) * 4;
+    c->sync_buf.alloc(total);
+    HIP_OK(hipMemset(c->sync_buf.p, 0, total));
+    uint8_t* base = c->sync_buf.as<uint8_t>();
+    DecodeArgs& A = c->dargs;
+    A = DecodeArgs{};
+    A.layers = c->layers_dev.as<const LayerW>();
+    A.emb = c->emb;
+    A.out = c->out;
+    A.onorm = c->onorm;
+    A.a = c->acts;
+    A.dm = c->dm;
+    A.max_chunks = c->max_chunks;
+    A.flags = reinterpret_cast<uint32_t*>(base);
+    A.abort_flag = reinterpret_cast<uint32_t*>(base + flags_b);
+    A.rlog = reinterpret_cast<float*>(base + flags_b + 256);
+    A.rpart = reinterpret_cast<float*>(base + flags_b + 256 + (rlog_b + 255) / 256 * 256);
+    c->flag_base = 0;
+}
+
+// One cooperative launch of k_decode over layers [l0, l1); vocab: also the
+// final norm, vocab projection, argmax and position advance.
+void launch_decode(qh_ctx* c, uint32_t l0, uint32_t l1, bool vocab) {
+    DecodeArgs A = c->dargs;
+    A.base = c->flag_base;
+    A.l0 = l0;
+    A.l1 = l1;
+    A.embed = 0;
+    A.vocab = vocab ? 1u : 0u;
+    c->flag_base += 6 * (l1 - l0) + (vocab ? 2 : 0);
+    void* args[] = {&A};
+    HIP_OK(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_decode), dim3(c->nwg), dim3(512), args, 0,
+                                      c->s));
+}
+
 // One token step: the captured graph, or the same kernels launched directly.
 void launch_step(qh_ctx* c) {
+    if (c->persist) {
+        hipLaunchKernelGGL(k_embed, dim3(1), dim3(kBlock), 0, c->s, c->emb, c->acts, c->dm);
+        launch_decode(c, 0, (uint32_t)c->layers.size(), true);
+        return;
+    }
     if (c->use_graph) {
         HIP_OK(hipGraphLaunch(c->exec, c->s));
     } else {
@@ -541,6 +634,7 @@ void load_image(qh_ctx* c, const uint8_t* data, size_t len, size_t context) {
         c->attn.push_back(a);
     }
     capture_graph(c);
+    setup_persist(c);
     c->loaded = true;
     c->pos = 0;
 }
@@ -576,6 +670,11 @@ void reset_model(qh_ctx* c) {
     if (err & kErrRouter) throw Error("invalid MoE router");
     if (err & kErrLogits) throw Error("nonfinite model output");
     if (err & kErrContext) throw Error("context limit " + std::to_string(c->context) + " reached");
+    if (err & kErrSync) {
+        if (c->persist_ok) HIP_OK(hipMemset(c->dargs.abort_flag, 0, 4));
+        HIP_OK(hipMemset(c->acts.attn_cnt, 0, pad32h(c->dm.kvheads) * 4));
+        throw Error("device synchronisation timed out");
+    }
     throw Error("device step failed");
 }
 
@@ -920,7 +1019,10 @@ int qh_layer_forward(qh_ctx* c, size_t layer, float* x, size_t pos, const float*
             sync(c);  // host staging vectors go out of scope
         }
         put_state(c, (uint32_t)pos, (uint32_t)pos + 1);
-        enqueue_layer(c, layer, false);
+        if (c->persist)
+            launch_decode(c, (uint32_t)layer, (uint32_t)layer + 1, false);
+        else
+            enqueue_layer(c, layer, false);
         HIP_OK(hipGetLastError());
         HIP_OK(hipMemcpyAsync(x, c->acts.x, d.hidden * 4, hipMemcpyDeviceToHost, c->s));
         if (ids) HIP_OK(hipMemcpyAsync(ids, c->acts.ids, d.top * 4, hipMemcpyDeviceToHost, c->s));
@@ -928,6 +1030,21 @@ int qh_layer_forward(qh_ctx* c, size_t layer, float* x, size_t pos, const float*
         DevState st = get_state(c);
         reset_model(c);
         if (st.err) fail_step(c, st.err);
+    });
+}
+
+int qh_persistent(const qh_ctx* c, int* out) {
+    return guarded(const_cast<qh_ctx*>(c), [&] {
+        need_model(const_cast<qh_ctx*>(c));
+        *out = c->persist ? 1 : 0;
+    });
+}
+
+int qh_set_persistent(qh_ctx* c, int enable) {
+    return guarded(c, [&] {
+        need_model(c);
+        if (enable && !c->persist_ok) throw Error("the persistent step does not cover this model");
+        c->persist = enable != 0;
     });
 }
 

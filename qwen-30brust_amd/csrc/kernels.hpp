@@ -35,6 +35,7 @@ enum : uint32_t {
     kErrLogits = 2u,   // non-finite output logits (src/model.rs:296-299)
     kErrToken = 4u,    // token outside vocabulary (src/model.rs:222)
     kErrContext = 8u,  // position beyond the allocated context
+    kErrSync = 16u,    // a cross-workgroup wait of the persistent step timed out
 };
 
 struct LayerW {
@@ -85,6 +86,24 @@ struct AttnArgs {
     uint32_t* counter;  // [kvheads]
     float* out;         // [heads*d]
     uint32_t* err;      // nullable: error bits (kErrContext on a chunk overflow)
+};
+
+// Arguments of the persistent token-step kernel (decode.hip): layers
+// [l0, l1) of one token, optionally preceded by the embedding of tokens[pos]
+// and followed by the vocab projection, argmax and position advance.
+struct DecodeArgs {
+    const LayerW* layers;  // device array, one per layer
+    DevMat emb, out;
+    const float* onorm;
+    Acts a;
+    ModelDims dm;
+    uint32_t max_chunks;   // attention chunks per KV head (<= 32)
+    uint32_t* flags;       // [gridDim.x * 32] per-workgroup phase flags
+    uint32_t* abort_flag;  // set when a wait times out; every wait then returns
+    float* rlog;           // [experts + 1] folded router logits, then the RMS scale
+    float* rpart;          // [gridDim.x][experts + 1] router partial dots + sum of squares
+    uint32_t base;         // flag value before this launch's first phase
+    uint32_t l0, l1, embed, vocab;
 };
 
 }  // namespace qh

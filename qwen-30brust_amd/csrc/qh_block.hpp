@@ -200,4 +200,31 @@ __device__ __forceinline__ void block_best(int32_t& k, uint32_t& i) {
     __syncthreads();
 }
 
+// ------------------------------------------- cross-workgroup data exchange --
+// Workgroups on different XCDs do not share an L2, so data handed from one
+// workgroup to another inside a kernel is written through to memory with
+// system-scope stores and read with loads that bypass the caches (sc0 sc1).
+// A producer waits for its stores (s_waitcnt 0) before publishing a flag or
+// counter; a consumer reads the data only after it has seen the flag.
+__device__ __forceinline__ void st_sys(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void st_sys_u(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ float ld_sys(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ uint32_t ld_sys_u(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+// 16-byte load that bypasses the caches (sc0 sc1).
+__device__ __forceinline__ float4 ld_sys4(__amdgpu_buffer_rsrc_t r, uint32_t off_bytes) {
+    auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off_bytes, 0, 17);
+    return *reinterpret_cast<float4*>(&v);
+}
+
 }  // namespace qh

@@ -455,18 +455,6 @@ constexpr uint32_t kFG = 8;    // most query heads per KV head
 constexpr uint32_t kFQ = 160;  // LDS stride of one query head: 8 parts of 16 dims, padded to 20
 constexpr uint32_t kFP = 36;   // LDS stride of one head's score row
 
-__device__ __forceinline__ void st_sys(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ float ld_sys(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-// 16-byte load that bypasses the (per-XCD, non-coherent) caches: sc0 sc1.
-__device__ __forceinline__ float4 ld_sys4(__amdgpu_buffer_rsrc_t r, uint32_t off_bytes) {
-    auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off_bytes, 0, 17);
-    return *reinterpret_cast<float4*>(&v);
-}
-
 // K and V slices (16 dims at part*16) of key tt + tid/8 of KV head g.
 __device__ __forceinline__ void kv_slice_load(float4 (&kr)[4], float4 (&vr)[4], const float* kc, const float* vc,
                                               uint32_t g, uint32_t ctx, uint32_t tt, uint32_t t1, uint32_t pos) {
@@ -675,7 +663,7 @@ __global__ __launch_bounds__(kBlock) void k_attn128(LayerW L, AttnArgs aa, Acts 
         st_sys(dst + 3, o4.w);
     }
     if (threadIdx.x < 2 * G) st_sys(pml + ((size_t)(g * G + threadIdx.x / 2) * mc + c) * 2 + (threadIdx.x & 1), ml[threadIdx.x]);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the stores above have completed
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's write-through stores have completed
     __syncthreads();
     QH_MARK(1, 4);
     if (threadIdx.x == 0) {

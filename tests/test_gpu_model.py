@@ -137,11 +137,12 @@ def test_generate_matches_stepwise_forward(dev):
     assert np.array_equal(lg, last)
 
 
+@pytest.mark.parametrize("persistent", [True, False])
 @pytest.mark.parametrize("more_bits", [True, False])
-def test_layer_30b_shapes_at_pos_1024(dev, more_bits):
+def test_layer_30b_shapes_at_pos_1024(dev, more_bits, persistent):
     """Config 3: one decoder layer at 30B-A3B shapes, position 1024 with 1024
     pre-filled N(0,1) KV positions; layer 0 types (Q6_K attn_v / down) and a
-    plain Q4_K layer."""
+    plain Q4_K layer; through the persistent step and the per-phase kernels."""
     # a previously loaded model with a different attention tile must not leak
     # its geometry into this one (regression: tile chosen after sizing buffers)
     engine.Model(synth.build_image(synth.tiny_k(), threads=8), 64, device=dev).forward(1)
@@ -150,6 +151,8 @@ def test_layer_30b_shapes_at_pos_1024(dev, more_bits):
     g = oracle.Gguf(img)
     om = oracle.Model(g, spec.context)
     m = engine.Model(img, spec.context, device=dev)
+    m.persistent = persistent
+    assert m.persistent == persistent
     pos, kvd = 1024, spec.kvheads * spec.head_dim
     x = synth.normal(21, spec.hidden)
     kp = synth.normal(22, pos * kvd)
@@ -162,6 +165,32 @@ def test_layer_30b_shapes_at_pos_1024(dev, more_bits):
     print(f"router 8th/9th margin {margin:.3e}")
     assert np.array_equal(ids_g, ids_r), margin
     assert np.allclose(w_g, w_r, rtol=1e-5, atol=1e-6)
+    assert rel_err(xg, xr) <= REL
+
+
+@pytest.fixture(scope="module")
+def layer30b_q4k():
+    spec = synth.layer30b(more_bits=False)
+    img = synth.build_image(spec, threads=8)
+    return spec, img
+
+
+@pytest.mark.parametrize("pos", [0, 1, 31, 32, 33, 200, 700])
+def test_persistent_layer_attention_chunking(dev, layer30b_q4k, pos):
+    """The persistent step at positions that exercise the attention split: one
+    key, one chunk, chunk boundaries (32 keys per chunk), and up to 22
+    chunks merged per KV head; against the oracle layer."""
+    spec, img = layer30b_q4k
+    om = oracle.Model(oracle.Gguf(img), spec.context)
+    m = engine.Model(img, spec.context, device=dev)
+    assert m.persistent
+    kvd = spec.kvheads * spec.head_dim
+    x = synth.normal(31 + pos, spec.hidden)
+    kp = synth.normal(32 + pos, max(pos, 1) * kvd)[: pos * kvd]
+    vp = synth.normal(33 + pos, max(pos, 1) * kvd)[: pos * kvd]
+    xr, ids_r, _ = om.layer_forward(0, x, pos, kp, vp)
+    xg, ids_g, _ = m.layer_forward(0, x, pos, kp, vp)
+    assert np.array_equal(ids_g, ids_r)
     assert rel_err(xg, xr) <= REL
 
 
