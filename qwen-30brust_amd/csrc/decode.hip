@@ -79,6 +79,17 @@ struct Ctx {
     uint32_t r0, nr;  // this workgroup's rows of x
 };
 
+// A copy of the launch constants whose per-lane fields are opaque to the
+// optimiser: values derived from them inside a phase cannot be hoisted out of
+// the layer loop, so each phase recomputes its few index expressions instead
+// of every phase's indices staying live in registers for the whole kernel.
+__device__ __forceinline__ Ctx fresh(const Ctx& c0) {
+    Ctx c = c0;
+    asm volatile("" : "+v"(c.tid));
+    asm volatile("" : "+v"(c.lane));
+    return c;
+}
+
 __device__ __forceinline__ float dsum(float v, float* red) {
     v = wave_sum(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
@@ -145,8 +156,9 @@ __device__ __forceinline__ float4 load_norm_x(const Ctx& c, const float* x, floa
 // Flat rows [q | k | v]; wave gw owns rows gw, gw + NWV, gw + 2 NWV.  q and k
 // share format KQ, v has KV.  Rows have H <= 2048 columns: lane = chunk.
 template <uint32_t KQ, uint32_t KV>
-__device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c,
+__device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
                                           bool wait_x, uint32_t& ph) {
+    const Ctx c = fresh(c0);
     const uint32_t nq = L.q.rows, nk = L.k.rows, nt = nq + nk + L.v.rows, cpr = c.H / 32;
     typename Fmt<KQ>::Raw wq[kQkvPerWave];
     typename Fmt<KV>::Raw wvv[kQkvPerWave];
@@ -162,7 +174,9 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
     }
     float4 nw = make_float4(0.f, 0.f, 0.f, 0.f);
     if (4 * c.tid < c.H) nw = reinterpret_cast<const float4*>(L.attn_norm)[c.tid];
+    QH_MARK(0, 0);
     if (wait_x && !wait_all(A, S, ph)) return false;  // x of the previous layer (phase F)
+    QH_MARK(0, 1);
     float* xs = S.big;
     const float4 xv = load_norm_x(c, A.a.x, nw, A.dm.eps, xs, S.red);
     // this workgroup's residual rows, kept in LDS through the layer
@@ -195,6 +209,7 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
             if (c.lane == 0) st_sys(out, acc);
         }
     }
+    QH_MARK(0, 2);
     signal(A, ++ph);
     return true;
 }
@@ -216,8 +231,9 @@ __device__ __forceinline__ void kv_slice(float4 (&kr)[4], float4 (&vr)[4], const
     }
 }
 
-__device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c,
+__device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
                                            uint32_t& ph) {
+    const Ctx c = fresh(c0);
     const Acts& a = A.a;
     const ModelDims& dm = A.dm;
     const uint32_t nch = min((c.T + 31) / 32, A.max_chunks);
@@ -237,7 +253,9 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
     const float qw0 = L.q_norm[lane], qw1 = L.q_norm[lane + 64];
     const float kw0 = L.k_norm[lane], kw1 = L.k_norm[lane + 64];
     const float2 cs = a.rope[(size_t)pos * 64 + lane];
+    QH_MARK(1, 0);
     if (!wait_all(A, S, ph)) return false;  // q/k/v (phase A)
+    QH_MARK(1, 1);
     float* qs = S.big;              // [8][160]  normalised, rotated queries (parts padded to 20)
     float* kn = qs + 8 * 160;       // [160]     new key, same layout
     float* vn = kn + 160;           // [128]     new value
@@ -270,6 +288,7 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
             L.kcache[((size_t)g * ctx + pos) * 128 + lane + 64] = o1;
         }
     }
+    QH_MARK(1, 4);
     if (tid < 32) {
         const float* vsrc = a.v + g * 128 + 4 * tid;
         const float4 v4 = make_float4(ld_sys(vsrc), ld_sys(vsrc + 1), ld_sys(vsrc + 2), ld_sys(vsrc + 3));
@@ -277,6 +296,7 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
         if (holds) reinterpret_cast<float4*>(L.vcache + ((size_t)g * ctx + pos) * 128)[tid] = v4;
     }
     __syncthreads();
+    QH_MARK(1, 5);
     const float root = sqrtf(128.0f);
     float mh = -INFINITY, lh = 0.f;               // head wv (softmax wave)
     float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);  // threads < 256: head tid/32, dims 4*(tid%32)
@@ -354,6 +374,7 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
         ml[wv * 2 + 1] = lh;
     }
     __syncthreads();
+    QH_MARK(1, 2);
     if (nch == 1) {
         if (wv < 4 && hq < G) {
             const float inv = 1.0f / ml[hq * 2 + 1];
@@ -436,6 +457,7 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
         st_sys(out + 2, O.z * inv);
         st_sys(out + 3, O.w * inv);
     }
+    QH_MARK(1, 3);
     signal(A, ++ph);
     return true;
 }
@@ -443,8 +465,9 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
 // ======================================================== C: o-projection ==
 // Wave wv owns row r0 + wv (qd <= 4096 columns: chunks lane, lane + 64).
 template <uint32_t KO>
-__device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c,
+__device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
                                             uint32_t& ph) {
+    const Ctx c = fresh(c0);
     const uint32_t ocpr = c.qd / 32, E = c.E;
     typename Fmt<KO>::Raw w0, w1;
     const bool rowok = c.wv < c.nr;
@@ -463,7 +486,9 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
         if (2 * q + 1 < c.nr) rw1 = wr[2 * q + 1];
     }
     if (c.tid < c.nr) S.wn[c.tid] = L.ffn_norm[c.r0 + c.tid];
+    QH_MARK(2, 0);
     if (!wait_all(A, S, ph)) return false;  // attention output (phase B)
+    QH_MARK(2, 1);
     float* xs = S.big;
     {
         const __amdgpu_buffer_rsrc_t ar = buf_rsrc(A.a.attn, c.qd * 4);
@@ -501,6 +526,7 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
         v = wave_sum(v);
         if (c.lane == 0) st_sys(A.rpart + (size_t)c.b * c.E1 + E, v);
     }
+    QH_MARK(2, 2);
     signal(A, ++ph);
     return true;
 }
@@ -508,9 +534,12 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
 // ========================================================== D: router fold ==
 // Workgroup e <= E folds column e (and the sum of squares) over the partial
 // rows of every workgroup, in one fixed order.
-__device__ __forceinline__ bool phase_fold(const DecodeArgs& A, DecodeLds& S, const Ctx& c, uint32_t& ph) {
+__device__ __forceinline__ bool phase_fold(const DecodeArgs& A, DecodeLds& S, const Ctx& c0, uint32_t& ph) {
+    const Ctx c = fresh(c0);
     if (c.b < c.E1) {
+        QH_MARK(3, 0);
         if (!wait_all(A, S, ph)) return false;  // router partials (phase C)
+        QH_MARK(3, 1);
         float v = 0.f, vs = 0.f;
         if (c.tid < c.nwg) {
             v = ld_sys(A.rpart + (size_t)c.tid * c.E1 + c.b);
@@ -522,6 +551,7 @@ __device__ __forceinline__ bool phase_fold(const DecodeArgs& A, DecodeLds& S, co
             const float s = 1.0f / sqrtf(fsq / (float)c.H + A.dm.eps);
             st_sys(A.rlog + c.b, c.b < c.E ? s * fold : s);
         }
+        QH_MARK(3, 2);
     }
     signal(A, ++ph);
     return true;
@@ -529,13 +559,16 @@ __device__ __forceinline__ bool phase_fold(const DecodeArgs& A, DecodeLds& S, co
 
 // ============================================== E + F: routed expert FFN ==
 template <uint32_t KG, uint32_t KD>
-__device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c,
+__device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
                                           uint32_t& ph) {
+    const Ctx c = fresh(c0);
     const Acts& a = A.a;
     const uint32_t E = c.E, top = c.top, ff = c.ff, fp = c.fp, H = c.H, cpr = H / 32;
     float4 fn = make_float4(0.f, 0.f, 0.f, 0.f);
     if (4 * c.tid < H) fn = reinterpret_cast<const float4*>(L.ffn_norm)[c.tid];
+    QH_MARK(4, 0);
     if (!wait_all(A, S, ph)) return false;  // folded logits (phase D)
+    QH_MARK(4, 1);
     if (c.tid <= E) S.lg[c.tid] = ld_sys(A.rlog + c.tid);
     float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
     if (4 * c.tid < H) xv = ld_sys4(buf_rsrc(a.x, H * 4), c.tid * 16);
@@ -585,6 +618,7 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         for (uint32_t i = 0; i < top; i++) sum += S.ex[i];
         S.wts[c.tid] = S.ex[c.tid] / sum;
     }
+    QH_MARK(4, 2);
     // gate/up rows of pairs p = gw*3 + k: (slot p / ff, row p % ff)
     typename Fmt<KG>::Raw wg[kPairsPerWave], wu[kPairsPerWave];
 #pragma unroll
@@ -614,6 +648,7 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         }
         if (c.tid < E) a.logits_r[c.tid] = S.lg[c.tid];
     }
+    QH_MARK(4, 4);
     {
         float xa[16], xb[16], sa, sb;
         if (c.lane < cpr) x_runs<KG>(xs, c.lane, xa, xb, sa, sb);
@@ -636,6 +671,7 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
             }
         }
     }
+    QH_MARK(4, 5);
     // down rows of phase F (row r0 + wv of each routed expert), requested
     // before the wait: lane units u = lane + 64 i = (slot u / dcpr, chunk u % dcpr)
     const uint32_t dcpr = ff / 32, U = top * dcpr;
@@ -649,14 +685,18 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
             wd[i] = Fmt<KD>::load(drow, L.down.geo, u % dcpr);
         }
     }
+    QH_MARK(4, 3);
     signal(A, ++ph);
+    QH_MARK(5, 0);
     if (!wait_all(A, S, ph)) return false;  // SwiGLU outputs (phase E)
+    QH_MARK(5, 1);
     {
         const uint32_t nh = top * fp;
         const __amdgpu_buffer_rsrc_t hr = buf_rsrc(a.h, nh * 4);
         for (uint32_t i = c.tid; i < nh / 4; i += kDT) reinterpret_cast<float4*>(xs)[i] = ld_sys4(hr, i * 16);
     }
     __syncthreads();
+    QH_MARK(5, 3);
     if (c.wv < c.nr) {  // wave-uniform
         float acc = 0.f;
 #pragma unroll
@@ -676,13 +716,15 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
             st_sys(a.x + c.r0 + c.wv, xn);
         }
     }
+    QH_MARK(5, 2);
     signal(A, ++ph);
     return true;
 }
 
 // =========================================================== V: vocab ==
 template <uint32_t KV>
-__device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, const Ctx& c, uint32_t& ph) {
+__device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, const Ctx& c0, uint32_t& ph) {
+    const Ctx c = fresh(c0);
     const Acts& a = A.a;
     const DevMat& mv = A.out;
     const uint32_t V = A.dm.vocab, ngrp = (V + kVocabRows - 1) / kVocabRows, cpr = c.H / 32;
@@ -698,7 +740,9 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
     load_group(cur, c.gw);
     float4 on = make_float4(0.f, 0.f, 0.f, 0.f);
     if (4 * c.tid < c.H) on = reinterpret_cast<const float4*>(A.onorm)[c.tid];
+    QH_MARK(6, 0);
     if (!wait_all(A, S, ph)) return;  // x after the last layer
+    QH_MARK(6, 1);
     float* xs = S.big;
     load_norm_x(c, a.x, on, A.dm.eps, xs, S.red);
     float xa[16], xb[16], sa, sb;
@@ -728,6 +772,7 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
 #pragma unroll
         for (uint32_t k = 0; k < kVocabRows; k++) cur[k] = nxt[k];
     }
+    QH_MARK(6, 2);
     if (nf) S.bad = 1;
     wave_best(bk, bi);
     if (c.lane == 0) {
@@ -766,6 +811,7 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
         if (c.pos + 1 >= a.st->n_given && c.pos + 1 <= A.dm.ctx) a.tokens[c.pos + 1] = i0;
         a.st->pos = c.pos + 1;
     }
+    QH_MARK(6, 3);
 }
 
 // ================================================================= kernels ==

@@ -146,7 +146,9 @@ template <> struct Fmt<Q5_K> {
 
 // -------------------------------------------------------------------- Q6_K --
 template <> struct Fmt<Q6_K> {
-    struct Raw { uint4 ql, qh; uint32_t sc, d; };
+    // ql, qh of the chunk; the 8 scale bytes of its half-block (selected in
+    // dot(), so that load() only issues loads); d
+    struct Raw { uint4 ql, qh; uint2 s8; uint32_t d; };
     static __device__ __forceinline__ uint32_t xoff_a(uint32_t c) {
         uint32_t j = c & 7;
         return (c >> 3) * 256 + (j >> 2) * 128 + ((j & 3) >> 1) * 32 + (j & 1) * 16;
@@ -154,19 +156,19 @@ template <> struct Fmt<Q6_K> {
     static __device__ __forceinline__ uint32_t xoff_b(uint32_t c) { return xoff_a(c) + 64; }
     static __device__ __forceinline__ Raw load(const uint8_t* row, const RowGeo& g, uint32_t c) {
         uint32_t b = c >> 3, j = c & 7;
-        // scales of this chunk: sc[(j>>2)*8 + qa*2 + (j&1)] (quarter qa) and +4
-        // (quarter qa+2); the 8 bytes of half j>>2 arrive as one 8-byte load
-        const uint2 s8 = *reinterpret_cast<const uint2*>(row + g.off_c + b * 16 + (j >> 2) * 8);
-        const uint32_t sh = (((j & 3) >> 1) * 2 + (j & 1)) * 8;
-        const uint32_t sc = ((s8.x >> sh) & 0xffu) | (((s8.y >> sh) & 0xffu) << 8);
         return {ld16(row + g.off_a + b * 128 + j * 16),
-                ld16(row + g.off_b + b * 64 + (j >> 2) * 32 + (j & 1) * 16), sc,
+                ld16(row + g.off_b + b * 64 + (j >> 2) * 32 + (j & 1) * 16),
+                *reinterpret_cast<const uint2*>(row + g.off_c + b * 16 + (j >> 2) * 8),
                 ld_u16(row + g.off_d + b * 2)};
     }
     static __device__ __forceinline__ float dot(const Raw& r, uint32_t c, const float* xa,
                                                 const float* xb, float sa, float sb) {
+        // scales of this chunk: sc[(j>>2)*8 + qa*2 + (j&1)] (quarter qa) and +4
+        // (quarter qa+2), bytes sh/8 of the two words of s8
+        const uint32_t jj = c & 7, sh = (((jj & 3) >> 1) * 2 + (jj & 1)) * 8;
+        const uint32_t rsc = ((r.s8.x >> sh) & 0xffu) | (((r.s8.y >> sh) & 0xffu) << 8);
         uint32_t j = c & 7, qa = (j & 3) >> 1;
-        float sca = (float)(int8_t)(r.sc & 0xffu), scb = (float)(int8_t)(r.sc >> 8);
+        float sca = (float)(int8_t)(rsc & 0xffu), scb = (float)(int8_t)(rsc >> 8);
         float d = h2f(r.d);
         uint32_t l[4] = {r.ql.x, r.ql.y, r.ql.z, r.ql.w};
         uint32_t h[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
