@@ -2,32 +2,40 @@
 // src/sampling.rs:26-35) as ONE launch of one 512-thread workgroup per CU,
 // preceded by k_embed (the embedding row of tokens[pos], model.rs:225).
 //
-// The workgroups run six phases per layer and hand data to each other
-// through memory instead of through kernel boundaries:
+// Per layer the workgroups run six phases:
 //   A  RMSNorm + q/k/v projections
-//   B  Q/K RMSNorm, RoPE, KV append, split-T GQA attention, chunk merge
-//   C  output projection + residual for this workgroup's rows of x, and the
-//      router partial dots over those rows
-//   D  router fold: workgroup e folds logit e over all partial rows
+//   B  Q/K RMSNorm, RoPE, KV append, split-T GQA attention; chunk 0 of each
+//      KV head merges the other chunks' partials
+//   C  output projection + residual for this workgroup's rows of x
+//   D  every workgroup reads all of x' and its RMS scale; workgroup e < E
+//      computes router logit e
 //   E  top-k routing (every workgroup, identically), gate/up + SwiGLU rows
 //   F  down projections + routing-weighted combine + residual, own rows
 // then V: final RMSNorm, vocab projection and argmax partials, and the
 // argmax / next token / position advance by workgroup 0.
 //
-// Synchronisation: after a phase a workgroup waits for its own
-// write-through stores and publishes flags[b] = base + phase; a workgroup that
-// needs phase p polls every flag until it reaches base + p.  Before it polls,
-// a workgroup issues every load that does not depend on the awaited phase --
-// the weights it will use next, norm vectors, the KV history, and once the
-// routing is known the down-projection rows -- so their latency overlaps the
-// wait.  Each wait is bounded: on timeout the workgroup raises abort_flag
-// and every other wait returns, so the grid always drains.
+// Hand-over without flags or barriers: every value one workgroup passes to
+// another is a 64-bit word (tag << 32) | bits written through to memory with
+// a system-scope store, where tag = base + the number of the writing phase
+// (6 per layer, 1 for V; base grows by the launch's phase count, so tags
+// never repeat between launches).  A reader polls exactly the words it needs
+// until each carries the tag it expects: a phase starts as soon as its own
+// inputs exist, and no producer waits for its stores to complete.  Before it
+// polls, a workgroup issues every load that does not depend on the awaited
+// words (its next weights, norm vectors, the KV history, and once the routing
+// is known the down-projection rows).  Every wait is bounded: on timeout the
+// workgroup raises abort_flag and every other wait returns, so the grid
+// always drains.
+//
+// Reuse of a buffer in the next layer is safe without any barrier: every
+// workgroup owns rows of x (the host checks it), so a workgroup that has read
+// all of x'' (or x') of layer l knows every workgroup has finished phase F
+// (or C) of layer l, and with it every read of the buffers it overwrites next.
 //
 // Each phase body is instantiated for the formats of the Q4_K_M mix (q, k,
 // o, gate, up: Q4_K; v, down, vocab: Q4_K or Q6_K) and selected once per
-// phase, so a wave's register tiles have the exact chunk size.  The host
-// launches this path only for models and shapes it covers (engine.hip:
-// persist_supported); everything else runs the per-phase kernels.
+// phase.  The host launches this path only for models and shapes it covers
+// (engine.hip: persist_supported); everything else runs the per-phase kernels.
 #include "qh_block.hpp"
 #include "qh_tile.hpp"
 
@@ -35,15 +43,16 @@ namespace qh {
 
 constexpr int kDT = 512;
 constexpr int kDW = kDT / 64;
-constexpr uint32_t kFlagStride = 32;        // flags 128 bytes apart
 constexpr uint32_t kSpinLimit = 1u << 22;   // polls before a wait gives up
 constexpr uint32_t kDChunks = 32;           // most attention chunk workgroups per KV head
-constexpr uint32_t kDTile = 32;             // keys per attention tile
-constexpr uint32_t kDSmem = 8192;           // floats of phase scratch
+constexpr uint32_t kDTile = 64;             // keys per attention tile (and at least per chunk)
+constexpr uint32_t kDSmem = 11264;          // floats of phase scratch
 constexpr uint32_t kQkvPerWave = 3;         // q/k/v rows per wave
 constexpr uint32_t kPairsPerWave = 3;       // gate/up row pairs per wave
+constexpr uint32_t kHBlock = kPairsPerWave * kDW;  // SwiGLU outputs per workgroup
 constexpr uint32_t kDownUnits = 3;          // (expert, chunk) units per lane in F
 constexpr uint32_t kVocabRows = 4;          // vocab rows per wave group
+constexpr uint32_t kGatherPairs = 6;        // word pairs in flight per thread in a gather
 
 // Formats of the Q4_K_M mix; the host routes other models to the per-phase
 // kernels.
@@ -57,9 +66,9 @@ struct DecodeLds {
     long long ck[256];        // composite top-k keys
     float big[kDSmem];        // phase scratch (x, attention tiles, h)
     float xo[8];              // this workgroup's rows of the residual stream
-    float wn[8];              // ffn_norm of those rows
-    float red[kDW];
-    float lg[256];            // router logits, then [E] = RMS scale
+    float hv[kHBlock];        // this workgroup's SwiGLU outputs
+    float red[2 * kDW];
+    float lg[256];            // router logits
     float sv[8];
     uint32_t sid[8];
     float ex[8];
@@ -68,15 +77,14 @@ struct DecodeLds {
     int32_t bk[kDW];
     uint32_t bi[kDW];
     uint32_t abort;
-    uint32_t last;
     uint32_t bad;
 };
 
 // Per-workgroup constants of one launch.
 struct Ctx {
     uint32_t b, nwg, tid, wv, lane, gw, NWV;
-    uint32_t pos, T, H, E, E1, top, ff, fp, G, qd, ctx;
-    uint32_t r0, nr;  // this workgroup's rows of x
+    uint32_t pos, T, H, E, top, ff, G, qd, kvd, ctx;
+    uint32_t r0, nr, rpw;  // this workgroup's rows of x: [r0, r0 + nr), rpw per workgroup
 };
 
 // A copy of the launch constants whose per-lane fields are opaque to the
@@ -90,6 +98,152 @@ __device__ __forceinline__ Ctx fresh(const Ctx& c0) {
     return c;
 }
 
+// ------------------------------------------------------------ tagged words --
+__device__ __forceinline__ void put(uint64_t* p, float v, uint32_t tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ uint64_t ld_word(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Bookkeeping of one poll round: every 64th round checks the abort flag and
+// the time limit (on timeout raises the abort flag and kErrSync).  False when
+// the wait must stop (ab = true).
+__device__ __forceinline__ bool keep_polling(const DecodeArgs& A, uint32_t& spins, bool& ab) {
+    if ((++spins & 63) == 0) {
+        if (ld_sys_u(A.abort_flag) != 0) {
+            ab = true;
+            return false;
+        }
+        if (spins > kSpinLimit) {
+            st_sys_u(A.abort_flag, 1u);
+            atomicOr(&A.a.st->err, kErrSync);
+            ab = true;
+            return false;
+        }
+    }
+    __builtin_amdgcn_s_sleep(1);
+    return true;
+}
+
+__device__ __forceinline__ bool has_tag(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
+
+// Two adjacent words (16 bytes, 16-byte aligned) read past the caches.
+__device__ __forceinline__ void ld_pair(__amdgpu_buffer_rsrc_t r, uint32_t word, uint64_t& w0, uint64_t& w1) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(word * 8), 0, 17);
+    w0 = ((uint64_t)(uint32_t)v[1] << 32) | (uint32_t)v[0];
+    w1 = ((uint64_t)(uint32_t)v[3] << 32) | (uint32_t)v[2];
+}
+
+// Waits for N word pairs at once: pair k (words word[k], word[k] + 1 of r)
+// is awaited when bit k of need is set, its second word only when bit k of
+// hi is set too.  Every round re-reads all pairs still missing with one batch
+// of loads, so a wait costs one memory round trip per round however many
+// words it covers.  v[2k], v[2k + 1] receive the values.
+template <uint32_t N>
+__device__ __forceinline__ void poll_pairs(const DecodeArgs& A, __amdgpu_buffer_rsrc_t r, const uint32_t (&word)[N],
+                                           uint32_t need, uint32_t hi, uint32_t tag, float (&v)[2 * N], bool& ab) {
+    uint32_t spins = 0;
+    while (need != 0) {
+        uint64_t w[2 * N];
+#pragma unroll
+        for (uint32_t k = 0; k < N; k++)
+            if ((need >> k) & 1) ld_pair(r, word[k], w[2 * k], w[2 * k + 1]);
+#pragma unroll
+        for (uint32_t k = 0; k < N; k++) {
+            if (((need >> k) & 1) && has_tag(w[2 * k], tag) && (!((hi >> k) & 1) || has_tag(w[2 * k + 1], tag))) {
+                v[2 * k] = __uint_as_float((uint32_t)w[2 * k]);
+                v[2 * k + 1] = __uint_as_float((uint32_t)w[2 * k + 1]);
+                need &= ~(1u << k);
+            }
+        }
+        if (need == 0 || !keep_polling(A, spins, ab)) break;
+    }
+}
+
+// The same for N single words base[idx[k]].
+template <uint32_t N>
+__device__ __forceinline__ void poll_words(const DecodeArgs& A, const uint64_t* base, const uint32_t (&idx)[N],
+                                           uint32_t need, uint32_t tag, float (&v)[N], bool& ab) {
+    uint32_t spins = 0;
+    while (need != 0) {
+        uint64_t w[N];
+#pragma unroll
+        for (uint32_t k = 0; k < N; k++)
+            if ((need >> k) & 1) w[k] = __hip_atomic_load(base + idx[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+#pragma unroll
+        for (uint32_t k = 0; k < N; k++) {
+            if (((need >> k) & 1) && has_tag(w[k], tag)) {
+                v[k] = __uint_as_float((uint32_t)w[k]);
+                need &= ~(1u << k);
+            }
+        }
+        if (need == 0 || !keep_polling(A, spins, ab)) break;
+    }
+}
+
+// dst[i] = value of src[i] for i < n, every word awaited with `tag` (src is
+// 16-byte aligned with room for an even number of words).  Ends with a
+// barrier; false when the step was aborted.
+__device__ __forceinline__ bool gather(const DecodeArgs& A, DecodeLds& S, const uint64_t* src, uint32_t n,
+                                       uint32_t tag, float* dst, uint32_t tid) {
+    const uint32_t np = (n + 1) / 2;
+    const __amdgpu_buffer_rsrc_t r = buf_rsrc(src, np * 16);
+    bool ab = false;
+    for (uint32_t p0 = tid; p0 < np; p0 += kGatherPairs * kDT) {
+        uint32_t word[kGatherPairs], need = 0, hi = 0;
+#pragma unroll
+        for (uint32_t k = 0; k < kGatherPairs; k++) {
+            const uint32_t p = p0 + k * kDT;
+            word[k] = 2 * p;
+            if (p < np) need |= 1u << k;
+            if (2 * p + 1 < n) hi |= 1u << k;
+        }
+        float v[2 * kGatherPairs];
+        poll_pairs<kGatherPairs>(A, r, word, need, hi, tag, v, ab);
+        if (ab) break;
+#pragma unroll
+        for (uint32_t k = 0; k < kGatherPairs; k++) {
+            const uint32_t p = p0 + k * kDT;
+            if (p < np) dst[2 * p] = v[2 * k];
+            if (2 * p + 1 < n) dst[2 * p + 1] = v[2 * k + 1];
+        }
+    }
+    if (ab) S.abort = 1;
+    __syncthreads();
+    return S.abort == 0;
+}
+
+// gather() preceded by a cheap readiness check: wave 0 first polls ns sample
+// words src[first + j * stride] (one per producer block, each block written
+// by one store instruction), and only then does the workgroup read all n
+// words.  A workgroup that waits long (for attention, say) thus polls a few
+// hundred bytes per round instead of the whole vector, so waiting workgroups
+// do not flood the memory channels that the producers are using.
+__device__ __forceinline__ bool gather_s(const DecodeArgs& A, DecodeLds& S, const uint64_t* src, uint32_t n,
+                                         uint32_t tag, float* dst, uint32_t tid, uint32_t ns, uint32_t first,
+                                         uint32_t stride) {
+    if (tid < 64) {
+        bool ab = false;
+        for (uint32_t j0 = 0; j0 < ns && !ab; j0 += 256) {
+            uint32_t idx[4], need = 0;
+#pragma unroll
+            for (uint32_t k = 0; k < 4; k++) {
+                const uint32_t j = j0 + tid + 64 * k;
+                idx[k] = first + j * stride;
+                if (j < ns) need |= 1u << k;
+            }
+            float v[4];
+            poll_words<4>(A, src, idx, need, tag, v, ab);
+        }
+        if (ab) S.abort = 1;
+    }
+    __syncthreads();
+    if (S.abort) return false;
+    return gather(A, S, src, n, tag, dst, tid);
+}
+
 __device__ __forceinline__ float dsum(float v, float* red) {
     v = wave_sum(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
@@ -100,48 +254,33 @@ __device__ __forceinline__ float dsum(float v, float* red) {
     __syncthreads();
     return s;
 }
-
-// Publishes "phase value done" for this workgroup.
-__device__ __forceinline__ void signal(const DecodeArgs& A, uint32_t value) {
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's write-through stores have completed
-    __syncthreads();
-    if (threadIdx.x == 0) st_sys_u(A.flags + blockIdx.x * kFlagStride, value);
-}
-
-// Waits until every workgroup has published `value`; false when the step was
-// aborted (a wait timed out somewhere).
-__device__ __forceinline__ bool wait_all(const DecodeArgs& A, DecodeLds& S, uint32_t value) {
-    if (threadIdx.x < gridDim.x) {
-        const uint32_t* f = A.flags + threadIdx.x * kFlagStride;
-        uint32_t spins = 0;
-        while ((int32_t)(ld_sys_u(f) - value) < 0) {
-            if ((++spins & 63) == 0) {
-                if (ld_sys_u(A.abort_flag) != 0) {
-                    S.abort = 1;
-                    break;
-                }
-                if (spins > kSpinLimit) {
-                    st_sys_u(A.abort_flag, 1u);
-                    atomicOr(&A.a.st->err, kErrSync);
-                    S.abort = 1;
-                    break;
-                }
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
+// Two block sums in one round.
+__device__ __forceinline__ float2 dsum2(float u, float v, float* red) {
+    u = wave_sum(u);
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) {
+        red[threadIdx.x >> 6] = u;
+        red[kDW + (threadIdx.x >> 6)] = v;
     }
     __syncthreads();
-    return S.abort == 0;
+    float su = 0.f, sv = 0.f;
+#pragma unroll
+    for (int i = 0; i < kDW; i++) {
+        su += red[i];
+        sv += red[kDW + i];
+    }
+    __syncthreads();
+    return make_float2(su, sv);
 }
 
-// x (H floats, written through) into LDS as RMSNorm(x) * w; returns this
-// thread's raw float4 of x.  H <= 2048: one float4 per thread.
-__device__ __forceinline__ float4 load_norm_x(const Ctx& c, const float* x, float4 w, float eps, float* xs,
-                                             float* red) {
+__device__ __forceinline__ float sumsq4(float4 v) { return fmaf(v.w, v.w, fmaf(v.z, v.z, fmaf(v.y, v.y, v.x * v.x))); }
+
+// RMSNorm (ops.rs:3-15) of the raw x in LDS xs[0..H), in place, with weights
+// w (this thread's float4); returns this thread's raw float4.  H <= 2048.
+__device__ __forceinline__ float4 norm_in_lds(const Ctx& c, float* xs, float4 w, float eps, float* red) {
     float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (4 * c.tid < c.H) xv = ld_sys4(buf_rsrc(x, c.H * 4), c.tid * 16);
-    const float ss = dsum(fmaf(xv.w, xv.w, fmaf(xv.z, xv.z, fmaf(xv.y, xv.y, xv.x * xv.x))), red);
-    const float scale = 1.0f / sqrtf(ss / (float)c.H + eps);
+    if (4 * c.tid < c.H) xv = reinterpret_cast<const float4*>(xs)[c.tid];
+    const float scale = 1.0f / sqrtf(dsum(sumsq4(xv), red) / (float)c.H + eps);
     if (4 * c.tid < c.H) {
         xs[4 * c.tid] = xv.x * (scale * w.x);
         xs[4 * c.tid + 1] = xv.y * (scale * w.y);
@@ -152,12 +291,17 @@ __device__ __forceinline__ float4 load_norm_x(const Ctx& c, const float* x, floa
     return xv;
 }
 
+// Tag of phase k (1..6) of layer l.
+__device__ __forceinline__ uint32_t ptag(const DecodeArgs& A, uint32_t l, uint32_t k) {
+    return A.base + 6 * (l - A.l0) + k;
+}
+
 // ================================================================== A: qkv ==
 // Flat rows [q | k | v]; wave gw owns rows gw, gw + NWV, gw + 2 NWV.  q and k
 // share format KQ, v has KV.  Rows have H <= 2048 columns: lane = chunk.
 template <uint32_t KQ, uint32_t KV>
 __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
-                                          bool wait_x, uint32_t& ph) {
+                                          uint32_t l) {
     const Ctx c = fresh(c0);
     const uint32_t nq = L.q.rows, nk = L.k.rows, nt = nq + nk + L.v.rows, cpr = c.H / 32;
     typename Fmt<KQ>::Raw wq[kQkvPerWave];
@@ -174,11 +318,17 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
     }
     float4 nw = make_float4(0.f, 0.f, 0.f, 0.f);
     if (4 * c.tid < c.H) nw = reinterpret_cast<const float4*>(L.attn_norm)[c.tid];
-    QH_MARK(0, 0);
-    if (wait_x && !wait_all(A, S, ph)) return false;  // x of the previous layer (phase F)
-    QH_MARK(0, 1);
     float* xs = S.big;
-    const float4 xv = load_norm_x(c, A.a.x, nw, A.dm.eps, xs, S.red);
+    QH_MARK(0, 0);
+    if (l == A.l0) {
+        // x as the embedding kernel (or the host) left it before this launch
+        if (4 * c.tid < c.H) reinterpret_cast<float4*>(xs)[c.tid] = ld_sys4(buf_rsrc(A.a.x, c.H * 4), c.tid * 16);
+        __syncthreads();
+    } else if (!gather_s(A, S, A.tx2, c.H, ptag(A, l - 1, 6), xs, c.tid, c.nwg, 0, c.rpw)) {
+        return false;  // x'' of the previous layer (phase F)
+    }
+    QH_MARK(0, 1);
+    const float4 xv = norm_in_lds(c, xs, nw, A.dm.eps, S.red);
     // this workgroup's residual rows, kept in LDS through the layer
     if (4 * c.tid < c.H) {
         const float e4[4] = {xv.x, xv.y, xv.z, xv.w};
@@ -188,6 +338,7 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
             if (r >= c.r0 && r < c.r0 + c.nr) S.xo[r - c.r0] = e4[i];
         }
     }
+    const uint32_t tag = ptag(A, l, 1);
     float xa[16], xb[16], sa, sb;
     if (c.lane < cpr) x_runs<KQ>(xs, c.lane, xa, xb, sa, sb);
 #pragma unroll
@@ -205,22 +356,30 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
                 }
             }
             acc = wave_sum(acc);
-            float* out = r < nq ? A.a.q + r : r < nq + nk ? A.a.k + (r - nq) : A.a.v + (r - nq - nk);
-            if (c.lane == 0) st_sys(out, acc);
+            if (c.lane == 0) put(A.tqkv + r, acc, tag);
         }
     }
     QH_MARK(0, 2);
-    signal(A, ++ph);
+    __syncthreads();  // xs is reused by the next phase
     return true;
 }
 
 // ============================================================ B: attention ==
-// KV head g = b / 32, chunk b % 32 (the k_attn128 scheme, reading the q/k/v
-// projections written through by phase A).
+// KV head g = b / 32, chunk b % 32.  A chunk covers >= 64 keys (at most
+// max_chunks chunks per head) and runs 64-key tiles on all eight waves:
+//   scores   thread (key tid/8, 16-dim part tid%8) holds its K slice in
+//            registers and reduces the 8 parts of each head on DPP;
+//   softmax  wave h owns head h (lane = key), online over the tiles;
+//   P.V      wave h, lane (4 dims j4, key half kh): the weights of keys t and
+//            t + 32 are broadcast with v_readlane, V is read from LDS.
+// Chunks > 0 pass their partial (o[128], m, l) on as tagged words; chunk 0
+// merges them (each half of a wave takes half of the chunks, 8 per round of
+// loads), or with a single chunk writes the output directly.
 __device__ __forceinline__ void kv_slice(float4 (&kr)[4], float4 (&vr)[4], const float* kc, const float* vc,
-                                         uint32_t g, uint32_t ctx, uint32_t tt, uint32_t t1, uint32_t pos) {
-    const uint32_t key = tt + ((threadIdx.x & 255) >> 3), j = (threadIdx.x & 7) * 16;
-    if (threadIdx.x < 256 && key < t1 && key != pos) {
+                                         uint32_t g, uint32_t ctx, uint32_t tt, uint32_t t1, uint32_t pos,
+                                         uint32_t tid) {
+    const uint32_t key = tt + (tid >> 3), j = (tid & 7) * 16;
+    if (key < t1 && key != pos) {
         const float4* ks = reinterpret_cast<const float4*>(kc + ((size_t)g * ctx + key) * 128 + j);
         const float4* vs = reinterpret_cast<const float4*>(vc + ((size_t)g * ctx + key) * 128 + j);
 #pragma unroll
@@ -231,244 +390,244 @@ __device__ __forceinline__ void kv_slice(float4 (&kr)[4], float4 (&vr)[4], const
     }
 }
 
+__device__ __forceinline__ float shfl32(float v) { return __shfl_xor(v, 32, 64); }
+
 __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
-                                           uint32_t& ph) {
+                                           uint32_t l) {
     const Ctx c = fresh(c0);
     const Acts& a = A.a;
     const ModelDims& dm = A.dm;
-    const uint32_t nch = min((c.T + 31) / 32, A.max_chunks);
+    const uint32_t nch = min((c.T + kDTile - 1) / kDTile, A.max_chunks);
     const uint32_t g = c.b / kDChunks, ch = c.b % kDChunks;
-    const bool active = g < dm.kvheads && ch < nch;
-    if (!active) {
-        signal(A, ++ph);
-        return true;
-    }
+    if (!(g < dm.kvheads && ch < nch)) return true;  // not an attention workgroup this step
     const uint32_t tid = c.tid, wv = c.wv, lane = c.lane, G = c.G, pos = c.pos, ctx = c.ctx;
     const uint32_t tc = (c.T + nch - 1) / nch;
     const uint32_t t0 = min(c.T, ch * tc), t1 = min(c.T, t0 + tc);
+    const bool holds = t0 <= pos && pos < t1;
+    const uint32_t tag_in = ptag(A, l, 1), tag = ptag(A, l, 2);
+    QH_MARK(1, 5);
     float4 kr[4], vr[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) kr[i] = vr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    kv_slice(kr, vr, L.kcache, L.vcache, g, ctx, t0, t1, pos);
+    kv_slice(kr, vr, L.kcache, L.vcache, g, ctx, t0, t1, pos, tid);
+    QH_MARK(1, 6);
     const float qw0 = L.q_norm[lane], qw1 = L.q_norm[lane + 64];
     const float kw0 = L.k_norm[lane], kw1 = L.k_norm[lane + 64];
     const float2 cs = a.rope[(size_t)pos * 64 + lane];
+    // Wave w: q head w (w < G); the new key by wave G % 8; the new value by
+    // wave 7.  Lane l holds elements l and l + 64 (the rotated pair).
+    const bool hasq = wv < G, hask = wv == G % kDW, hasv = wv == kDW - 1;
+    const uint32_t qo = (g * G + wv) * 128 + lane, ko = c.qd + g * 128 + lane, vo = c.qd + c.kvd + g * 128 + lane;
     QH_MARK(1, 0);
-    if (!wait_all(A, S, ph)) return false;  // q/k/v (phase A)
+    bool ab = false;
+    float qkv[6];
+    {
+        const uint32_t idx[6] = {qo, qo + 64, ko, ko + 64, vo, vo + 64};
+        poll_words<6>(A, A.tqkv, idx, (hasq ? 3u : 0u) | (hask ? 12u : 0u) | (hasv ? 48u : 0u), tag_in, qkv, ab);
+    }
+    const float qa = qkv[0], qb = qkv[1], ka = qkv[2], kb = qkv[3], va = qkv[4], vb = qkv[5];
     QH_MARK(1, 1);
-    float* qs = S.big;              // [8][160]  normalised, rotated queries (parts padded to 20)
-    float* kn = qs + 8 * 160;       // [160]     new key, same layout
-    float* vn = kn + 160;           // [128]     new value
-    float* vs = vn + 128;           // [32][128] value tile
-    float* ps = vs + kDTile * 128;  // [8][36]   scores, then exp weights
-    float* al = ps + 8 * 36;        // [8]       rescale factor of the tile
-    float* ml = al + 8;             // [8][2]    final (m, l) per head
-    const bool holds = t0 <= pos && pos < t1;
-    // Q/K RMSNorm (model.rs:233-238) + NeoX RoPE (ops.rs:17-28): lane l holds
-    // elements l and l + 64, the rotated pair
-    for (uint32_t vi = wv; vi <= G; vi += kDW) {
-        const bool isk = vi == G;
-        const float* src = isk ? a.k + g * 128 : a.q + (g * G + vi) * 128;
-        const float xa = ld_sys(src + lane), xb = ld_sys(src + lane + 64);
+    float* qs = S.big;               // [8][160]  normalised, rotated queries (parts padded to 20)
+    float* kn = qs + 8 * 160;        // [160]     new key, same layout
+    float* vn = kn + 160;            // [128]     new value
+    float* vs = vn + 128;            // [64][128] value tile
+    float* ps = vs + kDTile * 128;   // [8][64]   scores
+    // Q/K RMSNorm (model.rs:233-238) + NeoX RoPE (ops.rs:17-28)
+    auto norm_rope = [&](float xa, float xb, float w0, float w1, float* dst, bool append) {
         const float ssq = wave_sum(fmaf(xb, xb, xa * xa));
         const float sc = 1.0f / sqrtf(ssq / 128.0f + dm.eps);
-        const float y0 = xa * (sc * (isk ? kw0 : qw0));
-        const float y1 = xb * (sc * (isk ? kw1 : qw1));
+        const float y0 = xa * (sc * w0), y1 = xb * (sc * w1);
         float o0, o1;
         {
 #pragma clang fp contract(off)
             o0 = y0 * cs.x - y1 * cs.y;
             o1 = y0 * cs.y + y1 * cs.x;
         }
-        float* dst = isk ? kn : qs + vi * 160;
         dst[(lane / 16) * 20 + lane % 16] = o0;
         dst[((lane + 64) / 16) * 20 + lane % 16] = o1;
-        if (isk && holds) {  // KV append (model.rs:241-243)
+        if (append) {  // KV append (model.rs:241-243)
             L.kcache[((size_t)g * ctx + pos) * 128 + lane] = o0;
             L.kcache[((size_t)g * ctx + pos) * 128 + lane + 64] = o1;
         }
+    };
+    if (hasq) norm_rope(qa, qb, qw0, qw1, qs + wv * 160, false);
+    if (hask) norm_rope(ka, kb, kw0, kw1, kn, holds);
+    if (hasv) {
+        vn[lane] = va;
+        vn[lane + 64] = vb;
+        if (holds) {
+            L.vcache[((size_t)g * ctx + pos) * 128 + lane] = va;
+            L.vcache[((size_t)g * ctx + pos) * 128 + lane + 64] = vb;
+        }
     }
-    QH_MARK(1, 4);
-    if (tid < 32) {
-        const float* vsrc = a.v + g * 128 + 4 * tid;
-        const float4 v4 = make_float4(ld_sys(vsrc), ld_sys(vsrc + 1), ld_sys(vsrc + 2), ld_sys(vsrc + 3));
-        reinterpret_cast<float4*>(vn)[tid] = v4;
-        if (holds) reinterpret_cast<float4*>(L.vcache + ((size_t)g * ctx + pos) * 128)[tid] = v4;
-    }
+    if (ab) S.abort = 1;
     __syncthreads();
-    QH_MARK(1, 5);
+    if (S.abort) return false;
+    QH_MARK(1, 4);
     const float root = sqrtf(128.0f);
-    float mh = -INFINITY, lh = 0.f;               // head wv (softmax wave)
-    float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);  // threads < 256: head tid/32, dims 4*(tid%32)
-    const uint32_t hq = tid >> 5, j4 = tid & 31, part = tid & 7, kt = (tid & 255) >> 3;
+    const uint32_t part = tid & 7, kt = tid >> 3, j4 = lane & 31, kh = lane >> 5;
+    float mh = -INFINITY, lh = 0.f;               // head wv
+    float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);  // head wv, dims 4*j4, keys of half kh
     for (uint32_t tt = t0; tt < t1; tt += kDTile) {
         const uint32_t nt = min(kDTile, t1 - tt);
-        if (wv < 4) {  // threads 0..255 = (key kt, 16-dim part): scores + V tile
-            if (tt + kt == pos) {
+        if (tt + kt == pos) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                kr[i] = reinterpret_cast<const float4*>(kn + part * 20)[i];
+                vr[i] = reinterpret_cast<const float4*>(vn + part * 16)[i];
+            }
+        }
+        float mine = 0.f;
+#pragma unroll
+        for (uint32_t h = 0; h < 8; h++) {
+            float acc = 0.f;
+            if (h < G) {
+                const float4* q4 = reinterpret_cast<const float4*>(qs + h * 160 + part * 20);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    kr[i] = reinterpret_cast<const float4*>(kn + part * 20)[i];
-                    vr[i] = reinterpret_cast<const float4*>(vn + part * 16)[i];
+                    const float4 q = q4[i];
+                    acc = fmaf(q.x, kr[i].x, acc);
+                    acc = fmaf(q.y, kr[i].y, acc);
+                    acc = fmaf(q.z, kr[i].z, acc);
+                    acc = fmaf(q.w, kr[i].w, acc);
                 }
             }
-            float mine = 0.f;
-#pragma unroll
-            for (uint32_t h = 0; h < 8; h++) {
-                float acc = 0.f;
-                if (h < G) {
-                    const float4* q4 = reinterpret_cast<const float4*>(qs + h * 160 + part * 20);
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float4 q = q4[i];
-                        acc = fmaf(q.x, kr[i].x, acc);
-                        acc = fmaf(q.y, kr[i].y, acc);
-                        acc = fmaf(q.z, kr[i].z, acc);
-                        acc = fmaf(q.w, kr[i].w, acc);
-                    }
-                }
-                acc += dpp_f<kDppXor1>(acc);
-                acc += dpp_f<kDppXor2>(acc);
-                acc += dpp_f<kDppHalfMirror>(acc);
-                mine = part == h ? acc : mine;
-            }
-            if (kt < nt) {
-#pragma unroll
-                for (int i = 0; i < 4; i++) reinterpret_cast<float4*>(vs + kt * 128 + part * 16)[i] = vr[i];
-                if (part < G) ps[part * 36 + kt] = mine / root;
-            }
-            if (tt + kDTile < t1) kv_slice(kr, vr, L.kcache, L.vcache, g, ctx, tt + kDTile, t1, pos);
+            acc += dpp_f<kDppXor1>(acc);
+            acc += dpp_f<kDppXor2>(acc);
+            acc += dpp_f<kDppHalfMirror>(acc);
+            mine = part == h ? acc : mine;
         }
+        if (kt < nt) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) reinterpret_cast<float4*>(vs + kt * 128 + part * 16)[i] = vr[i];
+            if (part < G) ps[part * kDTile + kt] = mine / root;
+        }
+        if (tt + kDTile < t1) kv_slice(kr, vr, L.kcache, L.vcache, g, ctx, tt + kDTile, t1, pos, tid);
         __syncthreads();
-        if (wv < G) {  // online softmax: wave wv owns head wv
-            const float sv = lane < nt ? ps[wv * 36 + lane] : -INFINITY;
+        if (wv < G) {  // wave-uniform: online softmax and P.V of head wv
+            const float sv = lane < nt ? ps[wv * kDTile + lane] : -INFINITY;
             const float M = fmaxf(mh, wave_max(sv));
             const float e = lane < nt ? expf(sv - M) : 0.f;
-            const float sum = wave_sum(e);
             const float alpha = expf(mh - M);  // 0 on the first tile
-            lh = fmaf(lh, alpha, sum);
+            lh = fmaf(lh, alpha, wave_sum(e));
             mh = M;
-            if (lane < nt) ps[wv * 36 + lane] = e;
-            if (lane == 0) al[wv] = alpha;
-        }
-        __syncthreads();
-        if (wv < 4 && hq < G) {  // P.V
-            const float alpha = al[hq];
             o4.x *= alpha;
             o4.y *= alpha;
             o4.z *= alpha;
             o4.w *= alpha;
-            const float* phh = ps + hq * 36;
-            for (uint32_t t = 0; t < nt; t++) {
-                const float p = phh[t];
-                const float4 v = reinterpret_cast<const float4*>(vs + t * 128)[j4];
-                o4.x = fmaf(p, v.x, o4.x);
-                o4.y = fmaf(p, v.y, o4.y);
-                o4.z = fmaf(p, v.z, o4.z);
-                o4.w = fmaf(p, v.w, o4.w);
+            // keys t and t + 32 of the tile: e = 0 beyond nt, and V rows beyond
+            // nt are skipped (they may hold any bits)
+            const uint32_t nh = nt > kh * 32 ? min(32u, nt - kh * 32) : 0u;  // keys of this half
+            const float* vrow = vs + kh * 32 * 128 + 4 * j4;
+            const uint32_t n32 = min(32u, nt);
+            for (uint32_t q0 = 0; q0 < n32; q0 += 8) {
+                float4 v[8];
+#pragma unroll
+                for (uint32_t k = 0; k < 8; k++)
+                    v[k] = q0 + k < nh ? *reinterpret_cast<const float4*>(vrow + (q0 + k) * 128)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (uint32_t k = 0; k < 8; k++) {
+                    const uint32_t t = q0 + k;
+                    const float p0 = lane_f(e, t & 31), p1 = lane_f(e, (t & 31) + 32);
+                    const float p = kh ? p1 : p0;
+                    o4.x = fmaf(p, v[k].x, o4.x);
+                    o4.y = fmaf(p, v[k].y, o4.y);
+                    o4.z = fmaf(p, v[k].z, o4.z);
+                    o4.w = fmaf(p, v[k].w, o4.w);
+                }
             }
         }
         __syncthreads();
     }
-    if (lane == 0 && wv < G) {
-        ml[wv * 2] = mh;
-        ml[wv * 2 + 1] = lh;
-    }
-    __syncthreads();
     QH_MARK(1, 2);
-    if (nch == 1) {
-        if (wv < 4 && hq < G) {
-            const float inv = 1.0f / ml[hq * 2 + 1];
-            float* out = a.attn + (g * G + hq) * 128 + 4 * j4;
-            st_sys(out, o4.x * inv);
-            st_sys(out + 1, o4.y * inv);
-            st_sys(out + 2, o4.z * inv);
-            st_sys(out + 3, o4.w * inv);
+    // the two key halves of each head
+    o4.x += shfl32(o4.x);
+    o4.y += shfl32(o4.y);
+    o4.z += shfl32(o4.z);
+    o4.w += shfl32(o4.w);
+    const uint32_t mc = A.max_chunks;
+    if (ch > 0) {  // pass the partial on to chunk 0
+        if (wv < G && kh == 0) {
+            uint64_t* dst = A.tpart + ((size_t)(g * G + wv) * mc + ch) * kPartWords;
+            put(dst + 4 * j4, o4.x, tag);
+            put(dst + 4 * j4 + 1, o4.y, tag);
+            put(dst + 4 * j4 + 2, o4.z, tag);
+            put(dst + 4 * j4 + 3, o4.w, tag);
+            if (lane < 2) put(dst + 128 + lane, lane == 0 ? mh : lh, tag);
         }
-        signal(A, ++ph);
         return true;
     }
-    // chunk partials written through; the last chunk of the head merges them
-    const uint32_t mc = A.max_chunks;
-    float* po = a.part;
-    float* pml = a.part + (size_t)dm.heads * mc * 128;
-    if (wv < 4 && hq < G) {
-        float* dst = po + ((size_t)(g * G + hq) * mc + ch) * 128 + 4 * j4;
-        st_sys(dst, o4.x);
-        st_sys(dst + 1, o4.y);
-        st_sys(dst + 2, o4.z);
-        st_sys(dst + 3, o4.w);
-    }
-    if (tid < 2 * G) st_sys(pml + ((size_t)(g * G + tid / 2) * mc + ch) * 2 + (tid & 1), ml[tid]);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(&a.attn_cnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        S.last = old == nch - 1;
-        if (S.last) st_sys_u(&a.attn_cnt[g], 0u);
-    }
-    __syncthreads();
-    if (S.last && wv < 4 && hq < G) {
-        // online merge over chunk groups of 16 (all loads of a group at once):
-        // O = sum_c o_c exp(m_c - M) / L, L = sum_c l_c exp(m_c - M)
-        constexpr uint32_t kGrp = 16;
-        const float* mlh = pml + (size_t)(g * G + hq) * mc * 2;
-        const __amdgpu_buffer_rsrc_t orsrc = buf_rsrc(po, (uint32_t)((size_t)dm.heads * mc * 128 * 4));
-        const uint32_t obase = ((g * G + hq) * mc * 128 + 4 * j4) * 4;
-        float M = -INFINITY, Ls = 0.f;
-        float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (uint32_t c0 = 0; c0 < nch; c0 += kGrp) {
-            float m[kGrp], l[kGrp];
-            float4 o[kGrp];
+    if (wv < G) {  // wave-uniform
+        // O = sum_c o_c exp(m_c - M) / L,  L = sum_c l_c exp(m_c - M); half kh
+        // takes chunks kh + 2i (chunk 0 from registers), 8 per round of loads
+        float M = kh == 0 ? mh : -INFINITY, Ls = kh == 0 ? lh : 0.f;
+        float4 O = kh == 0 ? o4 : make_float4(0.f, 0.f, 0.f, 0.f);
+        const uint64_t* hb = A.tpart + (size_t)(g * G + wv) * mc * kPartWords;
+        const __amdgpu_buffer_rsrc_t pr = buf_rsrc(hb, mc * kPartWords * 8);
+        for (uint32_t cb = kh; cb < nch; cb += 16) {
+            uint32_t word[24], need = 0;
 #pragma unroll
-            for (uint32_t k = 0; k < kGrp; k++) {
-                if (c0 + k < nch) {
-                    m[k] = ld_sys(mlh + (c0 + k) * 2);
-                    l[k] = ld_sys(mlh + (c0 + k) * 2 + 1);
-                    o[k] = ld_sys4(orsrc, obase + (c0 + k) * 128 * 4);
+            for (uint32_t k = 0; k < 8; k++) {
+                const uint32_t cc = cb + 2 * k;
+                word[3 * k] = cc * kPartWords + 128;  // m, l
+                word[3 * k + 1] = cc * kPartWords + 4 * j4;
+                word[3 * k + 2] = cc * kPartWords + 4 * j4 + 2;
+                if (cc > 0 && cc < nch) need |= 7u << (3 * k);
+            }
+            float v[48];
+            poll_pairs<24>(A, pr, word, need, need, tag, v, ab);
+            if (ab) break;
+            float Mn = M;
+#pragma unroll
+            for (uint32_t k = 0; k < 8; k++)
+                if (cb + 2 * k > 0 && cb + 2 * k < nch) Mn = fmaxf(Mn, v[6 * k]);
+            const float f = expf(M - Mn);  // 0 while M = -inf
+            Ls *= f;
+            O.x *= f;
+            O.y *= f;
+            O.z *= f;
+            O.w *= f;
+#pragma unroll
+            for (uint32_t k = 0; k < 8; k++) {
+                if (cb + 2 * k > 0 && cb + 2 * k < nch) {
+                    const float e = expf(v[6 * k] - Mn);
+                    Ls = fmaf(v[6 * k + 1], e, Ls);
+                    O.x = fmaf(v[6 * k + 2], e, O.x);
+                    O.y = fmaf(v[6 * k + 3], e, O.y);
+                    O.z = fmaf(v[6 * k + 4], e, O.z);
+                    O.w = fmaf(v[6 * k + 5], e, O.w);
                 }
             }
-            float Mg = M;
-#pragma unroll
-            for (uint32_t k = 0; k < kGrp; k++)
-                if (c0 + k < nch) Mg = fmaxf(Mg, m[k]);
-            const float f0 = expf(M - Mg);  // 0 for the first group
-            Ls *= f0;
-            O.x *= f0;
-            O.y *= f0;
-            O.z *= f0;
-            O.w *= f0;
-#pragma unroll
-            for (uint32_t k = 0; k < kGrp; k++) {
-                if (c0 + k < nch) {
-                    const float e = expf(m[k] - Mg);
-                    Ls = fmaf(l[k], e, Ls);
-                    O.x = fmaf(o[k].x, e, O.x);
-                    O.y = fmaf(o[k].y, e, O.y);
-                    O.z = fmaf(o[k].z, e, O.z);
-                    O.w = fmaf(o[k].w, e, O.w);
-                }
-            }
-            M = Mg;
+            M = Mn;
         }
-        const float inv = 1.0f / Ls;
-        float* out = a.attn + (g * G + hq) * 128 + 4 * j4;
-        st_sys(out, O.x * inv);
-        st_sys(out + 1, O.y * inv);
-        st_sys(out + 2, O.z * inv);
-        st_sys(out + 3, O.w * inv);
+        // the two halves (a half without chunks has M = -inf and adds 0)
+        const float Mo = shfl32(M), Lo = shfl32(Ls);
+        const float4 Oo = make_float4(shfl32(O.x), shfl32(O.y), shfl32(O.z), shfl32(O.w));
+        if (kh == 0) {
+            const float Mn = fmaxf(M, Mo);
+            const float f0 = expf(M - Mn), f1 = expf(Mo - Mn);
+            const float inv = 1.0f / fmaf(Ls, f0, Lo * f1);
+            uint64_t* out = A.tatt + (g * G + wv) * 128 + 4 * j4;
+            put(out, fmaf(O.x, f0, Oo.x * f1) * inv, tag);
+            put(out + 1, fmaf(O.y, f0, Oo.y * f1) * inv, tag);
+            put(out + 2, fmaf(O.z, f0, Oo.z * f1) * inv, tag);
+            put(out + 3, fmaf(O.w, f0, Oo.w * f1) * inv, tag);
+        }
     }
+    if (ab) S.abort = 1;
     QH_MARK(1, 3);
-    signal(A, ++ph);
-    return true;
+    __syncthreads();
+    return S.abort == 0;
 }
 
 // ======================================================== C: o-projection ==
 // Wave wv owns row r0 + wv (qd <= 4096 columns: chunks lane, lane + 64).
 template <uint32_t KO>
 __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
-                                            uint32_t& ph) {
+                                            uint32_t l) {
     const Ctx c = fresh(c0);
-    const uint32_t ocpr = c.qd / 32, E = c.E;
+    const uint32_t ocpr = c.qd / 32;
     typename Fmt<KO>::Raw w0, w1;
     const bool rowok = c.wv < c.nr;
     const uint8_t* orow = L.o.w + (size_t)(c.r0 + c.wv) * L.o.drb;
@@ -476,25 +635,11 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
         if (c.lane < ocpr) w0 = Fmt<KO>::load(orow, L.o.geo, c.lane);
         if (c.lane + 64 < ocpr) w1 = Fmt<KO>::load(orow, L.o.geo, c.lane + 64);
     }
-    // F32 router weights of this workgroup's rows: thread (e = tid/4, q = tid%4)
-    // owns rows 2q, 2q + 1
-    const uint32_t e = c.tid >> 2, q = c.tid & 3;
-    float rw0 = 0.f, rw1 = 0.f;
-    if (e < E) {
-        const float* wr = reinterpret_cast<const float*>(L.router.w + (size_t)e * L.router.drb) + c.r0;
-        if (2 * q < c.nr) rw0 = wr[2 * q];
-        if (2 * q + 1 < c.nr) rw1 = wr[2 * q + 1];
-    }
-    if (c.tid < c.nr) S.wn[c.tid] = L.ffn_norm[c.r0 + c.tid];
     QH_MARK(2, 0);
-    if (!wait_all(A, S, ph)) return false;  // attention output (phase B)
-    QH_MARK(2, 1);
     float* xs = S.big;
-    {
-        const __amdgpu_buffer_rsrc_t ar = buf_rsrc(A.a.attn, c.qd * 4);
-        for (uint32_t i = c.tid; i < c.qd / 4; i += kDT) reinterpret_cast<float4*>(xs)[i] = ld_sys4(ar, i * 16);
-    }
-    __syncthreads();
+    if (!gather_s(A, S, A.tatt, c.qd, ptag(A, l, 2), xs, c.tid, c.qd / 128, 127, 128))
+        return false;  // attention output (phase B)
+    QH_MARK(2, 1);
     if (rowok) {  // wave-uniform
         float acc = 0.f;
         float xa[16], xb[16], sa, sb;
@@ -507,72 +652,56 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
             acc += Fmt<KO>::dot(w1, c.lane + 64, xa, xb, sa, sb);
         }
         acc = wave_sum(acc);
-        if (c.lane == 0) {
-            const float xn = S.xo[c.wv] + acc;  // residual (model.rs:246-248)
-            S.xo[c.wv] = xn;
-            st_sys(A.a.x + c.r0 + c.wv, xn);
-        }
-    }
-    __syncthreads();
-    // router partial dots over the rows (the logits are linear in x')
-    float p = 0.f;
-    if (2 * q < c.nr) p = rw0 * (S.wn[2 * q] * S.xo[2 * q]);
-    if (2 * q + 1 < c.nr) p = fmaf(rw1, S.wn[2 * q + 1] * S.xo[2 * q + 1], p);
-    p += dpp_f<kDppXor1>(p);
-    p += dpp_f<kDppXor2>(p);
-    if (q == 0 && e < E) st_sys(A.rpart + (size_t)c.b * c.E1 + e, p);
-    if (c.wv == 0) {
-        float v = c.lane < c.nr ? S.xo[c.lane] * S.xo[c.lane] : 0.f;
-        v = wave_sum(v);
-        if (c.lane == 0) st_sys(A.rpart + (size_t)c.b * c.E1 + E, v);
+        if (c.lane == 0) S.xo[c.wv] += acc;  // residual (model.rs:246-248)
     }
     QH_MARK(2, 2);
-    signal(A, ++ph);
+    __syncthreads();
+    if (c.tid < c.nr) put(A.tx1 + c.r0 + c.tid, S.xo[c.tid], ptag(A, l, 3));  // one store instruction
     return true;
 }
 
-// ========================================================== D: router fold ==
-// Workgroup e <= E folds column e (and the sum of squares) over the partial
-// rows of every workgroup, in one fixed order.
-__device__ __forceinline__ bool phase_fold(const DecodeArgs& A, DecodeLds& S, const Ctx& c0, uint32_t& ph) {
+// ================================================================ D: router ==
+// Every workgroup gathers x' into LDS and computes the ffn RMSNorm scale
+// s = 1/sqrt(mean(x'^2) + eps) (ops.rs:3-15); workgroup e < E also computes
+// logit e = s * sum_i Wr[e][i] (x'[i] w[i]) (model.rs:249-256) and passes it on.
+// Returns s (negative when the step was aborted).
+__device__ __forceinline__ float phase_router(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
+                                              uint32_t l) {
     const Ctx c = fresh(c0);
-    if (c.b < c.E1) {
-        QH_MARK(3, 0);
-        if (!wait_all(A, S, ph)) return false;  // router partials (phase C)
-        QH_MARK(3, 1);
-        float v = 0.f, vs = 0.f;
-        if (c.tid < c.nwg) {
-            v = ld_sys(A.rpart + (size_t)c.tid * c.E1 + c.b);
-            vs = ld_sys(A.rpart + (size_t)c.tid * c.E1 + c.E);
-        }
-        const float fold = dsum(v, S.red);
-        const float fsq = dsum(vs, S.red);
-        if (c.tid == 0) {
-            const float s = 1.0f / sqrtf(fsq / (float)c.H + A.dm.eps);
-            st_sys(A.rlog + c.b, c.b < c.E ? s * fold : s);
-        }
-        QH_MARK(3, 2);
+    const bool rt = c.b < c.E;
+    float4 wr = make_float4(0.f, 0.f, 0.f, 0.f), fw = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (rt && 4 * c.tid < c.H) {
+        wr = reinterpret_cast<const float4*>(L.router.w + (size_t)c.b * L.router.drb)[c.tid];
+        fw = reinterpret_cast<const float4*>(L.ffn_norm)[c.tid];
     }
-    signal(A, ++ph);
-    return true;
+    QH_MARK(3, 0);
+    float* xs = S.big;
+    if (!gather_s(A, S, A.tx1, c.H, ptag(A, l, 3), xs, c.tid, c.nwg, 0, c.rpw)) return -1.f;  // x' (phase C)
+    QH_MARK(3, 1);
+    float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (4 * c.tid < c.H) xv = reinterpret_cast<const float4*>(xs)[c.tid];
+    const float dt =
+        fmaf(wr.w, xv.w * fw.w, fmaf(wr.z, xv.z * fw.z, fmaf(wr.y, xv.y * fw.y, wr.x * (xv.x * fw.x))));
+    const float2 r = dsum2(sumsq4(xv), dt, S.red);
+    const float s = 1.0f / sqrtf(r.x / (float)c.H + A.dm.eps);
+    if (rt && c.tid == 0) put(A.tlog + c.b, s * r.y, ptag(A, l, 4));
+    QH_MARK(3, 2);
+    return s;
 }
 
 // ============================================== E + F: routed expert FFN ==
+// x' (raw) is in LDS from phase D, s its RMS scale.
 template <uint32_t KG, uint32_t KD>
 __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
-                                          uint32_t& ph) {
+                                          uint32_t l, float s, bool last) {
     const Ctx c = fresh(c0);
     const Acts& a = A.a;
-    const uint32_t E = c.E, top = c.top, ff = c.ff, fp = c.fp, H = c.H, cpr = H / 32;
+    const uint32_t E = c.E, top = c.top, ff = c.ff, H = c.H, cpr = H / 32;
     float4 fn = make_float4(0.f, 0.f, 0.f, 0.f);
     if (4 * c.tid < H) fn = reinterpret_cast<const float4*>(L.ffn_norm)[c.tid];
     QH_MARK(4, 0);
-    if (!wait_all(A, S, ph)) return false;  // folded logits (phase D)
+    if (!gather(A, S, A.tlog, E, ptag(A, l, 4), S.lg, c.tid)) return false;  // router logits (phase D)
     QH_MARK(4, 1);
-    if (c.tid <= E) S.lg[c.tid] = ld_sys(A.rlog + c.tid);
-    float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (4 * c.tid < H) xv = ld_sys4(buf_rsrc(a.x, H * 4), c.tid * 16);
-    __syncthreads();
     // top-k by rank under the total order, lower index on ties (ops.rs:45-56;
     // bit-exact on these logits): j outranks i iff ck[j] > ck[i]
     const uint32_t Ep = (E + 7) & ~7u;
@@ -631,10 +760,10 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
             wu[k] = Fmt<KG>::load(L.up.w + (size_t)ex * L.up.expert_stride + (size_t)rr * L.up.drb, L.up.geo, c.lane);
         }
     }
-    // xn = x' * (s * ffn_norm)
+    // xn = x' * (s * ffn_norm), in place (each thread rewrites its own float4)
     float* xs = S.big;
-    const float s = S.lg[E];
     if (4 * c.tid < H) {
+        const float4 xv = reinterpret_cast<const float4*>(xs)[c.tid];
         xs[4 * c.tid] = xv.x * (s * fn.x);
         xs[4 * c.tid + 1] = xv.y * (s * fn.y);
         xs[4 * c.tid + 2] = xv.z * (s * fn.z);
@@ -649,6 +778,7 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         if (c.tid < E) a.logits_r[c.tid] = S.lg[c.tid];
     }
     QH_MARK(4, 4);
+    const uint32_t tag_h = ptag(A, l, 5);
     {
         float xa[16], xb[16], sa, sb;
         if (c.lane < cpr) x_runs<KG>(xs, c.lane, xa, xb, sa, sb);
@@ -665,13 +795,18 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
                 uv = wave_sum(uv);
                 if (c.lane == 0) {
 #pragma clang fp contract(off)
-                    const float hv = (gv / (1.f + expf(-gv))) * uv;  // SwiGLU (model.rs:272)
-                    st_sys(a.h + (pr / ff) * fp + pr % ff, hv);
+                    S.hv[c.wv * kPairsPerWave + k] = (gv / (1.f + expf(-gv))) * uv;  // SwiGLU (model.rs:272)
                 }
             }
         }
     }
     QH_MARK(4, 5);
+    __syncthreads();  // S.hv complete; every wave is done with xn, which the gather overwrites
+    {
+        // this workgroup's outputs [slot][ff] flat at b * kHBlock, one store instruction
+        const uint32_t i = c.b * kHBlock + c.tid;
+        if (c.tid < kHBlock && i < top * ff) put(A.th + i, S.hv[c.tid], tag_h);
+    }
     // down rows of phase F (row r0 + wv of each routed expert), requested
     // before the wait: lane units u = lane + 64 i = (slot u / dcpr, chunk u % dcpr)
     const uint32_t dcpr = ff / 32, U = top * dcpr;
@@ -686,17 +821,11 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         }
     }
     QH_MARK(4, 3);
-    signal(A, ++ph);
+    // ================================================ F: down + combine
     QH_MARK(5, 0);
-    if (!wait_all(A, S, ph)) return false;  // SwiGLU outputs (phase E)
+    if (!gather_s(A, S, A.th, top * ff, tag_h, xs, c.tid, (top * ff + kHBlock - 1) / kHBlock, 0, kHBlock))
+        return false;  // SwiGLU outputs (phase E)
     QH_MARK(5, 1);
-    {
-        const uint32_t nh = top * fp;
-        const __amdgpu_buffer_rsrc_t hr = buf_rsrc(a.h, nh * 4);
-        for (uint32_t i = c.tid; i < nh / 4; i += kDT) reinterpret_cast<float4*>(xs)[i] = ld_sys4(hr, i * 16);
-    }
-    __syncthreads();
-    QH_MARK(5, 3);
     if (c.wv < c.nr) {  // wave-uniform
         float acc = 0.f;
 #pragma unroll
@@ -705,29 +834,30 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
             if (u < U) {
                 const uint32_t sl = u / dcpr, chn = u % dcpr;
                 float xa[16], xb[16], sa, sb;
-                x_runs<KD>(xs + sl * fp, chn, xa, xb, sa, sb);
+                x_runs<KD>(xs + sl * ff, chn, xa, xb, sa, sb);
                 acc = fmaf(S.wts[sl], Fmt<KD>::dot(wd[i], chn, xa, xb, sa, sb), acc);
             }
         }
         acc = wave_sum(acc);
-        if (c.lane == 0) {
-            const float xn = S.xo[c.wv] + acc;  // x += sum_s w_s down_s (model.rs:281-287)
-            S.xo[c.wv] = xn;
-            st_sys(a.x + c.r0 + c.wv, xn);
-        }
+        if (c.lane == 0) S.xo[c.wv] += acc;  // x += sum_s w_s down_s (model.rs:281-287)
     }
     QH_MARK(5, 2);
-    signal(A, ++ph);
+    __syncthreads();
+    if (c.tid < c.nr) {
+        put(A.tx2 + c.r0 + c.tid, S.xo[c.tid], ptag(A, l, 6));  // one store instruction
+        if (last) a.x[c.r0 + c.tid] = S.xo[c.tid];            // x after the launch, for the host
+    }
     return true;
 }
 
 // =========================================================== V: vocab ==
 template <uint32_t KV>
-__device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, const Ctx& c0, uint32_t& ph) {
+__device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, const Ctx& c0) {
     const Ctx c = fresh(c0);
     const Acts& a = A.a;
     const DevMat& mv = A.out;
     const uint32_t V = A.dm.vocab, ngrp = (V + kVocabRows - 1) / kVocabRows, cpr = c.H / 32;
+    const uint32_t tag = A.base + 6 * (A.l1 - A.l0) + 1;
     using Raw = typename Fmt<KV>::Raw;
     auto load_group = [&](Raw (&t)[kVocabRows], uint32_t gi) {
 #pragma unroll
@@ -741,10 +871,11 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
     float4 on = make_float4(0.f, 0.f, 0.f, 0.f);
     if (4 * c.tid < c.H) on = reinterpret_cast<const float4*>(A.onorm)[c.tid];
     QH_MARK(6, 0);
-    if (!wait_all(A, S, ph)) return;  // x after the last layer
-    QH_MARK(6, 1);
     float* xs = S.big;
-    load_norm_x(c, a.x, on, A.dm.eps, xs, S.red);
+    if (!gather_s(A, S, A.tx2, c.H, ptag(A, A.l1 - 1, 6), xs, c.tid, c.nwg, 0, c.rpw))
+        return;  // x after the last layer
+    QH_MARK(6, 1);
+    norm_in_lds(c, xs, on, A.dm.eps, S.red);
     float xa[16], xb[16], sa, sb;
     if (c.lane < cpr) x_runs<KV>(xs, c.lane, xa, xb, sa, sb);
     int32_t bk = INT32_MIN;
@@ -784,18 +915,21 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
         int32_t k0 = S.bk[0];
         uint32_t i0 = S.bi[0];
         for (int w = 1; w < kDW; w++) best_merge(k0, i0, S.bk[w], S.bi[w]);
-        st_sys_u(a.fin_key + c.b, (uint32_t)k0);
-        st_sys_u(a.fin_idx + c.b, i0);
+        put(A.tfin + 2 * c.b, __int_as_float(k0), tag);
+        put(A.tfin + 2 * c.b + 1, __uint_as_float(i0), tag);
         if (S.bad) atomicOr(&a.st->err, kErrLogits);
     }
-    signal(A, ++ph);
+    QH_MARK(6, 4);
     if (c.b != 0) return;
-    if (!wait_all(A, S, ph)) return;  // every workgroup's argmax partial
+    // workgroup 0: argmax over every workgroup's partial
+    float* fin = S.big + 2048;
+    if (!gather(A, S, A.tfin, 2 * c.nwg, tag, fin, c.tid)) return;
+    QH_MARK(6, 5);
     int32_t k1 = INT32_MIN;
     uint32_t i1 = 0xffffffffu;
     if (c.tid < c.nwg) {
-        k1 = (int32_t)ld_sys_u(a.fin_key + c.tid);
-        i1 = ld_sys_u(a.fin_idx + c.tid);
+        k1 = __float_as_int(fin[2 * c.tid]);
+        i1 = __float_as_uint(fin[2 * c.tid + 1]);
     }
     wave_best(k1, i1);
     if (c.lane == 0) {
@@ -854,29 +988,28 @@ __global__ __launch_bounds__(kDT) void k_decode(DecodeArgs A) {
     c.T = c.pos + 1;
     c.H = dm.hidden;
     c.E = dm.experts;
-    c.E1 = c.E + 1;
     c.top = dm.top;
     c.ff = dm.ff;
-    c.fp = pad32(dm.ff);
     c.G = dm.heads / dm.kvheads;
     c.qd = dm.heads * 128;
+    c.kvd = dm.kvheads * 128;
     c.ctx = dm.ctx;
     const uint32_t rpw = (c.H + c.nwg - 1) / c.nwg;
+    c.rpw = rpw;
     c.r0 = c.b * rpw;
     c.nr = c.r0 < c.H ? min(rpw, c.H - c.r0) : 0;
-    uint32_t ph = A.base;
     for (uint32_t l = A.l0; l < A.l1; l++) {
         const LayerW& L = A.layers[l];
-        const bool wait_x = l != A.l0;
         bool ok = true;
-        QH_DISPATCH_KM(L.v.kind, KV, ok = phase_qkv<Q4_K, KV>(A, S, L, c, wait_x, ph));
-        if (!ok || !phase_attn(A, S, L, c, ph)) return;
-        ok = phase_oproj<Q4_K>(A, S, L, c, ph);
-        if (!ok || !phase_fold(A, S, c, ph)) return;
-        QH_DISPATCH_KM(L.down.kind, KD, ok = phase_moe<Q4_K, KD>(A, S, L, c, ph));
+        QH_DISPATCH_KM(L.v.kind, KV, ok = phase_qkv<Q4_K, KV>(A, S, L, c, l));
+        if (!ok || !phase_attn(A, S, L, c, l)) return;
+        if (!phase_oproj<Q4_K>(A, S, L, c, l)) return;
+        const float s = phase_router(A, S, L, c, l);
+        if (s < 0.f) return;
+        QH_DISPATCH_KM(L.down.kind, KD, ok = phase_moe<Q4_K, KD>(A, S, L, c, l, s, l + 1 == A.l1));
         if (!ok) return;
     }
-    if (A.vocab) QH_DISPATCH_KM(A.out.kind, KV, phase_vocab<KV>(A, S, c, ph));
+    if (A.vocab) QH_DISPATCH_KM(A.out.kind, KV, phase_vocab<KV>(A, S, c));
 }
 
 }  // namespace qh

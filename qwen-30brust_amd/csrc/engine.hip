@@ -168,8 +168,9 @@ struct qh_ctx {
     bool persist_ok = false;  // the model's formats and shapes are covered
     bool persist = false;     // and it is enabled (QH_NO_PERSIST=1 or qh_set_persistent(0) disable it)
     uint32_t nwg = 0;         // workgroups of k_decode (one per CU)
-    uint32_t flag_base = 0;   // phase flags reached by the last launch
-    DevBuf layers_dev, sync_buf;
+    uint32_t flag_base = 0;   // tag of the last phase launched
+    DevBuf layers_dev, sync_buf;  // sync_buf: abort flag and tagged exchange words
+    size_t sync_bytes = 0;
     DecodeArgs dargs{};
 
     // launch geometry of the step kernels; per layer the held chunk slots
@@ -464,7 +465,9 @@ bool persist_supported(const qh_ctx* c, uint32_t nwg) {
     const uint32_t G = d.heads / d.kvheads, NWV = nwg * 8;
     auto km = [](uint32_t k) { return k == Q4_K || k == Q6_K; };
     if (!(d.head_dim == 128 && G >= 1 && G <= 8 && d.heads * 128 <= 4096 && d.kvheads * 32 <= nwg)) return false;
-    if (!(d.hidden % 256 == 0 && d.hidden <= 2048 && d.hidden <= 8 * nwg)) return false;
+    // every workgroup owns rows of x: the tagged exchange relies on it
+    const uint32_t rpw = (d.hidden + nwg - 1) / nwg;
+    if (!(d.hidden % 256 == 0 && d.hidden <= 2048 && rpw <= 8 && (nwg - 1) * rpw < d.hidden)) return false;
     if (!(d.experts <= 128 && d.experts + 1 <= nwg && d.top >= 1 && d.top <= 8)) return false;
     if (!(d.ff % 256 == 0 && (uint64_t)d.top * d.ff <= 3ull * NWV && d.top * (d.ff / 32) <= 192 &&
           d.top * pad32h(d.ff) <= 8192))
@@ -493,12 +496,6 @@ void setup_persist(qh_ctx* c) {
     const ModelDims& d = c->dm;
     c->layers_dev.alloc(c->layers.size() * sizeof(LayerW));
     HIP_OK(hipMemcpy(c->layers_dev.p, c->layers.data(), c->layers.size() * sizeof(LayerW), hipMemcpyHostToDevice));
-    // flags [nwg][32] | abort | rlog [E+1] | rpart [nwg][E+1]
-    const size_t flags_b = (size_t)nwg * 32 * 4, rlog_b = (size_t)(d.experts + 1) * 4;
-    const size_t total = flags_b + 256 + (rlog_b + 255) / 256 * 256 + (size_t)nwg * (d.experts + 1) * 4;
-    c->sync_buf.alloc(total);
-    HIP_OK(hipMemset(c->sync_buf.p, 0, total));
-    uint8_t* base = c->sync_buf.as<uint8_t>();
     DecodeArgs& A = c->dargs;
     A = DecodeArgs{};
     A.layers = c->layers_dev.as<const LayerW>();
@@ -508,23 +505,54 @@ void setup_persist(qh_ctx* c) {
     A.a = c->acts;
     A.dm = c->dm;
     A.max_chunks = c->max_chunks;
-    A.flags = reinterpret_cast<uint32_t*>(base);
-    A.abort_flag = reinterpret_cast<uint32_t*>(base + flags_b);
-    A.rlog = reinterpret_cast<float*>(base + flags_b + 256);
-    A.rpart = reinterpret_cast<float*>(base + flags_b + 256 + (rlog_b + 255) / 256 * 256);
+    // abort flag | tagged words of each exchange, every region 256-byte aligned
+    const uint64_t qd = (uint64_t)d.heads * 128, kvd = (uint64_t)d.kvheads * 128;
+    struct Region {
+        uint64_t words;
+        uint64_t** dst;
+    } regions[] = {
+        {d.hidden, &A.tx1},
+        {d.hidden, &A.tx2},
+        {qd + 2 * kvd, &A.tqkv},
+        {qd, &A.tatt},
+        {(uint64_t)d.heads * c->max_chunks * kPartWords, &A.tpart},
+        {d.experts, &A.tlog},
+        {(uint64_t)d.top * d.ff, &A.th},
+        {2ull * nwg, &A.tfin},
+    };
+    auto up256 = [](uint64_t b) { return (b + 255) / 256 * 256; };
+    size_t total = 256;
+    for (const Region& r : regions) total += up256((r.words + 1) * 8);
+    c->sync_buf.alloc(total);
+    c->sync_bytes = total;
+    HIP_OK(hipMemset(c->sync_buf.p, 0, total));
+    uint8_t* q = c->sync_buf.as<uint8_t>();
+    A.abort_flag = reinterpret_cast<uint32_t*>(q);
+    q += 256;
+    for (const Region& r : regions) {
+        *r.dst = reinterpret_cast<uint64_t*>(q);
+        q += up256((r.words + 1) * 8);
+    }
     c->flag_base = 0;
 }
 
 // One cooperative launch of k_decode over layers [l0, l1); vocab: also the
 // final norm, vocab projection, argmax and position advance.
 void launch_decode(qh_ctx* c, uint32_t l0, uint32_t l1, bool vocab) {
+    if (!(l0 < l1 && l1 <= c->layers.size())) throw Error("decode launch needs a non-empty layer range");
+    const uint32_t phases = 6 * (l1 - l0) + (vocab ? 1 : 0);
+    if (c->flag_base > 0xFFFFFFFFu - phases) {
+        // tags would wrap: clear every tagged word (no launch is reading them:
+        // this stream runs the launches in order) and start again from 0
+        HIP_OK(hipMemsetAsync(c->sync_buf.p, 0, c->sync_bytes, c->s));
+        c->flag_base = 0;
+    }
     DecodeArgs A = c->dargs;
     A.base = c->flag_base;
     A.l0 = l0;
     A.l1 = l1;
-    A.embed = 0;
     A.vocab = vocab ? 1u : 0u;
-    c->flag_base += 6 * (l1 - l0) + (vocab ? 2 : 0);
+    c->flag_base += phases;
     void* args[] = {&A};
     HIP_OK(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_decode), dim3(c->nwg), dim3(512), args, 0,
                                       c->s));

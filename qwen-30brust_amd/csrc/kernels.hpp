@@ -89,8 +89,11 @@ struct AttnArgs {
 };
 
 // Arguments of the persistent token-step kernel (decode.hip): layers
-// [l0, l1) of one token, optionally preceded by the embedding of tokens[pos]
-// and followed by the vocab projection, argmax and position advance.
+// [l0, l1) of one token, followed (vocab = 1) by the vocab projection, argmax
+// and position advance.  Workgroups hand values to each other as tagged
+// words: bits 63..32 carry the tag of the phase that wrote the value (base +
+// phase number), bits 31..0 the value; a reader waits for its tag.
+constexpr uint32_t kPartWords = 130;  // words per attention chunk partial: o[128], m, l
 struct DecodeArgs {
     const LayerW* layers;  // device array, one per layer
     DevMat emb, out;
@@ -98,12 +101,17 @@ struct DecodeArgs {
     Acts a;
     ModelDims dm;
     uint32_t max_chunks;   // attention chunks per KV head (<= 32)
-    uint32_t* flags;       // [gridDim.x * 32] per-workgroup phase flags
     uint32_t* abort_flag;  // set when a wait times out; every wait then returns
-    float* rlog;           // [experts + 1] folded router logits, then the RMS scale
-    float* rpart;          // [gridDim.x][experts + 1] router partial dots + sum of squares
-    uint32_t base;         // flag value before this launch's first phase
-    uint32_t l0, l1, embed, vocab;
+    uint64_t* tx1;         // [hidden]  x after attention (x')
+    uint64_t* tx2;         // [hidden]  x after the MoE block (x'')
+    uint64_t* tqkv;        // [heads*d + 2*kvheads*d] q | k | v projections
+    uint64_t* tatt;        // [heads*d] attention output
+    uint64_t* tpart;       // [heads][max_chunks][d + 2] attention chunk partials (o, m, l)
+    uint64_t* tlog;        // [experts] router logits
+    uint64_t* th;          // [top][ff] SwiGLU outputs
+    uint64_t* tfin;        // [gridDim.x][2] vocab argmax partials (key, index)
+    uint32_t base;         // tag before this launch's first phase
+    uint32_t l0, l1, vocab;
 };
 
 }  // namespace qh
