@@ -296,12 +296,67 @@ __device__ __forceinline__ uint32_t ptag(const DecodeArgs& A, uint32_t l, uint32
     return A.base + 6 * (l - A.l0) + k;
 }
 
+// Chunk geometry of the attention workgroups: KV head g = b / 32, chunk
+// b % 32; a chunk covers >= 64 keys, at most max_chunks chunks per head.
+struct AttnChunk {
+    uint32_t nch, g, ch, t0, t1;
+    bool active;
+};
+__device__ __forceinline__ AttnChunk attn_chunk(const DecodeArgs& A, const Ctx& c) {
+    AttnChunk k;
+    k.nch = min((c.T + kDTile - 1) / kDTile, A.max_chunks);
+    k.g = c.b / kDChunks;
+    k.ch = c.b % kDChunks;
+    k.active = k.g < A.dm.kvheads && k.ch < k.nch;
+    const uint32_t tc = (c.T + k.nch - 1) / k.nch;
+    k.t0 = min(c.T, k.ch * tc);
+    k.t1 = min(c.T, k.t0 + tc);
+    return k;
+}
+
+// What an attention workgroup loads before it has q/k/v: the first K/V
+// slice of its chunk, the q/k norm weights and the rotary table row.
+struct AttnPre {
+    float4 kr[4], vr[4];
+    float qw0, qw1, kw0, kw1;
+    float2 cs;
+};
+
+__device__ __forceinline__ void kv_slice(float4 (&kr)[4], float4 (&vr)[4], const float* kc, const float* vc,
+                                         uint32_t g, uint32_t ctx, uint32_t tt, uint32_t t1, uint32_t pos,
+                                         uint32_t tid) {
+    const uint32_t key = tt + (tid >> 3), j = (tid & 7) * 16;
+    if (key < t1 && key != pos) {
+        const float* ks = kc + ((size_t)g * ctx + key) * 128 + j;
+        const float* vs = vc + ((size_t)g * ctx + key) * 128 + j;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            kr[i] = gld<float4>(ks + 4 * i);
+            vr[i] = gld<float4>(vs + 4 * i);
+        }
+    }
+}
+
+// Issued by attention workgroups in phase A, before they wait for x.
+__device__ __forceinline__ void attn_prefetch(const DecodeArgs& A, const LayerW& L, const Ctx& c, AttnPre& P) {
+    const AttnChunk k = attn_chunk(A, c);
+    if (!k.active) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++) P.kr[i] = P.vr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    kv_slice(P.kr, P.vr, L.kcache, L.vcache, k.g, c.ctx, k.t0, k.t1, c.pos, c.tid);
+    P.qw0 = gld<float>(L.q_norm + c.lane);
+    P.qw1 = gld<float>(L.q_norm + c.lane + 64);
+    P.kw0 = gld<float>(L.k_norm + c.lane);
+    P.kw1 = gld<float>(L.k_norm + c.lane + 64);
+    P.cs = gld<float2>(A.a.rope + (size_t)c.pos * 64 + c.lane);
+}
+
 // ================================================================== A: qkv ==
 // Flat rows [q | k | v]; wave gw owns rows gw, gw + NWV, gw + 2 NWV.  q and k
 // share format KQ, v has KV.  Rows have H <= 2048 columns: lane = chunk.
 template <uint32_t KQ, uint32_t KV>
 __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
-                                          uint32_t l) {
+                                          uint32_t l, AttnPre& P) {
     const Ctx c = fresh(c0);
     const uint32_t nq = L.q.rows, nk = L.k.rows, nt = nq + nk + L.v.rows, cpr = c.H / 32;
     typename Fmt<KQ>::Raw wq[kQkvPerWave];
@@ -317,7 +372,8 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
         }
     }
     float4 nw = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (4 * c.tid < c.H) nw = reinterpret_cast<const float4*>(L.attn_norm)[c.tid];
+    if (4 * c.tid < c.H) nw = gld<float4>(L.attn_norm + 4 * c.tid);
+    attn_prefetch(A, L, c, P);
     float* xs = S.big;
     QH_MARK(0, 0);
     if (l == A.l0) {
@@ -375,45 +431,21 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
 // Chunks > 0 pass their partial (o[128], m, l) on as tagged words; chunk 0
 // merges them (each half of a wave takes half of the chunks, 8 per round of
 // loads), or with a single chunk writes the output directly.
-__device__ __forceinline__ void kv_slice(float4 (&kr)[4], float4 (&vr)[4], const float* kc, const float* vc,
-                                         uint32_t g, uint32_t ctx, uint32_t tt, uint32_t t1, uint32_t pos,
-                                         uint32_t tid) {
-    const uint32_t key = tt + (tid >> 3), j = (tid & 7) * 16;
-    if (key < t1 && key != pos) {
-        const float4* ks = reinterpret_cast<const float4*>(kc + ((size_t)g * ctx + key) * 128 + j);
-        const float4* vs = reinterpret_cast<const float4*>(vc + ((size_t)g * ctx + key) * 128 + j);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            kr[i] = ks[i];
-            vr[i] = vs[i];
-        }
-    }
-}
-
 __device__ __forceinline__ float shfl32(float v) { return __shfl_xor(v, 32, 64); }
 
 __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
-                                           uint32_t l) {
+                                           uint32_t l, AttnPre& P) {
     const Ctx c = fresh(c0);
-    const Acts& a = A.a;
     const ModelDims& dm = A.dm;
-    const uint32_t nch = min((c.T + kDTile - 1) / kDTile, A.max_chunks);
-    const uint32_t g = c.b / kDChunks, ch = c.b % kDChunks;
-    if (!(g < dm.kvheads && ch < nch)) return true;  // not an attention workgroup this step
+    const AttnChunk k = attn_chunk(A, c);
+    if (!k.active) return true;  // not an attention workgroup this step
+    const uint32_t nch = k.nch, g = k.g, ch = k.ch, t0 = k.t0, t1 = k.t1;
     const uint32_t tid = c.tid, wv = c.wv, lane = c.lane, G = c.G, pos = c.pos, ctx = c.ctx;
-    const uint32_t tc = (c.T + nch - 1) / nch;
-    const uint32_t t0 = min(c.T, ch * tc), t1 = min(c.T, t0 + tc);
     const bool holds = t0 <= pos && pos < t1;
     const uint32_t tag_in = ptag(A, l, 1), tag = ptag(A, l, 2);
-    QH_MARK(1, 5);
-    float4 kr[4], vr[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) kr[i] = vr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    kv_slice(kr, vr, L.kcache, L.vcache, g, ctx, t0, t1, pos, tid);
-    QH_MARK(1, 6);
-    const float qw0 = L.q_norm[lane], qw1 = L.q_norm[lane + 64];
-    const float kw0 = L.k_norm[lane], kw1 = L.k_norm[lane + 64];
-    const float2 cs = a.rope[(size_t)pos * 64 + lane];
+    float4(&kr)[4] = P.kr;
+    float4(&vr)[4] = P.vr;
+    const float2 cs = P.cs;
     // Wave w: q head w (w < G); the new key by wave G % 8; the new value by
     // wave 7.  Lane l holds elements l and l + 64 (the rotated pair).
     const bool hasq = wv < G, hask = wv == G % kDW, hasv = wv == kDW - 1;
@@ -450,8 +482,8 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
             L.kcache[((size_t)g * ctx + pos) * 128 + lane + 64] = o1;
         }
     };
-    if (hasq) norm_rope(qa, qb, qw0, qw1, qs + wv * 160, false);
-    if (hask) norm_rope(ka, kb, kw0, kw1, kn, holds);
+    if (hasq) norm_rope(qa, qb, P.qw0, P.qw1, qs + wv * 160, false);
+    if (hask) norm_rope(ka, kb, P.kw0, P.kw1, kn, holds);
     if (hasv) {
         vn[lane] = va;
         vn[lane + 64] = vb;
@@ -671,8 +703,8 @@ __device__ __forceinline__ float phase_router(const DecodeArgs& A, DecodeLds& S,
     const bool rt = c.b < c.E;
     float4 wr = make_float4(0.f, 0.f, 0.f, 0.f), fw = make_float4(0.f, 0.f, 0.f, 0.f);
     if (rt && 4 * c.tid < c.H) {
-        wr = reinterpret_cast<const float4*>(L.router.w + (size_t)c.b * L.router.drb)[c.tid];
-        fw = reinterpret_cast<const float4*>(L.ffn_norm)[c.tid];
+        wr = gld<float4>(L.router.w + (size_t)c.b * L.router.drb + 16 * c.tid);
+        fw = gld<float4>(L.ffn_norm + 4 * c.tid);
     }
     QH_MARK(3, 0);
     float* xs = S.big;
@@ -698,7 +730,7 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
     const Acts& a = A.a;
     const uint32_t E = c.E, top = c.top, ff = c.ff, H = c.H, cpr = H / 32;
     float4 fn = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (4 * c.tid < H) fn = reinterpret_cast<const float4*>(L.ffn_norm)[c.tid];
+    if (4 * c.tid < H) fn = gld<float4>(L.ffn_norm + 4 * c.tid);
     QH_MARK(4, 0);
     if (!gather(A, S, A.tlog, E, ptag(A, l, 4), S.lg, c.tid)) return false;  // router logits (phase D)
     QH_MARK(4, 1);
@@ -760,6 +792,19 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
             wu[k] = Fmt<KG>::load(L.up.w + (size_t)ex * L.up.expert_stride + (size_t)rr * L.up.drb, L.up.geo, c.lane);
         }
     }
+    // down rows of phase F (row r0 + wv of each routed expert), requested
+    // with the gate/up rows: lane units u = lane + 64 i = (slot u / dcpr, chunk u % dcpr)
+    const uint32_t dcpr = ff / 32, U = top * dcpr;
+    typename Fmt<KD>::Raw wd[kDownUnits];
+#pragma unroll
+    for (uint32_t i = 0; i < kDownUnits; i++) {
+        const uint32_t u = c.lane + 64 * i;
+        if (c.wv < c.nr && u < U) {
+            const uint8_t* drow = L.down.w + (size_t)S.ids[u / dcpr] * L.down.expert_stride +
+                                  (size_t)(c.r0 + c.wv) * L.down.drb;
+            wd[i] = Fmt<KD>::load(drow, L.down.geo, u % dcpr);
+        }
+    }
     // xn = x' * (s * ffn_norm), in place (each thread rewrites its own float4)
     float* xs = S.big;
     if (4 * c.tid < H) {
@@ -806,19 +851,6 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         // this workgroup's outputs [slot][ff] flat at b * kHBlock, one store instruction
         const uint32_t i = c.b * kHBlock + c.tid;
         if (c.tid < kHBlock && i < top * ff) put(A.th + i, S.hv[c.tid], tag_h);
-    }
-    // down rows of phase F (row r0 + wv of each routed expert), requested
-    // before the wait: lane units u = lane + 64 i = (slot u / dcpr, chunk u % dcpr)
-    const uint32_t dcpr = ff / 32, U = top * dcpr;
-    typename Fmt<KD>::Raw wd[kDownUnits];
-#pragma unroll
-    for (uint32_t i = 0; i < kDownUnits; i++) {
-        const uint32_t u = c.lane + 64 * i;
-        if (c.wv < c.nr && u < U) {
-            const uint8_t* drow = L.down.w + (size_t)S.ids[u / dcpr] * L.down.expert_stride +
-                                  (size_t)(c.r0 + c.wv) * L.down.drb;
-            wd[i] = Fmt<KD>::load(drow, L.down.geo, u % dcpr);
-        }
     }
     QH_MARK(4, 3);
     // ================================================ F: down + combine
@@ -869,7 +901,7 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
     Raw cur[kVocabRows], nxt[kVocabRows];
     load_group(cur, c.gw);
     float4 on = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (4 * c.tid < c.H) on = reinterpret_cast<const float4*>(A.onorm)[c.tid];
+    if (4 * c.tid < c.H) on = gld<float4>(A.onorm + 4 * c.tid);
     QH_MARK(6, 0);
     float* xs = S.big;
     if (!gather_s(A, S, A.tx2, c.H, ptag(A, A.l1 - 1, 6), xs, c.tid, c.nwg, 0, c.rpw))
@@ -999,10 +1031,13 @@ __global__ __launch_bounds__(kDT) void k_decode(DecodeArgs A) {
     c.r0 = c.b * rpw;
     c.nr = c.r0 < c.H ? min(rpw, c.H - c.r0) : 0;
     for (uint32_t l = A.l0; l < A.l1; l++) {
-        const LayerW& L = A.layers[l];
+        // read through the constant address space: scalar loads, which do
+        // not wait behind this wave's outstanding vector loads and stores
+        const LayerW& L = *(const LayerW*)((const __attribute__((address_space(4))) LayerW*)A.layers + l);
         bool ok = true;
-        QH_DISPATCH_KM(L.v.kind, KV, ok = phase_qkv<Q4_K, KV>(A, S, L, c, l));
-        if (!ok || !phase_attn(A, S, L, c, l)) return;
+        AttnPre P;
+        QH_DISPATCH_KM(L.v.kind, KV, ok = phase_qkv<Q4_K, KV>(A, S, L, c, l, P));
+        if (!ok || !phase_attn(A, S, L, c, l, P)) return;
         if (!phase_oproj<Q4_K>(A, S, L, c, l)) return;
         const float s = phase_router(A, S, L, c, l);
         if (s < 0.f) return;

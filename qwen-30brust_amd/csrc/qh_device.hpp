@@ -42,10 +42,22 @@ __device__ __forceinline__ void kscale(uint32_t s0, uint32_t s1, uint32_t s2, ui
     }
 }
 
-__device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
-__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
-    return *reinterpret_cast<const uint16_t*>(p);
+// Loads from device memory through global-address-space pointers: they
+// compile to global_load (counted by vmcnt only).  A load through a generic
+// pointer of unknown origin compiles to flat_load, which also counts in
+// lgkmcnt, so every later LDS wait would wait for it as well.
+template <typename T>
+using gptr = const __attribute__((address_space(1))) T*;
+template <typename T>
+__device__ __forceinline__ T gld(const void* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return *(gptr<T>)p;
+#else
+    return *static_cast<const T*>(p);  // host pass: never executed
+#endif
 }
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) { return gld<uint4>(p); }
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return gld<uint16_t>(p); }
 
 // Hides a value from the optimiser's known-bits analysis, so that byte k of a
 // pre-masked word still converts with one v_cvt_f32_ubyte<k> instead of a
@@ -158,7 +170,7 @@ template <> struct Fmt<Q6_K> {
         uint32_t b = c >> 3, j = c & 7;
         return {ld16(row + g.off_a + b * 128 + j * 16),
                 ld16(row + g.off_b + b * 64 + (j >> 2) * 32 + (j & 1) * 16),
-                *reinterpret_cast<const uint2*>(row + g.off_c + b * 16 + (j >> 2) * 8),
+                gld<uint2>(row + g.off_c + b * 16 + (j >> 2) * 8),
                 ld_u16(row + g.off_d + b * 2)};
     }
     static __device__ __forceinline__ float dot(const Raw& r, uint32_t c, const float* xa,
@@ -261,10 +273,9 @@ template <> struct Fmt<F32> {
     static __device__ __forceinline__ uint32_t xoff_a(uint32_t c) { return c * 32; }
     static __device__ __forceinline__ uint32_t xoff_b(uint32_t c) { return c * 32 + 16; }
     static __device__ __forceinline__ Raw load(const uint8_t* row, const RowGeo&, uint32_t c) {
-        const float4* p = reinterpret_cast<const float4*>(row + c * 128);
         Raw r;
 #pragma unroll
-        for (int k = 0; k < 8; k++) r.v[k] = p[k];
+        for (int k = 0; k < 8; k++) r.v[k] = gld<float4>(row + c * 128 + 16 * k);
         return r;
     }
     static __device__ __forceinline__ float dot(const Raw& r, uint32_t, const float* xa,
