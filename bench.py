@@ -159,7 +159,7 @@ def main():
         del src, dst
 
     alt_warmup, alt_steps = 4, 32
-    ctx = args.prompt + args.warmup + args.steps + args.profile_steps + alt_warmup + alt_steps + 8
+    ctx = args.prompt + args.warmup + args.steps + 2 * args.profile_steps + alt_warmup + alt_steps + 8
     spec = synth.qwen30b(layers=args.layers, context=max(4096, ctx))
     threads = min(16, os.cpu_count() or 1)
     t0 = time.time()
@@ -182,7 +182,13 @@ def main():
     log(f"decode: {ms_per_step:.3f} ms/token, {tok_s:.1f} tok/s")
 
     persistent = model.persistent
-    pos_mid = pos_start + args.warmup + args.steps
+    decode_launch = None
+    if persistent:
+        # the k_decode launch alone, timed with HIP events on its stream
+        ms_embed, ms_decode = model.profile_decode(args.profile_steps)
+        decode_launch = {"ms_embed": round(ms_embed, 4), "ms_decode": round(ms_decode, 4)}
+        log(f"persistent step: k_embed {ms_embed*1e3:.1f} us, k_decode {ms_decode*1e3:.1f} us per token")
+    pos_mid = pos_start + args.warmup + args.steps + (args.profile_steps if persistent else 0)
     # the per-phase kernels: timed as a second line, and profiled one kernel
     # class at a time (HIP events between direct launches)
     model.persistent = False
@@ -199,8 +205,9 @@ def main():
         # one k_decode launch (plus the 1-WG embedding kernel) per token: its
         # algorithmic bytes are the whole token's (weights + KV + activations)
         dom = "decode_step"
-        per_launch_bytes = sum(bytes_cls.values())
-        per_launch_ms = ms_per_step
+        pos_dec = pos_start + args.warmup + args.steps + args.profile_steps / 2
+        per_launch_bytes = sum(algorithmic_bytes(model, pos_dec).values())
+        per_launch_ms = decode_launch["ms_decode"]
     else:
         dom = max(breakdown, key=breakdown.get)
         launches = 1 if dom in ("vocab", "finish") else args.layers
@@ -239,6 +246,7 @@ def main():
                              "GB_s": round(w_active * tok_s / 1e9, 1),
                              "frac": round(w_active * tok_s / 1e9 / HBM_PEAK_GBS, 4)},
         "step": "persistent k_decode (one launch per token)" if persistent else "per-phase kernels",
+        "decode_launch": decode_launch,
         "per_phase_kernels": {"ms_per_token": round(ms_alt, 4), "tok_s": round(1000.0 / ms_alt, 2),
                               "breakdown": classes},
         "matvec": matvec,

@@ -141,6 +141,13 @@ int qh_persistent(const qh_ctx *ctx, int *out);
  * kernels).  Enabling fails when the model is not covered. */
 int qh_set_persistent(qh_ctx *ctx, int enable);
 
+/* Persistent-step timing (no counterpart in the reference): `steps` decode
+ * steps continuing from the current position, with HIP events on the
+ * context's stream around each kernel of the step; ms_embed / ms_decode
+ * receive the mean milliseconds of the embedding kernel and of the one
+ * k_decode launch per token.  Fails unless the persistent step is selected. */
+int qh_profile_decode(qh_ctx *ctx, size_t steps, double *ms_embed, double *ms_decode);
+
 /* Benchmark surface: `warmup` untimed then `steps` timed greedy decode steps
  * continuing from the current position, timed with HIP events on the
  * context's stream.  ms_total receives the timed milliseconds. */

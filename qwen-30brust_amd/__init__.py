@@ -75,6 +75,7 @@ _SIGS = {
     "qh_bench_decode": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(C.c_double)]),
     "qh_persistent": (C.c_int, [C.c_void_p, C.POINTER(C.c_int)]),
     "qh_set_persistent": (C.c_int, [C.c_void_p, C.c_int]),
+    "qh_profile_decode": (C.c_int, [C.c_void_p, C.c_size_t, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "qh_profile_step": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]),
     "qh_bench_matvec": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint32, C.c_size_t,
                                   C.c_size_t, C.c_size_t, C.c_size_t, C.POINTER(C.c_double)]),
@@ -255,6 +256,13 @@ class Model:
     @persistent.setter
     def persistent(self, enable):
         self.dev._check(lib().qh_set_persistent(self.dev.h, 1 if enable else 0))
+
+    def profile_decode(self, steps):
+        """Mean GPU ms of (the embedding kernel, the k_decode launch) per token
+        of the persistent step, from HIP events around each kernel."""
+        e, d = C.c_double(), C.c_double()
+        self.dev._check(lib().qh_profile_decode(self.dev.h, steps, C.byref(e), C.byref(d)))
+        return e.value, d.value
 
     def bench_decode(self, warmup, steps):
         ms = C.c_double()

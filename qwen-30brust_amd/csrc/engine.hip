@@ -1076,6 +1076,39 @@ int qh_set_persistent(qh_ctx* c, int enable) {
     });
 }
 
+int qh_profile_decode(qh_ctx* c, size_t steps, double* ms_embed, double* ms_decode) {
+    return guarded(c, [&] {
+        need_model(c);
+        if (!c->persist) throw Error("profile_decode times the persistent step: it is not selected");
+        if (c->pos == 0) throw Error("profile_decode continues a sequence: run a prompt first");
+        if (c->pos + steps > c->context) throw Error("prompt + max-tokens exceed --ctx");
+        hipEvent_t ev[3];
+        for (auto& e : ev) HIP_OK(hipEventCreate(&e));
+        double acc[2] = {0.0, 0.0};
+        put_state(c, (uint32_t)c->pos, (uint32_t)c->pos);
+        for (size_t s = 0; s < steps; s++) {
+            HIP_OK(hipEventRecord(ev[0], c->s));
+            hipLaunchKernelGGL(k_embed, dim3(1), dim3(kBlock), 0, c->s, c->emb, c->acts, c->dm);
+            HIP_OK(hipEventRecord(ev[1], c->s));
+            launch_decode(c, 0, (uint32_t)c->layers.size(), true);
+            HIP_OK(hipEventRecord(ev[2], c->s));
+            HIP_OK(hipEventSynchronize(ev[2]));
+            for (int k = 0; k < 2; k++) {
+                float ms = 0;
+                HIP_OK(hipEventElapsedTime(&ms, ev[k], ev[k + 1]));
+                acc[k] += ms;
+            }
+        }
+        for (auto& e : ev) (void)hipEventDestroy(e);
+        DevState st = get_state(c);
+        if (st.err) fail_step(c, st.err);
+        c->pos += steps;
+        c->stats.matvecs += matvecs_per_token(c) * steps;
+        *ms_embed = acc[0] / (double)steps;
+        *ms_decode = acc[1] / (double)steps;
+    });
+}
+
 int qh_bench_decode(qh_ctx* c, size_t warmup, size_t steps, double* ms_total) {
     return guarded(c, [&] {
         need_model(c);

@@ -175,11 +175,12 @@ def layer30b_q4k():
     return spec, img
 
 
-@pytest.mark.parametrize("pos", [0, 1, 31, 32, 33, 200, 700])
+@pytest.mark.parametrize("pos", [0, 1, 63, 64, 65, 700, 1100, 2047])
 def test_persistent_layer_attention_chunking(dev, layer30b_q4k, pos):
     """The persistent step at positions that exercise the attention split: one
-    key, one chunk, chunk boundaries (32 keys per chunk), and up to 22
-    chunks merged per KV head; against the oracle layer."""
+    key, one chunk, chunk boundaries (64-key tiles, at least 64 keys per
+    chunk), 11 chunks per KV head (one merge round), 18 (both halves of the
+    merging wave, two rounds) and 32 (the most); against the oracle layer."""
     spec, img = layer30b_q4k
     om = oracle.Model(oracle.Gguf(img), spec.context)
     m = engine.Model(img, spec.context, device=dev)
@@ -220,3 +221,19 @@ def test_greedy_30b_token_loop_matches_oracle(dev):
         print(f"step {i}: oracle {ref_ids[-1]} device {int(got[i])} margin {margins[-1]:.3e}", flush=True)
     print(f"smallest top-1/top-2 margin {min(margins):.3e}")
     assert list(got) == ref_ids
+
+
+def test_persistent_profile_decode(dev, layer30b_q4k):
+    """qh_profile_decode times the embedding kernel and the k_decode launch of
+    each step and advances the position by one per step, like qh_forward."""
+    spec, img = layer30b_q4k
+    m = engine.Model(img, spec.context, device=dev)
+    assert m.persistent
+    m.generate(np.array([3, 17, 5], np.uint32), 1)
+    pos = m.position
+    e, d = m.profile_decode(4)
+    assert e > 0 and d > 0
+    assert m.position == pos + 4
+    m.persistent = False
+    with pytest.raises(engine.EngineError):
+        m.profile_decode(1)
