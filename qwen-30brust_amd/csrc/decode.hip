@@ -765,20 +765,18 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         }
     }
     __syncthreads();
-    // softmax over the selected logits, in order (ops.rs:29-44)
-    if (c.tid < top) {
-        float mx = -INFINITY;
-        for (uint32_t i = 0; i < top; i++) mx = fmaxf(mx, S.sv[i]);
-        S.ex[c.tid] = expf(S.sv[c.tid] - mx);
-        S.ids[c.tid] = S.sid[c.tid];
+    // softmax over the selected logits (ops.rs:29-44) on wave 0, lane k = rank k
+    if (c.wv == 0) {  // wave-uniform
+        const float v = c.lane < top ? S.sv[c.lane] : -INFINITY;
+        const float mx = wave_max(v);
+        const float e = c.lane < top ? expf(v - mx) : 0.f;
+        const float sum = wave_sum(e);
+        if (c.lane < top) {
+            S.ids[c.lane] = S.sid[c.lane];
+            S.wts[c.lane] = e / sum;
+        }
     }
     __syncthreads();
-    if (c.tid < top) {
-#pragma clang fp contract(off)
-        float sum = 0.f;
-        for (uint32_t i = 0; i < top; i++) sum += S.ex[i];
-        S.wts[c.tid] = S.ex[c.tid] / sum;
-    }
     QH_MARK(4, 2);
     // gate/up rows of pairs p = gw*3 + k: (slot p / ff, row p % ff)
     typename Fmt<KG>::Raw wg[kPairsPerWave], wu[kPairsPerWave];
@@ -790,19 +788,6 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
             wg[k] = Fmt<KG>::load(L.gate.w + (size_t)ex * L.gate.expert_stride + (size_t)rr * L.gate.drb, L.gate.geo,
                                   c.lane);
             wu[k] = Fmt<KG>::load(L.up.w + (size_t)ex * L.up.expert_stride + (size_t)rr * L.up.drb, L.up.geo, c.lane);
-        }
-    }
-    // down rows of phase F (row r0 + wv of each routed expert), requested
-    // with the gate/up rows: lane units u = lane + 64 i = (slot u / dcpr, chunk u % dcpr)
-    const uint32_t dcpr = ff / 32, U = top * dcpr;
-    typename Fmt<KD>::Raw wd[kDownUnits];
-#pragma unroll
-    for (uint32_t i = 0; i < kDownUnits; i++) {
-        const uint32_t u = c.lane + 64 * i;
-        if (c.wv < c.nr && u < U) {
-            const uint8_t* drow = L.down.w + (size_t)S.ids[u / dcpr] * L.down.expert_stride +
-                                  (size_t)(c.r0 + c.wv) * L.down.drb;
-            wd[i] = Fmt<KD>::load(drow, L.down.geo, u % dcpr);
         }
     }
     // xn = x' * (s * ffn_norm), in place (each thread rewrites its own float4)
@@ -851,6 +836,19 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         // this workgroup's outputs [slot][ff] flat at b * kHBlock, one store instruction
         const uint32_t i = c.b * kHBlock + c.tid;
         if (c.tid < kHBlock && i < top * ff) put(A.th + i, S.hv[c.tid], tag_h);
+    }
+    // down rows of phase F (row r0 + wv of each routed expert), requested
+    // before the wait for the SwiGLU outputs: lane units u = lane + 64 i = (slot u / dcpr, chunk u % dcpr)
+    const uint32_t dcpr = ff / 32, U = top * dcpr;
+    typename Fmt<KD>::Raw wd[kDownUnits];
+#pragma unroll
+    for (uint32_t i = 0; i < kDownUnits; i++) {
+        const uint32_t u = c.lane + 64 * i;
+        if (c.wv < c.nr && u < U) {
+            const uint8_t* drow = L.down.w + (size_t)S.ids[u / dcpr] * L.down.expert_stride +
+                                  (size_t)(c.r0 + c.wv) * L.down.drb;
+            wd[i] = Fmt<KD>::load(drow, L.down.geo, u % dcpr);
+        }
     }
     QH_MARK(4, 3);
     // ================================================ F: down + combine
