@@ -123,6 +123,20 @@ int qh_reset(qh_ctx *ctx);
 /* == Model::position (src/model.rs:170). */
 int qh_position(const qh_ctx *ctx, size_t *out);
 
+/* Batched prefill of `n` prompt tokens from the current position: replaces
+ * the sequential prompt loop of src/main.rs:250-256 (one Model::forward per
+ * prompt token, src/model.rs:209-302) with layer-at-a-time fp16 matrix-core
+ * GEMMs and a causal flash-attention pass, in chunks of up to 2048 tokens.
+ * Fills the KV cache for those positions, writes the greedy id after the
+ * last prompt token to the device token ring (so qh_forward / qh_generate
+ * continue from it), advances the position by n.  logits (vocab floats) and
+ * argmax (nullable) receive the last prompt token's output.  Numerics: fp16
+ * operands with fp32 accumulation (logits within about 1e-2 relative of the
+ * FP32 path); fails for models it does not cover (head_dim != 128, more than
+ * 8 query heads per KV head, more than 128 experts, projections other than
+ * Q4_K/Q6_K). */
+int qh_prefill(qh_ctx *ctx, const uint32_t *prompt, size_t n, float *logits, uint32_t *argmax);
+
 /* One decoder layer (the loop body src/model.rs:227-287) applied to x[hidden]
  * in place at position `pos`, with this layer's KV history replaced by
  * kprev/vprev (time-major, `pos` positions).  ids/w (nullable) receive the

@@ -76,6 +76,7 @@ _SIGS = {
     "qh_persistent": (C.c_int, [C.c_void_p, C.POINTER(C.c_int)]),
     "qh_set_persistent": (C.c_int, [C.c_void_p, C.c_int]),
     "qh_profile_decode": (C.c_int, [C.c_void_p, C.c_size_t, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "qh_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.POINTER(C.c_uint32)]),
     "qh_profile_step": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]),
     "qh_bench_matvec": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint32, C.c_size_t,
                                   C.c_size_t, C.c_size_t, C.c_size_t, C.POINTER(C.c_double)]),
@@ -226,6 +227,15 @@ class Model:
         lg = np.empty(self.config["vocab"], np.float32) if want_logits else None
         self.dev._check(lib().qh_generate(self.dev.h, _ptr(p), p.size, n_new, _ptr(out), _ptr(lg)))
         return (out[:n_new], lg) if want_logits else out[:n_new]
+
+    def prefill(self, prompt, want_logits=True):
+        """Batched prefill of `prompt` from the current position (fp16 matrix
+        cores); returns (greedy id, logits of the last prompt token)."""
+        p = np.ascontiguousarray(prompt, np.uint32)
+        lg = np.empty(self.config["vocab"], np.float32) if want_logits else None
+        am = C.c_uint32()
+        self.dev._check(lib().qh_prefill(self.dev.h, _ptr(p), p.size, _ptr(lg), C.byref(am)))
+        return am.value, lg
 
     def layer_forward(self, layer, x, pos, kprev, vprev):
         x = np.array(x, np.float32)

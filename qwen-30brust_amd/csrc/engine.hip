@@ -44,6 +44,21 @@ __global__ void k_finish(Acts, ModelDims, uint32_t);
 // Persistent token step (decode.hip).
 __global__ void k_embed(DevMat, Acts, ModelDims);
 __global__ void k_decode(DecodeArgs);
+// Batched prefill (prefill.hip).
+template <uint32_t K> __global__ void k_gemm(const _Float16*, uint32_t, uint32_t, DevMat, float*, uint32_t, uint32_t);
+template <uint32_t K> __global__ void k_gemm_gateup(const _Float16*, uint32_t, ExpertTiles, DevMat, DevMat, _Float16*);
+template <uint32_t K> __global__ void k_gemm_down(const _Float16*, ExpertTiles, DevMat, float*);
+__global__ void k_pf_embed(DevMat, const uint32_t*, uint32_t, uint32_t, float*, DevState*);
+__global__ void k_pf_norm(const float*, const float*, uint32_t, float, _Float16*, float*);
+__global__ void k_pf_qkrope(const float*, const float*, const float*, const float2*, uint32_t, uint32_t, uint32_t,
+                            uint32_t, uint32_t, float, _Float16*, float*, float*);
+__global__ void k_pf_attn(const _Float16*, const float*, const float*, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t,
+                          _Float16*);
+__global__ void k_pf_router(const float*, DevMat, uint32_t, uint32_t, uint32_t, float*);
+__global__ void k_pf_topk(const float*, uint32_t, uint32_t, uint32_t, uint32_t*, float*, DevState*);
+__global__ void k_pf_group(const uint32_t*, uint32_t, uint32_t, uint32_t, uint32_t*, uint32_t*, uint32_t*, uint32_t*,
+                           uint32_t*, uint32_t*);
+__global__ void k_pf_combine(float*, const float*, const float*, uint32_t, uint32_t);
 }  // namespace qh
 
 using namespace qh;
@@ -180,6 +195,17 @@ struct qh_ctx {
     int vocab_slots = 0;
     size_t lds_h = 0, lds_attn = 0, lds_o = 0, lds_gu = 0, lds_down = 0;
 
+    // batched prefill: buffers for chunks of up to pf_cap tokens
+    struct Prefill {
+        uint32_t cap = 0;
+        DevBuf buf;
+        float *X = nullptr, *Xn32 = nullptr, *QKV = nullptr, *LR = nullptr, *wts = nullptr, *Y = nullptr;
+        _Float16 *Xn16 = nullptr, *Q16 = nullptr, *O16 = nullptr, *Hs = nullptr;
+        uint32_t *ids = nullptr, *goff = nullptr, *tok = nullptr, *asg = nullptr, *te = nullptr, *tm = nullptr,
+                 *ntile = nullptr;
+        uint32_t max_tiles = 0;
+    } pf;
+
     // scratch for the API surfaces
     DevBuf sa, sb, sc, sd;
     HostPinned pin;
@@ -195,6 +221,8 @@ struct qh_ctx {
         layers.clear();
         attn.clear();
         acts_buf.release();
+        pf.buf.release();
+        pf.cap = 0;
         layers_dev.release();
         sync_buf.release();
         persist_ok = persist = false;
@@ -708,6 +736,113 @@ void reset_model(qh_ctx* c) {
 
 uint64_t matvecs_per_token(const qh_ctx* c) { return c->cfg.layers * (5 + 3 * c->cfg.top) + 1; }
 
+// ------------------------------------------------------------ prefill --
+constexpr uint32_t kPrefillChunk = 2048;  // most prompt tokens per batched pass
+
+// Whether the batched prefill covers the model: head_dim 128 with at most 8
+// query heads per KV head, at most 128 experts, F32 router, and every
+// projection Q4_K or Q6_K with column counts in 64-column slices.
+std::string prefill_gap(const qh_ctx* c) {
+    const ModelDims& d = c->dm;
+    auto km = [](uint32_t k) { return k == Q4_K || k == Q6_K; };
+    if (d.head_dim != 128) return "head_dim " + std::to_string(d.head_dim) + " (needs 128)";
+    if (d.heads % d.kvheads || d.heads / d.kvheads > 8) return "more than 8 query heads per KV head";
+    if (d.experts > 128) return "more than 128 experts";
+    if (d.hidden % 64 || d.ff % 64) return "hidden or expert width not a multiple of 64";
+    for (const LayerW& L : c->layers) {
+        if (!(km(L.q.kind) && km(L.k.kind) && km(L.v.kind) && km(L.o.kind) && km(L.gate.kind) &&
+              L.up.kind == L.gate.kind && km(L.down.kind)))
+            return "a projection is not Q4_K or Q6_K";
+        if (L.router.kind != F32) return "router is not F32";
+    }
+    return "";
+}
+
+void prefill_alloc(qh_ctx* c, uint32_t cap) {
+    auto& P = c->pf;
+    if (P.cap >= cap) return;
+    const ModelDims& d = c->dm;
+    const uint64_t H = d.hidden, qd = (uint64_t)d.heads * 128, kvd = (uint64_t)d.kvheads * 128;
+    const uint64_t n_asg = (uint64_t)cap * d.top;
+    const uint32_t max_tiles = (uint32_t)((n_asg + 127) / 128 + d.experts);
+    auto up = [](uint64_t b) { return (b + 255) / 256 * 256; };
+    struct R {
+        uint64_t bytes;
+        void** dst;
+    } regs[] = {
+        {cap * H * 4, (void**)&P.X},           {cap * H * 4, (void**)&P.Xn32},
+        {cap * (qd + 2 * kvd) * 4, (void**)&P.QKV}, {(uint64_t)cap * d.experts * 4, (void**)&P.LR},
+        {n_asg * 4, (void**)&P.wts},           {n_asg * H * 4, (void**)&P.Y},
+        {cap * H * 2, (void**)&P.Xn16},        {(uint64_t)d.heads * cap * 128 * 2, (void**)&P.Q16},
+        {cap * qd * 2, (void**)&P.O16},        {n_asg * d.ff * 2, (void**)&P.Hs},
+        {n_asg * 4, (void**)&P.ids},           {(uint64_t)(d.experts + 1) * 4, (void**)&P.goff},
+        {n_asg * 4, (void**)&P.tok},           {n_asg * 4, (void**)&P.asg},
+        {(uint64_t)max_tiles * 4, (void**)&P.te}, {(uint64_t)max_tiles * 4, (void**)&P.tm},
+        {4, (void**)&P.ntile},
+    };
+    uint64_t total = 0;
+    for (const R& r : regs) total += up(r.bytes);
+    P.buf.alloc(total);
+    HIP_OK(hipMemset(P.buf.p, 0, total));
+    uint8_t* q = P.buf.as<uint8_t>();
+    for (const R& r : regs) {
+        *r.dst = q;
+        q += up(r.bytes);
+    }
+    P.cap = cap;
+    P.max_tiles = max_tiles;
+}
+
+template <class F> void dispatch_km(uint32_t kind, F f) {
+    if (kind == Q4_K) f(std::integral_constant<uint32_t, Q4_K>{});
+    else f(std::integral_constant<uint32_t, Q6_K>{});
+}
+
+void pf_gemm(qh_ctx* c, const DevMat& W, const _Float16* A, uint32_t lda, uint32_t M, float* C, uint32_t ldc,
+             bool add) {
+    const dim3 grid((W.rows + 127) / 128, (M + 127) / 128);
+    dispatch_km(W.kind, [&](auto K) {
+        hipLaunchKernelGGL(k_gemm<decltype(K)::value>, grid, dim3(256), 0, c->s, A, lda, M, W, C, ldc, add ? 1u : 0u);
+    });
+}
+
+// One decoder layer (src/model.rs:227-287) for chunk tokens [0, S) at
+// positions p0 + t.
+void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
+    auto& P = c->pf;
+    const ModelDims& d = c->dm;
+    const LayerW& L = c->layers[l];
+    const uint32_t H = d.hidden, qd = d.heads * 128, kvd = d.kvheads * 128, row = qd + 2 * kvd;
+    hipLaunchKernelGGL(k_pf_norm, dim3(S), dim3(kBlock), 0, c->s, P.X, L.attn_norm, H, d.eps, P.Xn16,
+                       (float*)nullptr);
+    pf_gemm(c, L.q, P.Xn16, H, S, P.QKV, row, false);
+    pf_gemm(c, L.k, P.Xn16, H, S, P.QKV + qd, row, false);
+    pf_gemm(c, L.v, P.Xn16, H, S, P.QKV + qd + kvd, row, false);
+    hipLaunchKernelGGL(k_pf_qkrope, dim3(S), dim3(kBlock), 0, c->s, P.QKV, L.q_norm, L.k_norm, c->acts.rope, p0, S,
+                       d.heads, d.kvheads, d.ctx, d.eps, P.Q16, L.kcache, L.vcache);
+    hipLaunchKernelGGL(k_pf_attn, dim3((S + 31) / 32, d.kvheads), dim3(256), 0, c->s, P.Q16, L.kcache, L.vcache, p0, S,
+                       d.heads / d.kvheads, d.ctx, qd, P.O16);
+    pf_gemm(c, L.o, P.O16, qd, S, P.X, H, true);
+    hipLaunchKernelGGL(k_pf_norm, dim3(S), dim3(kBlock), 0, c->s, P.X, L.ffn_norm, H, d.eps, P.Xn16, P.Xn32);
+    hipLaunchKernelGGL(k_pf_router, dim3((S + 15) / 16), dim3(kBlock), 0, c->s, P.Xn32, L.router, S, H, d.experts,
+                       P.LR);
+    hipLaunchKernelGGL(k_pf_topk, dim3((S + kWaves - 1) / kWaves), dim3(kBlock), 0, c->s, P.LR, S, d.experts, d.top,
+                       P.ids, P.wts, c->acts.st);
+    hipLaunchKernelGGL(k_pf_group, dim3(1), dim3(1024), 0, c->s, P.ids, S * d.top, d.top, d.experts, P.goff, P.tok,
+                       P.asg, P.te, P.tm, P.ntile);
+    const ExpertTiles T{P.goff, P.tok, P.asg, P.te, P.tm, P.ntile};
+    const uint32_t tiles = (S * d.top + 127) / 128 + d.experts;
+    dispatch_km(L.gate.kind, [&](auto K) {
+        hipLaunchKernelGGL(k_gemm_gateup<decltype(K)::value>, dim3((d.ff + 127) / 128, tiles), dim3(256), 0, c->s,
+                           P.Xn16, H, T, L.gate, L.up, P.Hs);
+    });
+    dispatch_km(L.down.kind, [&](auto K) {
+        hipLaunchKernelGGL(k_gemm_down<decltype(K)::value>, dim3((H + 127) / 128, tiles), dim3(256), 0, c->s, P.Hs, T,
+                           L.down, P.Y);
+    });
+    hipLaunchKernelGGL(k_pf_combine, dim3(S), dim3(kBlock), 0, c->s, P.X, P.Y, P.wts, H, d.top);
+}
+
 double now_ms() {
     return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
 }
@@ -1003,6 +1138,51 @@ int qh_generate(qh_ctx* c, const uint32_t* prompt, size_t n_prompt, size_t n_new
         sync(c);
         c->pos += steps;
         c->stats.matvecs += matvecs_per_token(c) * steps;
+        c->stats.matvec_ms += now_ms() - t0;
+    });
+}
+
+int qh_prefill(qh_ctx* c, const uint32_t* prompt, size_t n, float* logits, uint32_t* argmax) {
+    return guarded(c, [&] {
+        double t0 = now_ms();
+        need_model(c);
+        if (n == 0) throw Error("empty prompt");
+        if (c->pos + n > c->context) throw Error("prompt + max-tokens exceed --ctx");
+        for (size_t i = 0; i < n; i++)
+            if (prompt[i] >= c->cfg.vocab) throw Error("token outside vocabulary");
+        const std::string gap = prefill_gap(c);
+        if (!gap.empty()) throw Error("batched prefill does not cover this model: " + gap);
+        size_t chunk = kPrefillChunk;
+        if (const char* e = std::getenv("QH_PREFILL_CHUNK")) chunk = std::max<long>(1, std::atol(e));
+        const uint32_t cap = (uint32_t)std::min<size_t>({n, chunk, kPrefillChunk, c->context});
+        prefill_alloc(c, cap);
+        auto& P = c->pf;
+        const ModelDims& d = c->dm;
+        const uint32_t p_start = (uint32_t)c->pos;
+        HIP_OK(hipMemcpyAsync(c->acts.tokens + p_start, prompt, n * 4, hipMemcpyHostToDevice, c->s));
+        // the tail (vocab projection + argmax) runs as the step of the last
+        // prompt token: tokens[pos + n] receives the greedy id
+        put_state(c, (uint32_t)(p_start + n - 1), (uint32_t)(p_start + n - 1));
+        uint32_t S = 0;
+        for (size_t c0 = 0; c0 < n; c0 += cap) {
+            S = (uint32_t)std::min<size_t>(cap, n - c0);
+            const uint32_t p0 = p_start + (uint32_t)c0;
+            hipLaunchKernelGGL(k_pf_embed, dim3(S), dim3(kBlock), 0, c->s, c->emb, c->acts.tokens + p0, d.hidden,
+                               d.vocab, P.X, c->acts.st);
+            for (size_t l = 0; l < c->layers.size(); l++) prefill_layer(c, l, S, p0);
+        }
+        HIP_OK(hipGetLastError());
+        HIP_OK(hipMemcpyAsync(c->acts.x, P.X + (size_t)(S - 1) * d.hidden, d.hidden * 4, hipMemcpyDeviceToDevice,
+                              c->s));
+        enqueue_tail(c);
+        HIP_OK(hipGetLastError());
+        DevState st = get_state(c);
+        if (st.err) fail_step(c, st.err);
+        if (logits) HIP_OK(hipMemcpyAsync(logits, c->acts.logits, c->cfg.vocab * 4, hipMemcpyDeviceToHost, c->s));
+        sync(c);
+        if (argmax) *argmax = st.argmax;
+        c->pos += n;
+        c->stats.matvecs += matvecs_per_token(c) * n;
         c->stats.matvec_ms += now_ms() - t0;
     });
 }

@@ -114,4 +114,16 @@ struct DecodeArgs {
     uint32_t l0, l1, vocab;
 };
 
+// Expert work list of the batched-prefill grouped GEMMs (prefill.hip): tile
+// y covers rows [tm, tm + 128) of expert te; the rows of expert e are
+// [goff[e], goff[e+1]) of the assignments sorted by expert.
+struct ExpertTiles {
+    const uint32_t* goff;   // [E + 1]
+    const uint32_t* tok;    // [n_asg] token of each sorted assignment
+    const uint32_t* asg;    // [n_asg] assignment id (token * top + slot) of each sorted assignment
+    const uint32_t* te;     // [max tiles] expert of tile y
+    const uint32_t* tm;     // [max tiles] first row (within the expert) of tile y
+    const uint32_t* ntile;  // [1] tiles in use
+};
+
 }  // namespace qh

@@ -1,0 +1,656 @@
+// Batched prefill: the reference runs a prompt as one Model::forward per
+// token (src/main.rs:250-256, src/model.rs:209-302); here a chunk of S prompt
+// tokens goes through each layer at once, so every projection is a GEMM
+// (S x K activations times the N x K quantised weight rows) on the fp16
+// matrix cores, and attention is a causal flash-attention pass over the
+// chunk and the cached history.
+//
+// Per layer (one launch each): RMSNorm -> fp16; q/k/v GEMMs; Q/K RMSNorm +
+// RoPE + KV append (fp32 cache, the decode path's layout); attention;
+// o-projection GEMM + residual; RMSNorm (fp16 and fp32); F32 router logits;
+// top-k + softmax; grouping of the (token, slot) assignments by expert;
+// grouped gate/up GEMM with SwiGLU; grouped down GEMM; routing-weighted
+// combine + residual in slot order.
+//
+// GEMM: 128 x 128 output tiles, 4 waves (2 x 2) of 64 x 64, K in 64-column
+// slices.  Each slice of the weight rows is dequantised from the device row
+// layout (Q4_K / Q6_K) straight into LDS as fp16 -- 64 columns are one
+// sub-block pair of a 256-element super-block -- and fed to
+// v_mfma_f32_16x16x32_f16 with fp32 accumulation.  The next slice's global
+// loads are issued before the current slice's MFMAs.
+#include "qh_block.hpp"
+
+namespace qh {
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+constexpr int kGM = 128, kGN = 128, kGK = 64, kGT = 256;
+constexpr int kGL = kGK + 8;  // LDS row pitch in halfs (144 bytes)
+
+// ------------------------------------------------------- weight slices --
+// Thread (row r, half h) of a 64-column slice s (0..3) of super-block b:
+// lo[i] = column 256 b + 64 s + 16 h + i, hi[i] = column 256 b + 64 s + 32 + 16 h + i.
+template <uint32_t KIND> struct WSlice;
+
+template <> struct WSlice<Q4_K> {
+    uint4 q, hdr;
+    __device__ __forceinline__ void load(const uint8_t* row, const RowGeo& g, uint32_t b, uint32_t s, uint32_t h) {
+        hdr = ld16(row + g.off_a + b * 16);
+        q = ld16(row + g.off_b + b * 128 + s * 32 + h * 16);
+    }
+    // d*sc*q - dmin*m (src/quant.rs:50-62), sub-blocks 2s (low nibbles) and 2s+1
+    __device__ __forceinline__ void dequant(uint32_t s, uint32_t, _Float16 (&lo)[16], _Float16 (&hi)[16]) const {
+        uint32_t scp, mp;
+        kscale_pair(hdr.y, hdr.z, hdr.w, s, scp, mp);
+        const float d = h2f(hdr.x & 0xffffu), dm = h2f(hdr.x >> 16);
+        const float a0 = d * (float)(scp & 0xffu), b0 = dm * (float)(mp & 0xffu);
+        const float a1 = d * (float)(scp >> 8), b1 = dm * (float)(mp >> 8);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t byte = (w[k] >> (8 * j)) & 0xffu;
+                lo[4 * k + j] = (_Float16)(a0 * (float)(byte & 15u) - b0);
+                hi[4 * k + j] = (_Float16)(a1 * (float)(byte >> 4) - b1);
+            }
+        }
+    }
+};
+
+template <> struct WSlice<Q6_K> {
+    uint4 l0, l1, qh;
+    uint2 sc;
+    uint32_t d;
+    __device__ __forceinline__ void load(const uint8_t* row, const RowGeo& g, uint32_t b, uint32_t s, uint32_t h) {
+        const uint32_t c = s >> 1;
+        l0 = ld16(row + g.off_a + b * 128 + c * 64 + h * 16);
+        l1 = ld16(row + g.off_a + b * 128 + c * 64 + 32 + h * 16);
+        qh = ld16(row + g.off_b + b * 64 + c * 32 + h * 16);
+        sc = gld<uint2>(row + g.off_c + b * 16 + c * 8);
+        d = ld_u16(row + g.off_d + b * 2);
+    }
+    // d*sc*(q-32) (src/quant.rs:63-77): quarters q0 = 2 (s & 1) and q0 + 1 of chunk s/2
+    __device__ __forceinline__ void dequant(uint32_t s, uint32_t h, _Float16 (&lo)[16], _Float16 (&hi)[16]) const {
+        const uint32_t q0 = 2 * (s & 1), sh = (s & 1) * 4;
+        const uint32_t i0 = q0 * 2 + h, i1 = (q0 + 1) * 2 + h;  // scale bytes
+        const uint32_t s0 = i0 < 4 ? sc.x >> (8 * i0) : sc.y >> (8 * (i0 - 4));
+        const uint32_t s1 = i1 < 4 ? sc.x >> (8 * i1) : sc.y >> (8 * (i1 - 4));
+        const float df = h2f(d);
+        const float a0 = df * (float)(int8_t)(s0 & 0xffu), a1 = df * (float)(int8_t)(s1 & 0xffu);
+        const uint32_t L0[4] = {l0.x, l0.y, l0.z, l0.w}, L1[4] = {l1.x, l1.y, l1.z, l1.w};
+        const uint32_t QH[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t hb = (QH[k] >> (8 * j)) & 0xffu;
+                const int qa = (int)(((L0[k] >> (8 * j + sh)) & 15u) | (((hb >> (2 * q0)) & 3u) << 4)) - 32;
+                const int qb = (int)(((L1[k] >> (8 * j + sh)) & 15u) | (((hb >> (2 * q0 + 2)) & 3u) << 4)) - 32;
+                lo[4 * k + j] = (_Float16)(a0 * (float)qa);
+                hi[4 * k + j] = (_Float16)(a1 * (float)qb);
+            }
+        }
+    }
+};
+
+__device__ __forceinline__ void st_h16(_Float16* dst, const _Float16 (&v)[16]) {
+    h8v a, b;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        a[i] = v[i];
+        b[i] = v[8 + i];
+    }
+    *reinterpret_cast<h8v*>(dst) = a;
+    *reinterpret_cast<h8v*>(dst + 8) = b;
+}
+
+// ---------------------------------------------------------------- GEMM --
+// acc[nb][mt][nt] += A[m0 .. m0+128) x W_nb[n0 .. n0+128)^T over K columns.
+// arow(r): pointer to the fp16 row of tile row r (nullptr: zero row).
+// wrow[nb]: this thread's weight row (row n0 + tid/2 of matrix nb; nullptr:
+// zero row).  Wave w owns output rows 64 (w & 1) .., columns 64 (w >> 1) ..
+template <uint32_t KIND, int NB>
+__device__ __forceinline__ void gemm_tile(const _Float16* arow, const uint8_t* const (&wrow)[NB], const RowGeo& g,
+                                          uint32_t K, f4v (&acc)[NB][4][4], _Float16* As, _Float16* Ws) {
+    const uint32_t tid = threadIdx.x, r = tid >> 1, h = tid & 1, lane = tid & 63, w = tid >> 6;
+    const uint32_t wm = w & 1, wn = w >> 1;
+    uint4 av[4];
+    WSlice<KIND> ws[NB];
+    auto gload = [&](uint32_t k0) {
+        const uint32_t b = k0 >> 8, s = (k0 >> 6) & 3;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            av[i] = arow ? gld<uint4>(arow + k0 + 32 * h + 8 * i) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++)
+            if (wrow[nb]) ws[nb].load(wrow[nb], g, b, s, h);
+    };
+    auto lstore = [&](uint32_t k0) {
+        const uint32_t s = (k0 >> 6) & 3;
+#pragma unroll
+        for (int i = 0; i < 4; i++) *reinterpret_cast<uint4*>(As + r * kGL + 32 * h + 8 * i) = av[i];
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+            _Float16 lo[16], hi[16];
+            if (wrow[nb]) {
+                ws[nb].dequant(s, h, lo, hi);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i++) lo[i] = hi[i] = (_Float16)0.f;
+            }
+            _Float16* dst = Ws + nb * kGN * kGL + r * kGL;
+            st_h16(dst + 16 * h, lo);
+            st_h16(dst + 32 + 16 * h, hi);
+        }
+    };
+    gload(0);
+    for (uint32_t k0 = 0; k0 < K; k0 += kGK) {
+        lstore(k0);
+        __syncthreads();
+        if (k0 + kGK < K) gload(k0 + kGK);
+#pragma unroll
+        for (uint32_t ks = 0; ks < 2; ks++) {
+            const uint32_t kc = 32 * ks + 8 * (lane >> 4);
+            h8v af[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++)
+                af[mt] = *reinterpret_cast<const h8v*>(As + (64 * wm + 16 * mt + (lane & 15)) * kGL + kc);
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) {
+#pragma unroll
+                for (int nt = 0; nt < 4; nt++) {
+                    const h8v bf = *reinterpret_cast<const h8v*>(Ws + nb * kGN * kGL +
+                                                                 (64 * wn + 16 * nt + (lane & 15)) * kGL + kc);
+#pragma unroll
+                    for (int mt = 0; mt < 4; mt++)
+                        acc[nb][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mt], bf, acc[nb][mt][nt], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Output element of acc[.][mt][nt][i] for this lane: tile row / column.
+__device__ __forceinline__ uint32_t acc_row(uint32_t mt, uint32_t i) {
+    const uint32_t lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) & 1;
+    return 64 * wm + 16 * mt + 4 * (lane >> 4) + i;
+}
+__device__ __forceinline__ uint32_t acc_col(uint32_t nt) {
+    const uint32_t lane = threadIdx.x & 63, wn = threadIdx.x >> 7;
+    return 64 * wn + 16 * nt + (lane & 15);
+}
+
+// Dense: C[m][n] (=, or += when add) A[m] . W[n] for m < M, n < W.rows.
+// Grid (ceil(N/128), ceil(M/128)).
+template <uint32_t KIND>
+__global__ __launch_bounds__(kGT) void k_gemm(const _Float16* A, uint32_t lda, uint32_t M, DevMat W, float* C,
+                                              uint32_t ldc, uint32_t add) {
+    __shared__ __align__(16) _Float16 smem[2 * kGM * kGL];
+    const uint32_t n0 = blockIdx.x * kGN, m0 = blockIdx.y * kGM, r = threadIdx.x >> 1;
+    const _Float16* arow = m0 + r < M ? A + (size_t)(m0 + r) * lda : nullptr;
+    const uint8_t* const wrow[1] = {n0 + r < W.rows ? W.w + (size_t)(n0 + r) * W.drb : nullptr};
+    f4v acc[1][4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) acc[0][mt][nt] = f4v{0.f, 0.f, 0.f, 0.f};
+    gemm_tile<KIND, 1>(arow, wrow, W.geo, W.cols, acc, smem, smem + kGM * kGL);
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t m = m0 + acc_row(mt, i), n = n0 + acc_col(nt);
+                if (m < M && n < W.rows) {
+                    float* p = C + (size_t)m * ldc + n;
+                    *p = add ? *p + acc[0][mt][nt][i] : acc[0][mt][nt][i];
+                }
+            }
+}
+
+
+// gate/up of the routed experts + SwiGLU (model.rs:266-274):
+// Hs[goff[e] + r][n] = silu(g) * u, fp16, for the sorted assignments.
+template <uint32_t KIND>
+__global__ __launch_bounds__(kGT) void k_gemm_gateup(const _Float16* Xn, uint32_t H, ExpertTiles G, DevMat Wg, DevMat Wu,
+                                                     _Float16* Hs) {
+    __shared__ __align__(16) _Float16 smem[3 * kGM * kGL];
+    if (blockIdx.y >= *G.ntile) return;
+    const uint32_t e = G.te[blockIdx.y], mt0 = G.tm[blockIdx.y];
+    const uint32_t base = G.goff[e], rows = G.goff[e + 1] - base;
+    const uint32_t n0 = blockIdx.x * kGN, r = threadIdx.x >> 1, ff = Wg.rows;
+    const _Float16* arow = mt0 + r < rows ? Xn + (size_t)G.tok[base + mt0 + r] * H : nullptr;
+    const bool nok = n0 + r < ff;
+    const uint8_t* const wrow[2] = {nok ? Wg.w + e * Wg.expert_stride + (size_t)(n0 + r) * Wg.drb : nullptr,
+                                    nok ? Wu.w + e * Wu.expert_stride + (size_t)(n0 + r) * Wu.drb : nullptr};
+    f4v acc[2][4][4];
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+            for (int nt = 0; nt < 4; nt++) acc[nb][mt][nt] = f4v{0.f, 0.f, 0.f, 0.f};
+    gemm_tile<KIND, 2>(arow, wrow, Wg.geo, Wg.cols, acc, smem, smem + kGM * kGL);
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t m = mt0 + acc_row(mt, i), n = n0 + acc_col(nt);
+                if (m < rows && n < ff) {
+#pragma clang fp contract(off)
+                    const float gv = acc[0][mt][nt][i], uv = acc[1][mt][nt][i];
+                    Hs[(size_t)(base + m) * ff + n] = (_Float16)((gv / (1.f + expf(-gv))) * uv);
+                }
+            }
+}
+
+// down of the routed experts: Y[asg][n] = Hs[goff[e] + r] . Wd_e[n].
+template <uint32_t KIND>
+__global__ __launch_bounds__(kGT) void k_gemm_down(const _Float16* Hs, ExpertTiles G, DevMat Wd, float* Y) {
+    __shared__ __align__(16) _Float16 smem[2 * kGM * kGL];
+    if (blockIdx.y >= *G.ntile) return;
+    const uint32_t e = G.te[blockIdx.y], mt0 = G.tm[blockIdx.y];
+    const uint32_t base = G.goff[e], rows = G.goff[e + 1] - base;
+    const uint32_t n0 = blockIdx.x * kGN, r = threadIdx.x >> 1, ff = Wd.cols, N = Wd.rows;
+    const _Float16* arow = mt0 + r < rows ? Hs + (size_t)(base + mt0 + r) * ff : nullptr;
+    const uint8_t* const wrow[1] = {n0 + r < N ? Wd.w + e * Wd.expert_stride + (size_t)(n0 + r) * Wd.drb : nullptr};
+    f4v acc[1][4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) acc[0][mt][nt] = f4v{0.f, 0.f, 0.f, 0.f};
+    gemm_tile<KIND, 1>(arow, wrow, Wd.geo, ff, acc, smem, smem + kGM * kGL);
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t m = mt0 + acc_row(mt, i), n = n0 + acc_col(nt);
+                if (m < rows && n < N) Y[(size_t)G.asg[base + m] * N + n] = acc[0][mt][nt][i];
+            }
+}
+
+// ------------------------------------------------------ element kernels --
+// X[t] = embedding row of tokens[t] (model.rs:225), bit-exact decode.
+__global__ __launch_bounds__(kBlock) void k_pf_embed(DevMat emb, const uint32_t* tokens, uint32_t H, uint32_t vocab,
+                                                     float* X, DevState* st) {
+    const uint32_t t = blockIdx.x, tok = tokens[t];
+    if (tok >= vocab) {
+        if (threadIdx.x == 0) atomicOr(&st->err, kErrToken);
+        return;
+    }
+    const uint8_t* row = emb.w + (size_t)tok * emb.drb;
+    for (uint32_t i = threadIdx.x; i < H; i += kBlock) X[(size_t)t * H + i] = dequant_value(row, emb.kind, emb.geo, i);
+}
+
+// RMSNorm (ops.rs:3-15) of row t: fp16 copy (GEMM input), optional fp32 copy.
+__global__ __launch_bounds__(kBlock) void k_pf_norm(const float* X, const float* w, uint32_t H, float eps,
+                                                    _Float16* Y16, float* Y32) {
+    __shared__ float red[kWaves];
+    const size_t t = blockIdx.x;
+    const float* x = X + t * H;
+    float ss = 0.f;
+    for (uint32_t i = threadIdx.x; i < H; i += kBlock) ss = fmaf(x[i], x[i], ss);
+    const float scale = 1.0f / sqrtf(block_sum(ss, red) / (float)H + eps);
+    for (uint32_t i = threadIdx.x; i < H; i += kBlock) {
+        const float v = x[i] * (scale * w[i]);
+        Y16[t * H + i] = (_Float16)v;
+        if (Y32) Y32[t * H + i] = v;
+    }
+}
+
+// Q/K RMSNorm per head (model.rs:233-238), NeoX RoPE at position p0 + t
+// (ops.rs:16-28), KV append (model.rs:241-243).  Row t of QKV is
+// [q (heads*128) | k (kvheads*128) | v (kvheads*128)].  Q goes to
+// Q16[head][t][128] (fp16), K and V to the fp32 cache [kvhead][ctx][128].
+// Wave w takes head slots w, w + 4, ...: 0..heads-1 q, then k, then v; lane
+// l holds elements l and l + 64, the rotated pair.
+__global__ __launch_bounds__(kBlock) void k_pf_qkrope(const float* QKV, const float* qn, const float* kn,
+                                                      const float2* rope, uint32_t p0, uint32_t S, uint32_t heads,
+                                                      uint32_t kvheads, uint32_t ctx, float eps, _Float16* Q16,
+                                                      float* kcache, float* vcache) {
+    const uint32_t t = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6, pos = p0 + t;
+    const uint32_t row = (heads + 2 * kvheads) * 128;
+    const float* x = QKV + (size_t)t * row;
+    const float2 cs = rope[(size_t)pos * 64 + lane];
+    for (uint32_t slot = w; slot < heads + 2 * kvheads; slot += kWaves) {  // wave-uniform
+        const float xa = x[slot * 128 + lane], xb = x[slot * 128 + lane + 64];
+        if (slot >= heads + kvheads) {
+            float* dst = vcache + ((size_t)(slot - heads - kvheads) * ctx + pos) * 128;
+            dst[lane] = xa;
+            dst[lane + 64] = xb;
+            continue;
+        }
+        const bool isq = slot < heads;
+        const float* nw = isq ? qn : kn;
+        const float ssq = wave_sum(fmaf(xb, xb, xa * xa));
+        const float sc = 1.0f / sqrtf(ssq / 128.0f + eps);
+        const float y0 = xa * (sc * nw[lane]), y1 = xb * (sc * nw[lane + 64]);
+        float o0, o1;
+        {
+#pragma clang fp contract(off)
+            o0 = y0 * cs.x - y1 * cs.y;
+            o1 = y0 * cs.y + y1 * cs.x;
+        }
+        if (isq) {
+            _Float16* dst = Q16 + ((size_t)slot * S + t) * 128;
+            dst[lane] = (_Float16)o0;
+            dst[lane + 64] = (_Float16)o1;
+        } else {
+            float* dst = kcache + ((size_t)(slot - heads) * ctx + pos) * 128;
+            dst[lane] = o0;
+            dst[lane + 64] = o1;
+        }
+    }
+}
+
+// Router logits (model.rs:249-256) of 16 tokens per workgroup against the F32
+// router rows (E <= 128): thread (expert tid % 128, tokens 8 (tid / 128) ..).
+// Each logit is one sequential fold over the columns.
+__global__ __launch_bounds__(kBlock) void k_pf_router(const float* Xn, DevMat R, uint32_t S, uint32_t H, uint32_t E,
+                                                      float* LR) {
+    __shared__ float xs[16][65];
+    __shared__ float rs[128][65];
+    const uint32_t t0 = blockIdx.x * 16, e = threadIdx.x & 127, tg = threadIdx.x >> 7;
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[j] = 0.f;
+    for (uint32_t k0 = 0; k0 < H; k0 += 64) {
+        for (uint32_t i = threadIdx.x; i < 16 * 64; i += kBlock) {
+            const uint32_t tt = i >> 6, kk = i & 63;
+            xs[tt][kk] = t0 + tt < S ? Xn[(size_t)(t0 + tt) * H + k0 + kk] : 0.f;
+        }
+        for (uint32_t i = threadIdx.x; i < 128 * 64; i += kBlock) {
+            const uint32_t ee = i >> 6, kk = i & 63;
+            rs[ee][kk] = ee < E ? reinterpret_cast<const float*>(R.w + (size_t)ee * R.drb)[k0 + kk] : 0.f;
+        }
+        __syncthreads();
+        for (uint32_t kk = 0; kk < 64; kk++) {
+            const float rv = rs[e][kk];
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[j] = fmaf(xs[8 * tg + j][kk], rv, acc[j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+        if (e < E && t0 + 8 * tg + j < S) LR[(size_t)(t0 + 8 * tg + j) * E + e] = acc[j];
+}
+
+// Top-k routing of one token per wave (ops.rs:45-56): the k largest logits
+// under the total order, lower index on ties; softmax over the chosen logits
+// in rank order (ops.rs:29-44).  E <= 128.
+__global__ __launch_bounds__(kBlock) void k_pf_topk(const float* LR, uint32_t S, uint32_t E, uint32_t top,
+                                                    uint32_t* ids, float* wts, DevState* st) {
+    const uint32_t lane = threadIdx.x & 63, t = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (t >= S) return;  // wave-uniform
+    const float* lg = LR + (size_t)t * E;
+    const float v0 = lane < E ? lg[lane] : 0.f, v1 = lane + 64 < E ? lg[lane + 64] : 0.f;
+    const bool bad = (lane < E && !finite_f(v0)) || (lane + 64 < E && !finite_f(v1));
+    if (__any(bad)) {
+        if (lane == 0) atomicOr(&st->err, kErrRouter);
+        return;
+    }
+    bool u0 = lane >= E, u1 = lane + 64 >= E;  // used (or absent)
+    float sel = 0.f;
+    uint32_t sid = 0;
+    for (uint32_t k = 0; k < top; k++) {
+        int32_t bk = INT32_MIN;
+        uint32_t bi = 0xffffffffu;
+        if (!u0) best_merge(bk, bi, total_key(v0), lane);
+        if (!u1) best_merge(bk, bi, total_key(v1), lane + 64);
+        wave_best(bk, bi);
+        if (bi == lane) u0 = true;
+        if (bi == lane + 64) u1 = true;
+        if (lane == k) {
+            sid = bi;
+            sel = lg[bi];
+        }
+    }
+    // softmax in rank order, sequential like ops.rs
+    const float mx = wave_max(lane < top ? sel : -INFINITY);
+    const float ex = lane < top ? expf(sel - mx) : 0.f;
+    float sum = 0.f;
+    {
+#pragma clang fp contract(off)
+        for (uint32_t k = 0; k < top; k++) sum += __shfl(ex, k, 64);
+    }
+    if (lane < top) {
+        ids[(size_t)t * top + lane] = sid;
+        wts[(size_t)t * top + lane] = ex / sum;
+    }
+}
+
+// Groups the S*top (token, slot) assignments by expert (one workgroup):
+// goff = exclusive prefix of the per-expert counts, tok/asg = the
+// assignments sorted by expert (order within an expert is arbitrary), and
+// the list of 128-row GEMM tiles (te, tm).
+__global__ __launch_bounds__(1024) void k_pf_group(const uint32_t* ids, uint32_t n, uint32_t top, uint32_t E,
+                                                   uint32_t* goff, uint32_t* tok, uint32_t* asg, uint32_t* te,
+                                                   uint32_t* tm, uint32_t* ntile) {
+    __shared__ uint32_t cnt[256], cur[256];
+    for (uint32_t e = threadIdx.x; e < E; e += 1024) cnt[e] = 0;
+    __syncthreads();
+    for (uint32_t a = threadIdx.x; a < n; a += 1024)
+        if (ids[a] < E) atomicAdd(&cnt[ids[a]], 1u);  // ids < E unless routing failed (reported)
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t off = 0, nt = 0;
+        for (uint32_t e = 0; e < E; e++) {
+            goff[e] = off;
+            cur[e] = off;
+            for (uint32_t m = 0; m < cnt[e]; m += kGM) {
+                te[nt] = e;
+                tm[nt] = m;
+                nt++;
+            }
+            off += cnt[e];
+        }
+        goff[E] = off;
+        *ntile = nt;
+    }
+    __syncthreads();
+    for (uint32_t a = threadIdx.x; a < n; a += 1024) {
+        if (ids[a] >= E) continue;
+        const uint32_t p = atomicAdd(&cur[ids[a]], 1u);
+        tok[p] = a / top;
+        asg[p] = a;
+    }
+}
+
+// MoE combine + residual (model.rs:281-287): moe = sum_k w_k down_k in rank
+// order, then x += moe.
+__global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y, const float* wts, uint32_t H,
+                                                       uint32_t top) {
+    const size_t t = blockIdx.x;
+    for (uint32_t i = threadIdx.x; i < H; i += kBlock) {
+#pragma clang fp contract(off)
+        float moe = 0.f;
+        for (uint32_t k = 0; k < top; k++) moe += wts[t * top + k] * Y[(t * top + k) * H + i];
+        X[t * H + i] += moe;
+    }
+}
+
+// ----------------------------------------------------------- attention --
+// Causal GQA attention (ops.rs:57-98) of chunk queries [q0, q0 + 32) -- at
+// positions p0 + q -- for the G <= 8 query heads of KV head g, over keys
+// [0, p0 + q] of the fp32 cache, on the fp16 matrix cores with an online
+// softmax (fp32 statistics).  Wave w takes query heads 2w and 2w + 1: four
+// query tiles qt = (head 2w + qt/2, queries 16 (qt & 1) ..).  Per 64-key block
+// the keys and values are staged in LDS as fp16 (V transposed) and
+//   S^T = K Q^T  (keys x queries: lane = (4 keys, 1 query), so each lane's
+//                 probabilities already form the A operand of P V, the key
+//                 order inside a 32-key step being the same permutation for
+//                 P and V),
+//   O  += P V    (queries x 128 dims).
+constexpr uint32_t kAQ = 32, kAK = 64;
+constexpr uint32_t kKL = 128 + 8, kVL = kAK + 8;  // LDS pitches (halfs)
+
+__global__ __launch_bounds__(kGT) void k_pf_attn(const _Float16* Q16, const float* kcache, const float* vcache,
+                                                 uint32_t p0, uint32_t S, uint32_t G, uint32_t ctx, uint32_t qd,
+                                                 _Float16* O16) {
+    __shared__ __align__(16) _Float16 Kl[kAK * kKL];
+    __shared__ __align__(16) _Float16 Vt[128 * kVL];
+    const uint32_t g = blockIdx.y, q0 = blockIdx.x * kAQ;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, grp = lane >> 4, col = lane & 15;
+    const float root = sqrtf(128.0f);
+    h8v qf[4][4];
+#pragma unroll
+    for (uint32_t qt = 0; qt < 4; qt++) {
+        const uint32_t hh = 2 * w + (qt >> 1), q = q0 + 16 * (qt & 1) + col;
+        const bool ok = hh < G && q < S;
+        const _Float16* src = Q16 + ((size_t)(g * G + hh) * S + q) * 128 + 8 * grp;
+#pragma unroll
+        for (uint32_t ks = 0; ks < 4; ks++) {
+            if (ok) {
+                qf[qt][ks] = gld<h8v>(src + 32 * ks);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) qf[qt][ks][i] = (_Float16)0.f;
+            }
+        }
+    }
+    f4v o[4][8];
+#pragma unroll
+    for (int qt = 0; qt < 4; qt++)
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) o[qt][dt] = f4v{0.f, 0.f, 0.f, 0.f};
+    float m[4], l[4];
+#pragma unroll
+    for (int qt = 0; qt < 4; qt++) {
+        m[qt] = -INFINITY;
+        l[qt] = 0.f;
+    }
+    const uint32_t kend = p0 + min(q0 + kAQ, S);  // keys [0, kend) can be attended
+    for (uint32_t k0 = 0; k0 < kend; k0 += kAK) {
+        {
+            // stage K (row-major) and V^T as fp16; zero beyond kend
+            const uint32_t key = tid >> 2, d0 = (tid & 3) * 32;
+            const bool ok = k0 + key < kend;
+            const float* kr = kcache + ((size_t)g * ctx + k0 + key) * 128 + d0;
+            const float* vr = vcache + ((size_t)g * ctx + k0 + key) * 128 + d0;
+#pragma unroll
+            for (uint32_t i = 0; i < 8; i++) {
+                const float4 kv = ok ? gld<float4>(kr + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float4 vv = ok ? gld<float4>(vr + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                _Float16* kd = Kl + key * kKL + d0 + 4 * i;
+                kd[0] = (_Float16)kv.x;
+                kd[1] = (_Float16)kv.y;
+                kd[2] = (_Float16)kv.z;
+                kd[3] = (_Float16)kv.w;
+                const uint32_t dd = d0 + 4 * i;
+                Vt[(dd + 0) * kVL + key] = (_Float16)vv.x;
+                Vt[(dd + 1) * kVL + key] = (_Float16)vv.y;
+                Vt[(dd + 2) * kVL + key] = (_Float16)vv.z;
+                Vt[(dd + 3) * kVL + key] = (_Float16)vv.w;
+            }
+        }
+        __syncthreads();
+        f4v st[4][4];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int qt = 0; qt < 4; qt++) st[kt][qt] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t ks = 0; ks < 4; ks++) {
+#pragma unroll
+            for (uint32_t kt = 0; kt < 4; kt++) {
+                const h8v af = *reinterpret_cast<const h8v*>(Kl + (16 * kt + col) * kKL + 32 * ks + 8 * grp);
+#pragma unroll
+                for (uint32_t qt = 0; qt < 4; qt++)
+                    st[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, qf[qt][ks], st[kt][qt], 0, 0, 0);
+            }
+        }
+        // scale (a divide, like ops.rs:87), causal mask, online softmax per query
+#pragma unroll
+        for (uint32_t qt = 0; qt < 4; qt++) {
+            const uint32_t qpos = p0 + q0 + 16 * (qt & 1) + col;
+            float mx = -INFINITY;
+#pragma unroll
+            for (uint32_t kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (uint32_t i = 0; i < 4; i++) {
+                    const uint32_t kpos = k0 + 16 * kt + 4 * grp + i;
+                    const float v = (kpos <= qpos && kpos < kend) ? st[kt][qt][i] / root : -INFINITY;
+                    st[kt][qt][i] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mn = fmaxf(m[qt], mx);
+            const float alpha = expf(m[qt] - mn);  // 0 on the first block
+            float ls = 0.f;
+#pragma unroll
+            for (uint32_t kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (uint32_t i = 0; i < 4; i++) {
+                    const float pv = expf(st[kt][qt][i] - mn);
+                    st[kt][qt][i] = pv;
+                    ls += pv;
+                }
+            l[qt] = fmaf(l[qt], alpha, ls);
+            m[qt] = mn;
+            // O rows of tile qt are queries 4 grp + i: their alpha is in lane 4 grp + i
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++) {
+                const float ai = __shfl(alpha, 4 * grp + i, 64);
+#pragma unroll
+                for (uint32_t dt = 0; dt < 8; dt++) o[qt][dt][i] *= ai;
+            }
+        }
+#pragma unroll
+        for (uint32_t ks2 = 0; ks2 < 2; ks2++) {
+            h8v pa[4];
+#pragma unroll
+            for (uint32_t qt = 0; qt < 4; qt++)
+#pragma unroll
+                for (uint32_t i = 0; i < 4; i++) {
+                    pa[qt][i] = (_Float16)st[2 * ks2][qt][i];
+                    pa[qt][4 + i] = (_Float16)st[2 * ks2 + 1][qt][i];
+                }
+#pragma unroll
+            for (uint32_t dt = 0; dt < 8; dt++) {
+                const _Float16* vrow = Vt + (16 * dt + col) * kVL + 32 * ks2 + 4 * grp;
+                const uint2 lo = *reinterpret_cast<const uint2*>(vrow), hi = *reinterpret_cast<const uint2*>(vrow + 16);
+                const uint4 bv = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                const h8v bf = __builtin_bit_cast(h8v, bv);
+#pragma unroll
+                for (uint32_t qt = 0; qt < 4; qt++)
+                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[qt], bf, o[qt][dt], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (uint32_t qt = 0; qt < 4; qt++) {
+        float lt = l[qt] + __shfl_xor(l[qt], 16, 64);
+        lt += __shfl_xor(lt, 32, 64);
+        const uint32_t hh = 2 * w + (qt >> 1);
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const float li = __shfl(lt, 4 * grp + i, 64);
+            const uint32_t q = q0 + 16 * (qt & 1) + 4 * grp + i;
+            if (hh < G && q < S) {
+                _Float16* dst = O16 + (size_t)q * qd + (g * G + hh) * 128 + col;
+#pragma unroll
+                for (uint32_t dt = 0; dt < 8; dt++) dst[16 * dt] = (_Float16)(o[qt][dt][i] / li);
+            }
+        }
+    }
+}
+
+#define QH_INSTANTIATE_PREFILL_GEMM(K)                                                                          \
+    template __global__ void k_gemm<K>(const _Float16*, uint32_t, uint32_t, DevMat, float*, uint32_t, uint32_t); \
+    template __global__ void k_gemm_gateup<K>(const _Float16*, uint32_t, ExpertTiles, DevMat, DevMat, _Float16*);     \
+    template __global__ void k_gemm_down<K>(const _Float16*, ExpertTiles, DevMat, float*);
+QH_INSTANTIATE_PREFILL_GEMM(Q4_K)
+QH_INSTANTIATE_PREFILL_GEMM(Q6_K)
+
+}  // namespace qh
