@@ -51,9 +51,10 @@ template <uint32_t K> __global__ void k_gemm_down(const _Float16*, ExpertTiles, 
 __global__ void k_pf_embed(DevMat, const uint32_t*, uint32_t, uint32_t, float*, DevState*);
 __global__ void k_pf_norm(const float*, const float*, uint32_t, float, _Float16*, float*);
 __global__ void k_pf_qkrope(const float*, const float*, const float*, const float2*, uint32_t, uint32_t, uint32_t,
-                            uint32_t, uint32_t, float, _Float16*, float*, float*);
-__global__ void k_pf_attn(const _Float16*, const float*, const float*, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t,
-                          _Float16*);
+                            uint32_t, uint32_t, float, _Float16*, float*, float*, _Float16*, _Float16*, uint32_t);
+__global__ void k_pf_attn(const _Float16*, const _Float16*, const _Float16*, uint32_t, uint32_t, uint32_t, uint32_t,
+                          uint32_t, uint32_t, _Float16*);
+__global__ void k_pf_kvh(const float*, const float*, uint32_t, uint32_t, uint32_t, uint32_t, _Float16*, _Float16*);
 __global__ void k_pf_router(const float*, DevMat, uint32_t, uint32_t, uint32_t, float*);
 __global__ void k_pf_topk(const float*, uint32_t, uint32_t, uint32_t, uint32_t*, float*, DevState*);
 __global__ void k_pf_group(const uint32_t*, uint32_t, uint32_t, uint32_t, uint32_t*, uint32_t*, uint32_t*, uint32_t*,
@@ -200,7 +201,7 @@ struct qh_ctx {
         uint32_t cap = 0;
         DevBuf buf;
         float *X = nullptr, *Xn32 = nullptr, *QKV = nullptr, *LR = nullptr, *wts = nullptr, *Y = nullptr;
-        _Float16 *Xn16 = nullptr, *Q16 = nullptr, *O16 = nullptr, *Hs = nullptr;
+        _Float16 *Xn16 = nullptr, *Q16 = nullptr, *O16 = nullptr, *Hs = nullptr, *Kh = nullptr, *Vth = nullptr;
         uint32_t *ids = nullptr, *goff = nullptr, *tok = nullptr, *asg = nullptr, *te = nullptr, *tm = nullptr,
                  *ntile = nullptr;
         uint32_t max_tiles = 0;
@@ -779,6 +780,8 @@ void prefill_alloc(qh_ctx* c, uint32_t cap) {
         {n_asg * 4, (void**)&P.tok},           {n_asg * 4, (void**)&P.asg},
         {(uint64_t)max_tiles * 4, (void**)&P.te}, {(uint64_t)max_tiles * 4, (void**)&P.tm},
         {4, (void**)&P.ntile},
+        {(uint64_t)d.kvheads * d.ctx * 128 * 2, (void**)&P.Kh},
+        {(uint64_t)d.kvheads * 128 * ((d.ctx + 63) / 64 * 64) * 2, (void**)&P.Vth},
     };
     uint64_t total = 0;
     for (const R& r : regs) total += up(r.bytes);
@@ -818,10 +821,14 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
     pf_gemm(c, L.q, P.Xn16, H, S, P.QKV, row, false);
     pf_gemm(c, L.k, P.Xn16, H, S, P.QKV + qd, row, false);
     pf_gemm(c, L.v, P.Xn16, H, S, P.QKV + qd + kvd, row, false);
+    const uint32_t vp = (d.ctx + 63) / 64 * 64;  // row pitch of the transposed V copy
+    if (p0 > 0)  // fp16 copies of this layer's earlier positions
+        hipLaunchKernelGGL(k_pf_kvh, dim3(p0), dim3(kBlock), 0, c->s, L.kcache, L.vcache, 0u, d.kvheads, d.ctx, vp,
+                           P.Kh, P.Vth);
     hipLaunchKernelGGL(k_pf_qkrope, dim3(S), dim3(kBlock), 0, c->s, P.QKV, L.q_norm, L.k_norm, c->acts.rope, p0, S,
-                       d.heads, d.kvheads, d.ctx, d.eps, P.Q16, L.kcache, L.vcache);
-    hipLaunchKernelGGL(k_pf_attn, dim3((S + 31) / 32, d.kvheads), dim3(256), 0, c->s, P.Q16, L.kcache, L.vcache, p0, S,
-                       d.heads / d.kvheads, d.ctx, qd, P.O16);
+                       d.heads, d.kvheads, d.ctx, d.eps, P.Q16, L.kcache, L.vcache, P.Kh, P.Vth, vp);
+    hipLaunchKernelGGL(k_pf_attn, dim3((S + 63) / 64, 2 * d.kvheads), dim3(256), 0, c->s, P.Q16, P.Kh, P.Vth, p0, S,
+                       d.heads / d.kvheads, d.ctx, vp, qd, P.O16);
     pf_gemm(c, L.o, P.O16, qd, S, P.X, H, true);
     hipLaunchKernelGGL(k_pf_norm, dim3(S), dim3(kBlock), 0, c->s, P.X, L.ffn_norm, H, d.eps, P.Xn16, P.Xn32);
     hipLaunchKernelGGL(k_pf_router, dim3((S + 15) / 16), dim3(kBlock), 0, c->s, P.Xn32, L.router, S, H, d.experts,

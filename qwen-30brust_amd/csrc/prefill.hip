@@ -315,7 +315,8 @@ __global__ __launch_bounds__(kBlock) void k_pf_norm(const float* X, const float*
 __global__ __launch_bounds__(kBlock) void k_pf_qkrope(const float* QKV, const float* qn, const float* kn,
                                                       const float2* rope, uint32_t p0, uint32_t S, uint32_t heads,
                                                       uint32_t kvheads, uint32_t ctx, float eps, _Float16* Q16,
-                                                      float* kcache, float* vcache) {
+                                                      float* kcache, float* vcache, _Float16* Kh, _Float16* Vth,
+                                                      uint32_t vp) {
     const uint32_t t = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6, pos = p0 + t;
     const uint32_t row = (heads + 2 * kvheads) * 128;
     const float* x = QKV + (size_t)t * row;
@@ -323,9 +324,12 @@ __global__ __launch_bounds__(kBlock) void k_pf_qkrope(const float* QKV, const fl
     for (uint32_t slot = w; slot < heads + 2 * kvheads; slot += kWaves) {  // wave-uniform
         const float xa = x[slot * 128 + lane], xb = x[slot * 128 + lane + 64];
         if (slot >= heads + kvheads) {
-            float* dst = vcache + ((size_t)(slot - heads - kvheads) * ctx + pos) * 128;
+            const uint32_t g = slot - heads - kvheads;
+            float* dst = vcache + ((size_t)g * ctx + pos) * 128;
             dst[lane] = xa;
             dst[lane + 64] = xb;
+            Vth[((size_t)g * 128 + lane) * vp + pos] = (_Float16)xa;
+            Vth[((size_t)g * 128 + lane + 64) * vp + pos] = (_Float16)xb;
             continue;
         }
         const bool isq = slot < heads;
@@ -347,41 +351,74 @@ __global__ __launch_bounds__(kBlock) void k_pf_qkrope(const float* QKV, const fl
             float* dst = kcache + ((size_t)(slot - heads) * ctx + pos) * 128;
             dst[lane] = o0;
             dst[lane + 64] = o1;
+            _Float16* dh = Kh + ((size_t)(slot - heads) * ctx + pos) * 128;
+            dh[lane] = (_Float16)o0;
+            dh[lane + 64] = (_Float16)o1;
         }
     }
 }
 
-// Router logits (model.rs:249-256) of 16 tokens per workgroup against the F32
-// router rows (E <= 128): thread (expert tid % 128, tokens 8 (tid / 128) ..).
-// Each logit is one sequential fold over the columns.
+// Router logits (model.rs:249-256) in fp32 on the matrix cores
+// (v_mfma_f32_16x16x4_f32: fp32 operands and accumulation): 16 tokens per
+// workgroup, wave w takes experts [32 w, 32 w + 32) (E <= 128); 64-column
+// slices of x and of the F32 router rows are staged in LDS, the next slice's
+// loads issued before the current slice's MFMAs.
 __global__ __launch_bounds__(kBlock) void k_pf_router(const float* Xn, DevMat R, uint32_t S, uint32_t H, uint32_t E,
                                                       float* LR) {
-    __shared__ float xs[16][65];
-    __shared__ float rs[128][65];
-    const uint32_t t0 = blockIdx.x * 16, e = threadIdx.x & 127, tg = threadIdx.x >> 7;
-    float acc[8];
+    constexpr uint32_t kP = 65;  // LDS pitch (floats)
+    __shared__ float xs[16 * kP];
+    __shared__ float rs[128 * kP];
+    const uint32_t t0 = blockIdx.x * 16, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint32_t grp = lane >> 4, col = lane & 15;
+    float4 xr, rr[8];
+    auto gload = [&](uint32_t k0) {
+        const uint32_t tt = tid >> 4, kk = 4 * (tid & 15);
+        xr = t0 + tt < S ? gld<float4>(Xn + (size_t)(t0 + tt) * H + k0 + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int j = 0; j < 8; j++) acc[j] = 0.f;
-    for (uint32_t k0 = 0; k0 < H; k0 += 64) {
-        for (uint32_t i = threadIdx.x; i < 16 * 64; i += kBlock) {
-            const uint32_t tt = i >> 6, kk = i & 63;
-            xs[tt][kk] = t0 + tt < S ? Xn[(size_t)(t0 + tt) * H + k0 + kk] : 0.f;
+        for (uint32_t i = 0; i < 8; i++) {
+            const uint32_t idx = tid + kBlock * i, ee = idx >> 4, k4 = 4 * (idx & 15);
+            rr[i] = ee < E ? gld<float4>(R.w + (size_t)ee * R.drb + 4 * (k0 + k4)) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        for (uint32_t i = threadIdx.x; i < 128 * 64; i += kBlock) {
-            const uint32_t ee = i >> 6, kk = i & 63;
-            rs[ee][kk] = ee < E ? reinterpret_cast<const float*>(R.w + (size_t)ee * R.drb)[k0 + kk] : 0.f;
+    };
+    f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
+    gload(0);
+    for (uint32_t k0 = 0; k0 < H; k0 += 64) {
+        {
+            const uint32_t tt = tid >> 4, kk = 4 * (tid & 15);
+            float* xd = xs + tt * kP + kk;
+            xd[0] = xr.x;
+            xd[1] = xr.y;
+            xd[2] = xr.z;
+            xd[3] = xr.w;
+#pragma unroll
+            for (uint32_t i = 0; i < 8; i++) {
+                const uint32_t idx = tid + kBlock * i, ee = idx >> 4, k4 = 4 * (idx & 15);
+                float* rd = rs + ee * kP + k4;
+                rd[0] = rr[i].x;
+                rd[1] = rr[i].y;
+                rd[2] = rr[i].z;
+                rd[3] = rr[i].w;
+            }
         }
         __syncthreads();
-        for (uint32_t kk = 0; kk < 64; kk++) {
-            const float rv = rs[e][kk];
+        if (k0 + 64 < H) gload(k0 + 64);
+#pragma unroll 4
+        for (uint32_t kk = 0; kk < 64; kk += 4) {
+            const float av = xs[col * kP + kk + grp];
 #pragma unroll
-            for (int j = 0; j < 8; j++) acc[j] = fmaf(xs[8 * tg + j][kk], rv, acc[j]);
+            for (uint32_t nt = 0; nt < 2; nt++)
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, rs[(32 * w + 16 * nt + col) * kP + kk + grp],
+                                                               acc[nt], 0, 0, 0);
         }
         __syncthreads();
     }
 #pragma unroll
-    for (int j = 0; j < 8; j++)
-        if (e < E && t0 + 8 * tg + j < S) LR[(size_t)(t0 + 8 * tg + j) * E + e] = acc[j];
+    for (uint32_t nt = 0; nt < 2; nt++)
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t t = t0 + 4 * grp + i, e = 32 * w + 16 * nt + col;
+            if (t < S && e < E) LR[(size_t)t * E + e] = acc[nt][i];
+        }
 }
 
 // Top-k routing of one token per wave (ops.rs:45-56): the k largest logits
@@ -479,33 +516,50 @@ __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y,
 }
 
 // ----------------------------------------------------------- attention --
-// Causal GQA attention (ops.rs:57-98) of chunk queries [q0, q0 + 32) -- at
-// positions p0 + q -- for the G <= 8 query heads of KV head g, over keys
-// [0, p0 + q] of the fp32 cache, on the fp16 matrix cores with an online
-// softmax (fp32 statistics).  Wave w takes query heads 2w and 2w + 1: four
-// query tiles qt = (head 2w + qt/2, queries 16 (qt & 1) ..).  Per 64-key block
-// the keys and values are staged in LDS as fp16 (V transposed) and
+// Causal GQA attention (ops.rs:57-98) of 64 chunk queries -- at positions
+// p0 + q -- for 4 of the G <= 8 query heads of KV head g (wave w: head
+// 4 hf + w, four 16-query tiles), over keys [0, p0 + q], on the fp16 matrix
+// cores with an online softmax in fp32.  Keys come from an fp16 copy of the
+// layer's K ([kvhead][pos][128]) and V, transposed ([kvhead][128][pos], row
+// pitch vp, a multiple of 64), so a
+// 64-key block is staged in LDS with straight 16-byte copies, then
 //   S^T = K Q^T  (keys x queries: lane = (4 keys, 1 query), so each lane's
 //                 probabilities already form the A operand of P V, the key
 //                 order inside a 32-key step being the same permutation for
 //                 P and V),
 //   O  += P V    (queries x 128 dims).
-constexpr uint32_t kAQ = 32, kAK = 64;
+// Query blocks are launched last-first: the causal triangle gives the late
+// blocks the most keys, so they start first and the others fill in.
+constexpr uint32_t kAQ = 64, kAK = 64;
 constexpr uint32_t kKL = 128 + 8, kVL = kAK + 8;  // LDS pitches (halfs)
 
-__global__ __launch_bounds__(kGT) void k_pf_attn(const _Float16* Q16, const float* kcache, const float* vcache,
-                                                 uint32_t p0, uint32_t S, uint32_t G, uint32_t ctx, uint32_t qd,
-                                                 _Float16* O16) {
+__device__ __forceinline__ uint2 pack4h(float a, float b, float c, float d) {
+    h8v t;  // only the first four used
+    t[0] = (_Float16)a;
+    t[1] = (_Float16)b;
+    t[2] = (_Float16)c;
+    t[3] = (_Float16)d;
+    const uint4 u = __builtin_bit_cast(uint4, t);
+    return make_uint2(u.x, u.y);
+}
+
+__global__ __launch_bounds__(kGT) void k_pf_attn(const _Float16* Q16, const _Float16* Kh, const _Float16* Vth,
+                                                 uint32_t p0, uint32_t S, uint32_t G, uint32_t ctx, uint32_t vp,
+                                                 uint32_t qd, _Float16* O16) {
     __shared__ __align__(16) _Float16 Kl[kAK * kKL];
     __shared__ __align__(16) _Float16 Vt[128 * kVL];
-    const uint32_t g = blockIdx.y, q0 = blockIdx.x * kAQ;
+    const uint32_t nqb = (S + kAQ - 1) / kAQ, q0 = (nqb - 1 - blockIdx.x) * kAQ;
+    const uint32_t g = blockIdx.y >> 1, hf = blockIdx.y & 1;
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, grp = lane >> 4, col = lane & 15;
-    const float root = sqrtf(128.0f);
+    const uint32_t hh = 4 * hf + w;  // query head within the group (wave-uniform)
+    const bool hok = hh < G;
+    // scores / sqrt(128) (ops.rs:87), exponentiated base 2
+    const float sc2 = 1.4426950408889634f / sqrtf(128.0f);
     h8v qf[4][4];
 #pragma unroll
     for (uint32_t qt = 0; qt < 4; qt++) {
-        const uint32_t hh = 2 * w + (qt >> 1), q = q0 + 16 * (qt & 1) + col;
-        const bool ok = hh < G && q < S;
+        const uint32_t q = q0 + 16 * qt + col;
+        const bool ok = hok && q < S;
         const _Float16* src = Q16 + ((size_t)(g * G + hh) * S + q) * 128 + 8 * grp;
 #pragma unroll
         for (uint32_t ks = 0; ks < 4; ks++) {
@@ -517,6 +571,8 @@ __global__ __launch_bounds__(kGT) void k_pf_attn(const _Float16* Q16, const floa
             }
         }
     }
+    // O^T tiles: lane holds dims 16 dt + 4 grp + i of query 16 qt + col, so the
+    // softmax statistics of its query are lane-local
     f4v o[4][8];
 #pragma unroll
     for (int qt = 0; qt < 4; qt++)
@@ -529,120 +585,141 @@ __global__ __launch_bounds__(kGT) void k_pf_attn(const _Float16* Q16, const floa
         l[qt] = 0.f;
     }
     const uint32_t kend = p0 + min(q0 + kAQ, S);  // keys [0, kend) can be attended
-    for (uint32_t k0 = 0; k0 < kend; k0 += kAK) {
-        {
-            // stage K (row-major) and V^T as fp16; zero beyond kend
-            const uint32_t key = tid >> 2, d0 = (tid & 3) * 32;
-            const bool ok = k0 + key < kend;
-            const float* kr = kcache + ((size_t)g * ctx + k0 + key) * 128 + d0;
-            const float* vr = vcache + ((size_t)g * ctx + k0 + key) * 128 + d0;
+    const _Float16* kg = Kh + (size_t)g * ctx * 128;
+    const _Float16* vg = Vth + (size_t)g * 128 * vp;
+    // staging: K thread (key tid/4, 32 dims); V^T thread (dim tid/2, 32 keys)
+    const uint32_t skey = tid >> 2, sd0 = (tid & 3) * 32, sdim = tid >> 1, skk0 = (tid & 1) * 32;
+    uint4 kr[4], vr[4];
+    auto kvload = [&](uint32_t k0) {
 #pragma unroll
-            for (uint32_t i = 0; i < 8; i++) {
-                const float4 kv = ok ? gld<float4>(kr + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
-                const float4 vv = ok ? gld<float4>(vr + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
-                _Float16* kd = Kl + key * kKL + d0 + 4 * i;
-                kd[0] = (_Float16)kv.x;
-                kd[1] = (_Float16)kv.y;
-                kd[2] = (_Float16)kv.z;
-                kd[3] = (_Float16)kv.w;
-                const uint32_t dd = d0 + 4 * i;
-                Vt[(dd + 0) * kVL + key] = (_Float16)vv.x;
-                Vt[(dd + 1) * kVL + key] = (_Float16)vv.y;
-                Vt[(dd + 2) * kVL + key] = (_Float16)vv.z;
-                Vt[(dd + 3) * kVL + key] = (_Float16)vv.w;
+        for (uint32_t i = 0; i < 4; i++)
+            kr[i] = k0 + skey < kend ? gld<uint4>(kg + (size_t)(k0 + skey) * 128 + sd0 + 8 * i) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t kk = skk0 + 8 * i;
+            if (k0 + kk + 8 <= kend) {
+                vr[i] = gld<uint4>(vg + (size_t)sdim * vp + k0 + kk);
+            } else if (k0 + kk < kend) {  // partial group at the end: element by element
+                h8v t;
+#pragma unroll
+                for (uint32_t j = 0; j < 8; j++)
+                    t[j] = k0 + kk + j < kend ? vg[(size_t)sdim * vp + k0 + kk + j] : (_Float16)0.f;
+                vr[i] = __builtin_bit_cast(uint4, t);
+            } else {
+                vr[i] = make_uint4(0, 0, 0, 0);
             }
+        }
+    };
+    kvload(0);
+    for (uint32_t k0 = 0; k0 < kend; k0 += kAK) {
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            *reinterpret_cast<uint4*>(Kl + skey * kKL + sd0 + 8 * i) = kr[i];
+            *reinterpret_cast<uint4*>(Vt + sdim * kVL + skk0 + 8 * i) = vr[i];
         }
         __syncthreads();
-        f4v st[4][4];
+        if (k0 + kAK < kend) kvload(k0 + kAK);  // next block, during this one
+        if (hok) {  // wave-uniform
+            f4v st[4][4];
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++)
+            for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-            for (int qt = 0; qt < 4; qt++) st[kt][qt] = f4v{0.f, 0.f, 0.f, 0.f};
+                for (int qt = 0; qt < 4; qt++) st[kt][qt] = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (uint32_t ks = 0; ks < 4; ks++) {
+            for (uint32_t ks = 0; ks < 4; ks++) {
 #pragma unroll
-            for (uint32_t kt = 0; kt < 4; kt++) {
-                const h8v af = *reinterpret_cast<const h8v*>(Kl + (16 * kt + col) * kKL + 32 * ks + 8 * grp);
+                for (uint32_t kt = 0; kt < 4; kt++) {
+                    const h8v af = *reinterpret_cast<const h8v*>(Kl + (16 * kt + col) * kKL + 32 * ks + 8 * grp);
+#pragma unroll
+                    for (uint32_t qt = 0; qt < 4; qt++)
+                        st[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, qf[qt][ks], st[kt][qt], 0, 0, 0);
+                }
+            }
+            // causal mask, online softmax per query
+#pragma unroll
+            for (uint32_t qt = 0; qt < 4; qt++) {
+                const uint32_t qpos = p0 + q0 + 16 * qt + col;
+                float mx = -INFINITY;
+#pragma unroll
+                for (uint32_t kt = 0; kt < 4; kt++)
+#pragma unroll
+                    for (uint32_t i = 0; i < 4; i++) {
+                        const uint32_t kpos = k0 + 16 * kt + 4 * grp + i;
+                        const float v = (kpos <= qpos && kpos < kend) ? st[kt][qt][i] * sc2 : -INFINITY;
+                        st[kt][qt][i] = v;
+                        mx = fmaxf(mx, v);
+                    }
+                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float mn = fmaxf(m[qt], mx);
+                const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);  // 0 on the first block
+                float ls = 0.f;
+#pragma unroll
+                for (uint32_t kt = 0; kt < 4; kt++)
+#pragma unroll
+                    for (uint32_t i = 0; i < 4; i++) {
+                        const float pv = __builtin_amdgcn_exp2f(st[kt][qt][i] - mn);
+                        st[kt][qt][i] = pv;
+                        ls += pv;
+                    }
+                l[qt] = fmaf(l[qt], alpha, ls);
+                m[qt] = mn;
+#pragma unroll
+                for (uint32_t dt = 0; dt < 8; dt++) o[qt][dt] *= alpha;
+            }
+            // O^T += V^T P^T: A = V^T rows (dims) with keys in the same
+            // permuted order as this lane's probabilities, B = P^T
+#pragma unroll
+            for (uint32_t ks2 = 0; ks2 < 2; ks2++) {
+                h8v pb[4];
 #pragma unroll
                 for (uint32_t qt = 0; qt < 4; qt++)
-                    st[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, qf[qt][ks], st[kt][qt], 0, 0, 0);
-            }
-        }
-        // scale (a divide, like ops.rs:87), causal mask, online softmax per query
 #pragma unroll
-        for (uint32_t qt = 0; qt < 4; qt++) {
-            const uint32_t qpos = p0 + q0 + 16 * (qt & 1) + col;
-            float mx = -INFINITY;
+                    for (uint32_t i = 0; i < 4; i++) {
+                        pb[qt][i] = (_Float16)st[2 * ks2][qt][i];
+                        pb[qt][4 + i] = (_Float16)st[2 * ks2 + 1][qt][i];
+                    }
 #pragma unroll
-            for (uint32_t kt = 0; kt < 4; kt++)
+                for (uint32_t dt = 0; dt < 8; dt++) {
+                    const _Float16* vrow = Vt + (16 * dt + col) * kVL + 32 * ks2 + 4 * grp;
+                    const uint2 lo = *reinterpret_cast<const uint2*>(vrow), hi = *reinterpret_cast<const uint2*>(vrow + 16);
+                    const h8v va = __builtin_bit_cast(h8v, make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
-                for (uint32_t i = 0; i < 4; i++) {
-                    const uint32_t kpos = k0 + 16 * kt + 4 * grp + i;
-                    const float v = (kpos <= qpos && kpos < kend) ? st[kt][qt][i] / root : -INFINITY;
-                    st[kt][qt][i] = v;
-                    mx = fmaxf(mx, v);
+                    for (uint32_t qt = 0; qt < 4; qt++)
+                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[qt], o[qt][dt], 0, 0, 0);
                 }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mn = fmaxf(m[qt], mx);
-            const float alpha = expf(m[qt] - mn);  // 0 on the first block
-            float ls = 0.f;
-#pragma unroll
-            for (uint32_t kt = 0; kt < 4; kt++)
-#pragma unroll
-                for (uint32_t i = 0; i < 4; i++) {
-                    const float pv = expf(st[kt][qt][i] - mn);
-                    st[kt][qt][i] = pv;
-                    ls += pv;
-                }
-            l[qt] = fmaf(l[qt], alpha, ls);
-            m[qt] = mn;
-            // O rows of tile qt are queries 4 grp + i: their alpha is in lane 4 grp + i
-#pragma unroll
-            for (uint32_t i = 0; i < 4; i++) {
-                const float ai = __shfl(alpha, 4 * grp + i, 64);
-#pragma unroll
-                for (uint32_t dt = 0; dt < 8; dt++) o[qt][dt][i] *= ai;
-            }
-        }
-#pragma unroll
-        for (uint32_t ks2 = 0; ks2 < 2; ks2++) {
-            h8v pa[4];
-#pragma unroll
-            for (uint32_t qt = 0; qt < 4; qt++)
-#pragma unroll
-                for (uint32_t i = 0; i < 4; i++) {
-                    pa[qt][i] = (_Float16)st[2 * ks2][qt][i];
-                    pa[qt][4 + i] = (_Float16)st[2 * ks2 + 1][qt][i];
-                }
-#pragma unroll
-            for (uint32_t dt = 0; dt < 8; dt++) {
-                const _Float16* vrow = Vt + (16 * dt + col) * kVL + 32 * ks2 + 4 * grp;
-                const uint2 lo = *reinterpret_cast<const uint2*>(vrow), hi = *reinterpret_cast<const uint2*>(vrow + 16);
-                const uint4 bv = make_uint4(lo.x, lo.y, hi.x, hi.y);
-                const h8v bf = __builtin_bit_cast(h8v, bv);
-#pragma unroll
-                for (uint32_t qt = 0; qt < 4; qt++)
-                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[qt], bf, o[qt][dt], 0, 0, 0);
             }
         }
         __syncthreads();
     }
+    if (!hok) return;
 #pragma unroll
     for (uint32_t qt = 0; qt < 4; qt++) {
         float lt = l[qt] + __shfl_xor(l[qt], 16, 64);
         lt += __shfl_xor(lt, 32, 64);
-        const uint32_t hh = 2 * w + (qt >> 1);
+        const float inv = 1.0f / lt;
+        const uint32_t q = q0 + 16 * qt + col;
+        if (q < S) {
+            _Float16* dst = O16 + (size_t)q * qd + (g * G + hh) * 128 + 4 * grp;
 #pragma unroll
-        for (uint32_t i = 0; i < 4; i++) {
-            const float li = __shfl(lt, 4 * grp + i, 64);
-            const uint32_t q = q0 + 16 * (qt & 1) + 4 * grp + i;
-            if (hh < G && q < S) {
-                _Float16* dst = O16 + (size_t)q * qd + (g * G + hh) * 128 + col;
-#pragma unroll
-                for (uint32_t dt = 0; dt < 8; dt++) dst[16 * dt] = (_Float16)(o[qt][dt][i] / li);
-            }
+            for (uint32_t dt = 0; dt < 8; dt++)
+                *reinterpret_cast<uint2*>(dst + 16 * dt) =
+                    pack4h(o[qt][dt][0] * inv, o[qt][dt][1] * inv, o[qt][dt][2] * inv, o[qt][dt][3] * inv);
         }
+    }
+}
+
+// fp16 copies of the KV cache positions [r0, r0 + gridDim.x) of one layer for
+// the attention: Kh[kvhead][pos][128] and Vth[kvhead][128][pos] (row pitch
+// vp, a multiple of 64).  One workgroup per position.
+__global__ __launch_bounds__(kBlock) void k_pf_kvh(const float* kcache, const float* vcache, uint32_t r0,
+                                                   uint32_t kvheads, uint32_t ctx, uint32_t vp, _Float16* Kh,
+                                                   _Float16* Vth) {
+    const uint32_t pos = r0 + blockIdx.x;
+    for (uint32_t i = threadIdx.x; i < kvheads * 128; i += kBlock) {
+        const uint32_t g = i >> 7, d = i & 127;
+        Kh[((size_t)g * ctx + pos) * 128 + d] = (_Float16)kcache[((size_t)g * ctx + pos) * 128 + d];
+        Vth[((size_t)g * 128 + d) * vp + pos] = (_Float16)vcache[((size_t)g * ctx + pos) * 128 + d];
     }
 }
 
