@@ -216,7 +216,7 @@ __global__ __launch_bounds__(kGT) void k_gemm(const _Float16* A, uint32_t lda, u
 // gate/up of the routed experts + SwiGLU (model.rs:266-274):
 // Hs[goff[e] + r][n] = silu(g) * u, fp16, for the sorted assignments.
 template <uint32_t KIND>
-__global__ __launch_bounds__(kGT) void k_gemm_gateup(const _Float16* Xn, uint32_t H, ExpertTiles G, DevMat Wg, DevMat Wu,
+__global__ __launch_bounds__(kGT, 2) void k_gemm_gateup(const _Float16* Xn, uint32_t H, ExpertTiles G, DevMat Wg, DevMat Wu,
                                                      _Float16* Hs) {
     __shared__ __align__(16) _Float16 smem[3 * kGM * kGL];
     if (blockIdx.y >= *G.ntile) return;
@@ -516,9 +516,9 @@ __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y,
 }
 
 // ----------------------------------------------------------- attention --
-// Causal GQA attention (ops.rs:57-98) of 64 chunk queries -- at positions
+// Causal GQA attention (ops.rs:57-98) of 32 chunk queries -- at positions
 // p0 + q -- for 4 of the G <= 8 query heads of KV head g (wave w: head
-// 4 hf + w, four 16-query tiles), over keys [0, p0 + q], on the fp16 matrix
+// 4 hf + w, two 16-query tiles), over keys [0, p0 + q], on the fp16 matrix
 // cores with an online softmax in fp32.  Keys come from an fp16 copy of the
 // layer's K ([kvhead][pos][128]) and V, transposed ([kvhead][128][pos], row
 // pitch vp, a multiple of 64), so a
@@ -530,7 +530,8 @@ __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y,
 //   O  += P V    (queries x 128 dims).
 // Query blocks are launched last-first: the causal triangle gives the late
 // blocks the most keys, so they start first and the others fill in.
-constexpr uint32_t kAQ = 64, kAK = 64;
+constexpr uint32_t kAQ = 32, kAK = 64;
+constexpr uint32_t kQT = kAQ / 16;  // 16-query tiles per wave
 constexpr uint32_t kKL = 128 + 8, kVL = kAK + 8;  // LDS pitches (halfs)
 
 __device__ __forceinline__ uint2 pack4h(float a, float b, float c, float d) {
@@ -543,7 +544,7 @@ __device__ __forceinline__ uint2 pack4h(float a, float b, float c, float d) {
     return make_uint2(u.x, u.y);
 }
 
-__global__ __launch_bounds__(kGT) void k_pf_attn(const _Float16* Q16, const _Float16* Kh, const _Float16* Vth,
+__global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _Float16* Kh, const _Float16* Vth,
                                                  uint32_t p0, uint32_t S, uint32_t G, uint32_t ctx, uint32_t vp,
                                                  uint32_t qd, _Float16* O16) {
     __shared__ __align__(16) _Float16 Kl[kAK * kKL];
@@ -555,9 +556,9 @@ __global__ __launch_bounds__(kGT) void k_pf_attn(const _Float16* Q16, const _Flo
     const bool hok = hh < G;
     // scores / sqrt(128) (ops.rs:87), exponentiated base 2
     const float sc2 = 1.4426950408889634f / sqrtf(128.0f);
-    h8v qf[4][4];
+    h8v qf[kQT][4];
 #pragma unroll
-    for (uint32_t qt = 0; qt < 4; qt++) {
+    for (uint32_t qt = 0; qt < kQT; qt++) {
         const uint32_t q = q0 + 16 * qt + col;
         const bool ok = hok && q < S;
         const _Float16* src = Q16 + ((size_t)(g * G + hh) * S + q) * 128 + 8 * grp;
@@ -573,14 +574,14 @@ __global__ __launch_bounds__(kGT) void k_pf_attn(const _Float16* Q16, const _Flo
     }
     // O^T tiles: lane holds dims 16 dt + 4 grp + i of query 16 qt + col, so the
     // softmax statistics of its query are lane-local
-    f4v o[4][8];
+    f4v o[kQT][8];
 #pragma unroll
-    for (int qt = 0; qt < 4; qt++)
+    for (int qt = 0; qt < (int)kQT; qt++)
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) o[qt][dt] = f4v{0.f, 0.f, 0.f, 0.f};
-    float m[4], l[4];
+    float m[kQT], l[kQT];
 #pragma unroll
-    for (int qt = 0; qt < 4; qt++) {
+    for (int qt = 0; qt < (int)kQT; qt++) {
         m[qt] = -INFINITY;
         l[qt] = 0.f;
     }
@@ -620,24 +621,24 @@ __global__ __launch_bounds__(kGT) void k_pf_attn(const _Float16* Q16, const _Flo
         __syncthreads();
         if (k0 + kAK < kend) kvload(k0 + kAK);  // next block, during this one
         if (hok) {  // wave-uniform
-            f4v st[4][4];
+            f4v st[4][kQT];
 #pragma unroll
             for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-                for (int qt = 0; qt < 4; qt++) st[kt][qt] = f4v{0.f, 0.f, 0.f, 0.f};
+                for (int qt = 0; qt < (int)kQT; qt++) st[kt][qt] = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (uint32_t ks = 0; ks < 4; ks++) {
 #pragma unroll
                 for (uint32_t kt = 0; kt < 4; kt++) {
                     const h8v af = *reinterpret_cast<const h8v*>(Kl + (16 * kt + col) * kKL + 32 * ks + 8 * grp);
 #pragma unroll
-                    for (uint32_t qt = 0; qt < 4; qt++)
+                    for (uint32_t qt = 0; qt < kQT; qt++)
                         st[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, qf[qt][ks], st[kt][qt], 0, 0, 0);
                 }
             }
             // causal mask, online softmax per query
 #pragma unroll
-            for (uint32_t qt = 0; qt < 4; qt++) {
+            for (uint32_t qt = 0; qt < kQT; qt++) {
                 const uint32_t qpos = p0 + q0 + 16 * qt + col;
                 float mx = -INFINITY;
 #pragma unroll
@@ -671,9 +672,9 @@ __global__ __launch_bounds__(kGT) void k_pf_attn(const _Float16* Q16, const _Flo
             // permuted order as this lane's probabilities, B = P^T
 #pragma unroll
             for (uint32_t ks2 = 0; ks2 < 2; ks2++) {
-                h8v pb[4];
+                h8v pb[kQT];
 #pragma unroll
-                for (uint32_t qt = 0; qt < 4; qt++)
+                for (uint32_t qt = 0; qt < kQT; qt++)
 #pragma unroll
                     for (uint32_t i = 0; i < 4; i++) {
                         pb[qt][i] = (_Float16)st[2 * ks2][qt][i];
@@ -685,7 +686,7 @@ __global__ __launch_bounds__(kGT) void k_pf_attn(const _Float16* Q16, const _Flo
                     const uint2 lo = *reinterpret_cast<const uint2*>(vrow), hi = *reinterpret_cast<const uint2*>(vrow + 16);
                     const h8v va = __builtin_bit_cast(h8v, make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
-                    for (uint32_t qt = 0; qt < 4; qt++)
+                    for (uint32_t qt = 0; qt < kQT; qt++)
                         o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[qt], o[qt][dt], 0, 0, 0);
                 }
             }
@@ -694,7 +695,7 @@ __global__ __launch_bounds__(kGT) void k_pf_attn(const _Float16* Q16, const _Flo
     }
     if (!hok) return;
 #pragma unroll
-    for (uint32_t qt = 0; qt < 4; qt++) {
+    for (uint32_t qt = 0; qt < kQT; qt++) {
         float lt = l[qt] + __shfl_xor(l[qt], 16, 64);
         lt += __shfl_xor(lt, 32, 64);
         const float inv = 1.0f / lt;
