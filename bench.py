@@ -61,6 +61,20 @@ def algorithmic_bytes(model, pos_avg):
     return b
 
 
+def prefill_flops(model, n):
+    """Algorithmic flops of a batched prefill of n tokens from position 0:
+    every projection (q, k, v, o, F32 router, the top experts' gate/up/down)
+    as 2 flops per weight per token, causal attention as 4 flops per
+    (query, key, head dim) pair over keys 0..t, and the last token's vocab
+    projection."""
+    c = model.config
+    H, L, top, ff, E = c["hidden"], c["layers"], c["top"], c["intermediate"], c["experts"]
+    qd, kvd, heads, d = c["heads"] * c["head_dim"], c["kvheads"] * c["head_dim"], c["heads"], c["head_dim"]
+    per_tok_layer = 2 * (qd * H + 2 * kvd * H + H * qd + E * H + top * 3 * ff * H)
+    attn = heads * (n * (n + 1) / 2) * d * 4
+    return L * (n * per_tok_layer + attn) + 2 * c["vocab"] * H
+
+
 def matvec_cases(engine, synth, dev):
     """Single quantized matvecs at 30B-A3B shapes (W ~ N(0,0.02), k-quantized),
     rotating over >= 512 MB of distinct weight copies so every launch streams
@@ -136,6 +150,8 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-matvec", action="store_true")
+    ap.add_argument("--prefill", type=int, default=2048,
+                    help="tokens of the batched-prefill measurement (0: skip)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (a known-size "
                          "kernel that calibrates HBM byte counters)")
@@ -160,7 +176,7 @@ def main():
 
     alt_warmup, alt_steps = 4, 32
     ctx = args.prompt + args.warmup + args.steps + 2 * args.profile_steps + alt_warmup + alt_steps + 8
-    spec = synth.qwen30b(layers=args.layers, context=max(4096, ctx))
+    spec = synth.qwen30b(layers=args.layers, context=max(4096, ctx, args.prefill))
     threads = min(16, os.cpu_count() or 1)
     t0 = time.time()
     img = synth.build_image(spec, threads=threads)
@@ -216,6 +232,27 @@ def main():
     achieved = per_launch_bytes / (per_launch_ms * 1e-3) / 1e9
     log(f"dominant kernel {dom}: {per_launch_ms*1e3:.1f} us/launch, {achieved:.0f} GB/s")
 
+    prefill = None
+    if args.prefill > 0:
+        # batched prefill of a fresh sequence (fp16 matrix cores); the
+        # reference's prompt loop is one sequential forward per token
+        pp = rng.integers(0, spec.vocab, args.prefill).astype(np.uint32)
+        times = []
+        for _ in range(3):
+            model.reset()
+            t0 = time.perf_counter()
+            model.prefill(pp, want_logits=False)
+            times.append(time.perf_counter() - t0)
+        pms = sorted(times)[1] * 1e3
+        fl = prefill_flops(model, args.prefill)
+        tfs = fl / (pms * 1e-3) / 1e12
+        prefill = {"tokens": args.prefill, "ms": round(pms, 2), "tok_s": round(args.prefill / pms * 1e3, 1),
+                   "flops": int(fl), "sequential_decode_ms_estimate": round(args.prefill * ms_per_step, 1),
+                   "roofline": {"bound": "mfma", "achieved": round(tfs, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                                "frac": round(tfs / 2500.0, 4), "dtype": "f16 operands, f32 accumulate"}}
+        log(f"batched prefill {args.prefill} tokens: {pms:.1f} ms, {args.prefill / pms * 1e3:.0f} tok/s, "
+            f"{tfs:.0f} TFLOP/s")
+
     w_active = sum(bytes_cls[k] for k in ("qkv", "oproj", "gateup", "down", "vocab"))
     matvec = [] if args.no_matvec else matvec_cases(engine, synth, dev)
     cpu = None if args.no_cpu else cpu_baseline(img, spec, threads)
@@ -249,6 +286,7 @@ def main():
         "decode_launch": decode_launch,
         "per_phase_kernels": {"ms_per_token": round(ms_alt, 4), "tok_s": round(1000.0 / ms_alt, 2),
                               "breakdown": classes},
+        "prefill": prefill,
         "matvec": matvec,
         "cpu_baseline": cpu,
     }
