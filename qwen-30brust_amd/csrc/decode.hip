@@ -47,7 +47,7 @@ constexpr uint32_t kSpinLimit = 1u << 22;   // polls before a wait gives up
 constexpr uint32_t kDChunks = 32;           // most attention chunk workgroups per KV head
 constexpr uint32_t kDTile = 64;             // keys per attention tile (and at least per chunk)
 constexpr uint32_t kDSmem = 11264;          // floats of phase scratch
-constexpr uint32_t kQkvPerWave = 3;         // q/k/v rows per wave
+constexpr uint32_t kQkvPerWave = 3;         // q/k/v rows per wave (at most)
 constexpr uint32_t kPairsPerWave = 3;       // gate/up row pairs per wave
 constexpr uint32_t kHBlock = kPairsPerWave * kDW;  // SwiGLU outputs per workgroup
 constexpr uint32_t kDownUnits = 3;          // (expert, chunk) units per lane in F
@@ -215,27 +215,38 @@ __device__ __forceinline__ bool gather(const DecodeArgs& A, DecodeLds& S, const 
     return S.abort == 0;
 }
 
-// gather() preceded by a cheap readiness check: wave 0 first polls ns sample
-// words src[first + j * stride] (one per producer block, each block written
-// by one store instruction), and only then does the workgroup read all n
-// words.  A workgroup that waits long (for attention, say) thus polls a few
-// hundred bytes per round instead of the whole vector, so waiting workgroups
-// do not flood the memory channels that the producers are using.
+// gather() preceded by a cheap readiness check: wave 0 polls ns <= 256
+// sample words src[first + j * stride] (one per producer block, each block
+// written by one store instruction) until three quarters of the producers
+// have written, and only then does the workgroup read all n words (gather()
+// then re-reads only what is still missing).  A workgroup that waits long
+// (for attention, say) thus polls a few hundred bytes per round instead of
+// the whole vector and does not flood the memory channels the producers are
+// using, while the last quarter of the producers overlaps the bulk read.
 __device__ __forceinline__ bool gather_s(const DecodeArgs& A, DecodeLds& S, const uint64_t* src, uint32_t n,
                                          uint32_t tag, float* dst, uint32_t tid, uint32_t ns, uint32_t first,
                                          uint32_t stride) {
-    if (tid < 64) {
+    if (tid < 64) {  // wave 0
         bool ab = false;
-        for (uint32_t j0 = 0; j0 < ns && !ab; j0 += 256) {
-            uint32_t idx[4], need = 0;
+        uint32_t idx[4], need = 0;
 #pragma unroll
-            for (uint32_t k = 0; k < 4; k++) {
-                const uint32_t j = j0 + tid + 64 * k;
-                idx[k] = first + j * stride;
-                if (j < ns) need |= 1u << k;
-            }
-            float v[4];
-            poll_words<4>(A, src, idx, need, tag, v, ab);
+        for (uint32_t k = 0; k < 4; k++) {
+            const uint32_t j = tid + 64 * k;
+            idx[k] = first + j * stride;
+            if (j < ns) need |= 1u << k;
+        }
+        const float want = (float)(ns - ns / 4);
+        uint32_t spins = 0;
+        while (true) {
+            uint64_t w[4];
+#pragma unroll
+            for (uint32_t k = 0; k < 4; k++)
+                if ((need >> k) & 1) w[k] = __hip_atomic_load(src + idx[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+#pragma unroll
+            for (uint32_t k = 0; k < 4; k++)
+                if (((need >> k) & 1) && has_tag(w[k], tag)) need &= ~(1u << k);
+            const float done = (float)ns - wave_sum((float)__builtin_popcount(need));  // wave-uniform
+            if (done >= want || !keep_polling(A, spins, ab)) break;
         }
         if (ab) S.abort = 1;
     }
@@ -354,16 +365,47 @@ __device__ __forceinline__ void attn_prefetch(const DecodeArgs& A, const LayerW&
 // ================================================================== A: qkv ==
 // Flat rows [q | k | v]; wave gw owns rows gw, gw + NWV, gw + 2 NWV.  q and k
 // share format KQ, v has KV.  Rows have H <= 2048 columns: lane = chunk.
+// Phase A rows go to the workgroups that are not attention workgroups this
+// step (those start on their K/V history instead), when the others can take
+// every row at kQkvPerWave rows per wave; otherwise to every workgroup.
+// Returns false for a workgroup without A rows, else its wave index gw and
+// the wave count NWV of the row assignment.
+__device__ __forceinline__ bool qkv_rows(const DecodeArgs& A, const Ctx& c, uint32_t nt, uint32_t& gw,
+                                         uint32_t& NWV) {
+    const AttnChunk k = attn_chunk(A, c);
+    const uint32_t nattn = A.dm.kvheads * k.nch;
+    if (nt > kQkvPerWave * kDW * (c.nwg - nattn)) {
+        gw = c.gw;
+        NWV = c.NWV;
+        return true;
+    }
+    if (k.active) return false;
+    const uint32_t g0 = c.b / kDChunks;
+    const uint32_t below = g0 < A.dm.kvheads ? g0 * k.nch + min(c.b % kDChunks, k.nch) : nattn;
+    gw = (c.b - below) * kDW + c.wv;
+    NWV = (c.nwg - nattn) * kDW;
+    return true;
+}
+
 template <uint32_t KQ, uint32_t KV>
 __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
                                           uint32_t l, AttnPre& P) {
     const Ctx c = fresh(c0);
     const uint32_t nq = L.q.rows, nk = L.k.rows, nt = nq + nk + L.v.rows, cpr = c.H / 32;
+    uint32_t gw, NWV;
+    if (!qkv_rows(A, c, nt, gw, NWV)) {
+        // attention workgroup without A rows: its residual rows are still in
+        // S.xo from phase F, or come from x on the launch's first layer
+        attn_prefetch(A, L, c, P);
+        if (l == A.l0 && c.tid < c.nr) S.xo[c.tid] = ld_sys(A.a.x + c.r0 + c.tid);
+        __syncthreads();
+        return true;
+    }
     typename Fmt<KQ>::Raw wq[kQkvPerWave];
     typename Fmt<KV>::Raw wvv[kQkvPerWave];
 #pragma unroll
     for (uint32_t k = 0; k < kQkvPerWave; k++) {
-        const uint32_t r = c.gw + k * c.NWV;
+        const uint32_t r = gw + k * NWV;
         if (r < nq + nk && c.lane < cpr) {
             const DevMat& m = r < nq ? L.q : L.k;
             wq[k] = Fmt<KQ>::load(m.w + (size_t)(r < nq ? r : r - nq) * m.drb, m.geo, c.lane);
@@ -399,7 +441,7 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
     if (c.lane < cpr) x_runs<KQ>(xs, c.lane, xa, xb, sa, sb);
 #pragma unroll
     for (uint32_t k = 0; k < kQkvPerWave; k++) {
-        const uint32_t r = c.gw + k * c.NWV;
+        const uint32_t r = gw + k * NWV;
         if (r < nt) {  // wave-uniform
             float acc = 0.f;
             if (c.lane < cpr) {
@@ -416,6 +458,7 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
         }
     }
     QH_MARK(0, 2);
+    QH_MARK_LAST(2, 4);
     __syncthreads();  // xs is reused by the next phase
     return true;
 }
@@ -439,6 +482,7 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
     const ModelDims& dm = A.dm;
     const AttnChunk k = attn_chunk(A, c);
     if (!k.active) return true;  // not an attention workgroup this step
+    QH_MARK(2, 3);
     const uint32_t nch = k.nch, g = k.g, ch = k.ch, t0 = k.t0, t1 = k.t1;
     const uint32_t tid = c.tid, wv = c.wv, lane = c.lane, G = c.G, pos = c.pos, ctx = c.ctx;
     const bool holds = t0 <= pos && pos < t1;
@@ -535,7 +579,9 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
             if (part < G) ps[part * kDTile + kt] = mine / root;
         }
         if (tt + kDTile < t1) kv_slice(kr, vr, L.kcache, L.vcache, g, ctx, tt + kDTile, t1, pos, tid);
+        QH_MARK(1, 5);
         __syncthreads();
+        QH_MARK(1, 6);
         if (wv < G) {  // wave-uniform: online softmax and P.V of head wv
             const float sv = lane < nt ? ps[wv * kDTile + lane] : -INFINITY;
             const float M = fmaxf(mh, wave_max(sv));
@@ -547,6 +593,7 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
             o4.y *= alpha;
             o4.z *= alpha;
             o4.w *= alpha;
+            QH_MARK(1, 7);
             // keys t and t + 32 of the tile: e = 0 beyond nt, and V rows beyond
             // nt are skipped (they may hold any bits)
             const uint32_t nh = nt > kh * 32 ? min(32u, nt - kh * 32) : 0u;  // keys of this half

@@ -8,14 +8,17 @@
 namespace qh {
 
 // Phase marks of the token-step kernels: QH_MARK(kernel, phase) records the
-// wall clock of thread 0 of each workgroup when a translation unit that
-// defines QH_PHASE_TRACE (and qh_phase_mark) includes the kernels; otherwise
-// it compiles to nothing.
+// wall clock of thread 0 of each workgroup, QH_MARK_LAST that of its last
+// wave to get there, when a translation unit that defines QH_PHASE_TRACE (and
+// the two functions) includes the kernels; otherwise they compile to nothing.
 #ifdef QH_PHASE_TRACE
 __device__ void qh_phase_mark(int kernel, int phase);
+__device__ void qh_phase_mark_last(int kernel, int phase);
 #define QH_MARK(k, p) ::qh::qh_phase_mark((k), (p))
+#define QH_MARK_LAST(k, p) ::qh::qh_phase_mark_last((k), (p))
 #else
 #define QH_MARK(k, p) ((void)0)
+#define QH_MARK_LAST(k, p) ((void)0)
 #endif
 
 // ------------------------------------------------------------------ helpers --
