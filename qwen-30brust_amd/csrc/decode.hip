@@ -635,6 +635,7 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
             put(dst + 4 * j4 + 3, o4.w, tag);
             if (lane < 2) put(dst + 128 + lane, lane == 0 ? mh : lh, tag);
         }
+        QH_MARK(2, 6);
         return true;
     }
     if (wv < G) {  // wave-uniform
@@ -656,6 +657,7 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
             }
             float v[48];
             poll_pairs<24>(A, pr, word, need, need, tag, v, ab);
+            QH_MARK(2, 5);
             if (ab) break;
             float Mn = M;
 #pragma unroll
