@@ -41,12 +41,16 @@
 
 namespace qh {
 
+typedef float f4v __attribute__((ext_vector_type(4)));  // one MFMA accumulator tile per lane
+
 constexpr int kDT = 512;
 constexpr int kDW = kDT / 64;
 constexpr uint32_t kSpinLimit = 1u << 22;   // polls before a wait gives up
 constexpr uint32_t kDChunks = 32;           // most attention chunk workgroups per KV head
 constexpr uint32_t kDTile = 64;             // keys per attention tile (and at least per chunk)
-constexpr uint32_t kDSmem = 11264;          // floats of phase scratch
+constexpr uint32_t kTP = 132;               // LDS pitch of the key and value tiles (floats)
+constexpr uint32_t kPP = 68;                // LDS pitch of the per-head scores (floats)
+constexpr uint32_t kDSmem = 11776;          // floats of phase scratch
 constexpr uint32_t kQkvPerWave = 3;         // q/k/v rows per wave (at most)
 constexpr uint32_t kPairsPerWave = 3;       // gate/up row pairs per wave
 constexpr uint32_t kHBlock = kPairsPerWave * kDW;  // SwiGLU outputs per workgroup
@@ -503,11 +507,13 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
     }
     const float qa = qkv[0], qb = qkv[1], ka = qkv[2], kb = qkv[3], va = qkv[4], vb = qkv[5];
     QH_MARK(1, 1);
-    float* qs = S.big;               // [8][160]  normalised, rotated queries (parts padded to 20)
+    float* qs = S.big;               // [8][160]  normalised, rotated queries (16-dim parts padded to 20)
     float* kn = qs + 8 * 160;        // [160]     new key, same layout
     float* vn = kn + 160;            // [128]     new value
-    float* vs = vn + 128;            // [64][128] value tile
-    float* ps = vs + kDTile * 128;   // [8][64]   scores
+    float* vs = vn + 128;            // [64][kTP] value tile
+    float* ps = vs + kDTile * kTP;   // [8][kPP]  scores, then probabilities
+    float* al = ps + 8 * kPP;        // [8]       rescale factor of each head for this tile
+    float* ot = al + 8;              // [8][128]  output of the chunk
     // Q/K RMSNorm (model.rs:233-238) + NeoX RoPE (ops.rs:17-28)
     auto norm_rope = [&](float xa, float xb, float w0, float w1, float* dst, bool append) {
         const float ssq = wave_sum(fmaf(xb, xb, xa * xa));
@@ -541,9 +547,9 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
     if (S.abort) return false;
     QH_MARK(1, 4);
     const float root = sqrtf(128.0f);
-    const uint32_t part = tid & 7, kt = tid >> 3, j4 = lane & 31, kh = lane >> 5;
-    float mh = -INFINITY, lh = 0.f;               // head wv
-    float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);  // head wv, dims 4*j4, keys of half kh
+    const uint32_t part = tid & 7, kt = tid >> 3, j4 = lane & 31, grp = lane >> 4, col = lane & 15;
+    float mh = -INFINITY, lh = 0.f;     // softmax state of head wv
+    f4v oacc = {0.f, 0.f, 0.f, 0.f};    // O[head 4 grp + i][dim 16 wv + col]
     for (uint32_t tt = t0; tt < t1; tt += kDTile) {
         const uint32_t nt = min(kDTile, t1 - tt);
         if (tt + kt == pos) {
@@ -553,6 +559,8 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
                 vr[i] = reinterpret_cast<const float4*>(vn + part * 16)[i];
             }
         }
+        // scores: thread (key kt, 16-dim part) holds its K slice in registers;
+        // the 8 parts of each head reduce on DPP
         float mine = 0.f;
 #pragma unroll
         for (uint32_t h = 0; h < 8; h++) {
@@ -573,58 +581,52 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
             acc += dpp_f<kDppHalfMirror>(acc);
             mine = part == h ? acc : mine;
         }
-        if (kt < nt) {
+        {
+            // the value tile; keys beyond nt as zero rows (probability 0, and a
+            // zero row keeps P V finite)
+            const bool in = kt < nt;
 #pragma unroll
-            for (int i = 0; i < 4; i++) reinterpret_cast<float4*>(vs + kt * 128 + part * 16)[i] = vr[i];
-            if (part < G) ps[part * kDTile + kt] = mine / root;
+            for (int i = 0; i < 4; i++)
+                reinterpret_cast<float4*>(vs + kt * kTP + part * 16)[i] = in ? vr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (in && part < G) ps[part * kPP + kt] = mine / root;
         }
         if (tt + kDTile < t1) kv_slice(kr, vr, L.kcache, L.vcache, g, ctx, tt + kDTile, t1, pos, tid);
         QH_MARK(1, 5);
         __syncthreads();
         QH_MARK(1, 6);
-        if (wv < G) {  // wave-uniform: online softmax and P.V of head wv
-            const float sv = lane < nt ? ps[wv * kDTile + lane] : -INFINITY;
+        if (wv < G) {  // wave-uniform: online softmax of head wv
+            const float sv = lane < nt ? ps[wv * kPP + lane] : -INFINITY;
             const float M = fmaxf(mh, wave_max(sv));
             const float e = lane < nt ? expf(sv - M) : 0.f;
             const float alpha = expf(mh - M);  // 0 on the first tile
             lh = fmaf(lh, alpha, wave_sum(e));
             mh = M;
-            o4.x *= alpha;
-            o4.y *= alpha;
-            o4.z *= alpha;
-            o4.w *= alpha;
-            QH_MARK(1, 7);
-            // keys t and t + 32 of the tile: e = 0 beyond nt, and V rows beyond
-            // nt are skipped (they may hold any bits)
-            const uint32_t nh = nt > kh * 32 ? min(32u, nt - kh * 32) : 0u;  // keys of this half
-            const float* vrow = vs + kh * 32 * 128 + 4 * j4;
-            const uint32_t n32 = min(32u, nt);
-            for (uint32_t q0 = 0; q0 < n32; q0 += 8) {
-                float4 v[8];
+            ps[wv * kPP + lane] = e;
+            if (lane == 0) al[wv] = alpha;
+        }
+        QH_MARK(1, 7);
+        __syncthreads();
+        // O[h][d] = alpha_h O[h][d] + sum_key P[h][key] V[key][d]: M = heads,
+        // N = 16 dims per wave, K = 64 keys
 #pragma unroll
-                for (uint32_t k = 0; k < 8; k++)
-                    v[k] = q0 + k < nh ? *reinterpret_cast<const float4*>(vrow + (q0 + k) * 128)
-                                       : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                for (uint32_t k = 0; k < 8; k++) {
-                    const uint32_t t = q0 + k;
-                    const float p0 = lane_f(e, t & 31), p1 = lane_f(e, (t & 31) + 32);
-                    const float p = kh ? p1 : p0;
-                    o4.x = fmaf(p, v[k].x, o4.x);
-                    o4.y = fmaf(p, v[k].y, o4.y);
-                    o4.z = fmaf(p, v[k].z, o4.z);
-                    o4.w = fmaf(p, v[k].w, o4.w);
-                }
-            }
+        for (uint32_t i = 0; i < 4; i++) oacc[i] *= 4 * grp + i < G ? al[4 * grp + i] : 0.f;
+#pragma unroll 8
+        for (uint32_t k4 = 0; k4 < kDTile / 4; k4++) {
+            const uint32_t key = 4 * k4 + grp;
+            const float pa = col < G ? ps[col * kPP + key] : 0.f;
+            const float vb = vs[key * kTP + 16 * wv + col];
+            oacc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vb, oacc, 0, 0, 0);
         }
         __syncthreads();
     }
     QH_MARK(1, 2);
-    // the two key halves of each head
-    o4.x += shfl32(o4.x);
-    o4.y += shfl32(o4.y);
-    o4.z += shfl32(o4.z);
-    o4.w += shfl32(o4.w);
+    // O to LDS as [head][128], then lane (head wv, dims 4 j4)
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++)
+        if (4 * grp + i < G) ot[(4 * grp + i) * 128 + 16 * wv + col] = oacc[i];
+    __syncthreads();
+    const float4 o4 = wv < G ? reinterpret_cast<const float4*>(ot + wv * 128)[j4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const uint32_t kh = lane >> 5;
     const uint32_t mc = A.max_chunks;
     if (ch > 0) {  // pass the partial on to chunk 0
         if (wv < G && kh == 0) {
