@@ -74,6 +74,25 @@ int qh_tensor_info(const qh_ctx *ctx, const char *name, uint32_t *kind, size_t *
 /* Sum of tensor payload bytes (src/main.rs:128 packed_weight_bytes). */
 int qh_packed_weight_bytes(const qh_ctx *ctx, uint64_t *out);
 
+/* == the `inspect` command (src/main.rs:119-131): Gguf::open + Config::from_gguf
+ * + validate_tensors + the context check ("invalid context") + Config::kv_bytes
+ * (src/model.rs:150-156, "KV size overflow"), on the file at `path`, with no
+ * device work and no context object.  On failure qh_last_error(NULL) holds
+ * the message. */
+typedef struct {
+    qh_config_t config;
+    uint64_t tensor_count;
+    uint64_t packed_weight_bytes;
+    uint64_t kv_f32_bytes_at_context;
+} qh_inspect_t;
+int qh_inspect(const char *path, size_t context, qh_inspect_t *out);
+
+/* == `Vulkan::devices` (src/backend.rs:162-172) for HIP: number of devices and
+ * a one-line description "name (arch, CUs, GiB)" of device `device`.  On
+ * failure qh_last_error(NULL) holds the message. */
+int qh_device_count(int *out);
+int qh_device_name(int device, char *buf, size_t cap);
+
 /* == Backend::matvec (src/backend.rs:14-23, resolution as `matrix`
  * src/backend.rs:57-75): y[rows] = W x for tensor `name`, expert slab
  * `expert` (-1 = None).  Errors: missing tensor, rank mismatch, expert out

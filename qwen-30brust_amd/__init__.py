@@ -43,8 +43,16 @@ class _Config(C.Structure):
                [("eps", C.c_float), ("theta", C.c_float)]
 
 
+class _Inspect(C.Structure):
+    _fields_ = [("config", _Config), ("tensor_count", C.c_uint64), ("packed_weight_bytes", C.c_uint64),
+                ("kv_f32_bytes_at_context", C.c_uint64)]
+
+
 _SIGS = {
     "qh_create": (C.c_int, [C.c_int, C.POINTER(C.c_void_p)]),
+    "qh_inspect": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(_Inspect)]),
+    "qh_device_count": (C.c_int, [C.POINTER(C.c_int)]),
+    "qh_device_name": (C.c_int, [C.c_int, C.c_char_p, C.c_size_t]),
     "qh_destroy": (None, [C.c_void_p]),
     "qh_last_error": (C.c_char_p, [C.c_void_p]),
     "qh_load_model": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t]),
@@ -107,6 +115,32 @@ def _ptr(a):
 
 def _f32(x):
     return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def inspect(path, ctx=4096):
+    """The reference's `inspect` command (src/main.rs:119-131) as a dict:
+    config, tensor_count, packed_weight_bytes, kv_f32_bytes_at_context.
+    Parses and validates the file without any device work."""
+    r = _Inspect()
+    if lib().qh_inspect(os.fsencode(str(path)), ctx, C.byref(r)) != 0:
+        raise EngineError(lib().qh_last_error(None).decode())
+    return {"config": {n: getattr(r.config, n) for n, _ in _Config._fields_},
+            "tensor_count": r.tensor_count, "packed_weight_bytes": r.packed_weight_bytes,
+            "kv_f32_bytes_at_context": r.kv_f32_bytes_at_context}
+
+
+def devices():
+    """One description per HIP device (the reference's `devices` command)."""
+    n = C.c_int(0)
+    if lib().qh_device_count(C.byref(n)) != 0:
+        raise EngineError(lib().qh_last_error(None).decode())
+    out = []
+    buf = C.create_string_buffer(512)
+    for d in range(n.value):
+        if lib().qh_device_name(d, buf, len(buf)) != 0:
+            raise EngineError(lib().qh_last_error(None).decode())
+        out.append(buf.value.decode())
+    return out
 
 
 class Device:

@@ -1,5 +1,6 @@
-"""Build recipe for the engine (libqwen_hip.so, hipcc for gfx950) and the
-synthetic-model generator (libqwen_synth.so, host-only g++).
+"""Build recipe for the engine (libqwen_hip.so, hipcc for gfx950), its
+command-line driver (qwen-hip) and the synthetic-model generator
+(libqwen_synth.so, host-only g++).
 
 Usage: python qwen-30brust_amd/build.py   (compiles every time it is called)
 """
@@ -14,6 +15,7 @@ CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 ENGINE_SO = os.path.join(PKG, "libqwen_hip.so")
 SYNTH_SO = os.path.join(PKG, "libqwen_synth.so")
+CLI = os.path.join(PKG, "qwen-hip")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
@@ -49,7 +51,18 @@ def build_engine():
     tmp = ENGINE_SO + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, ENGINE_SO)
+    build_cli()
     return ENGINE_SO
+
+
+def build_cli():
+    """qwen-hip, the command-line driver over the C ABI (links libqwen_hip.so
+    from its own directory)."""
+    tmp = CLI + ".tmp"
+    _run(["g++", "-O2", "-std=c++17", "-Wall", os.path.join(CSRC, "cli.cpp"), "-o", tmp,
+          "-L", PKG, "-lqwen_hip", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, CLI)
+    return CLI
 
 
 def build_synth():

@@ -602,6 +602,31 @@ void launch_step(qh_ctx* c) {
     }
 }
 
+// Read-only mapping of a whole file, unmapped when it goes out of scope.
+struct MappedFile {
+    const uint8_t* data = nullptr;
+    size_t len = 0;
+    explicit MappedFile(const char* path) {
+        const int fd = open(path, O_RDONLY);
+        if (fd < 0) throw Error(std::string("open ") + path);
+        struct stat sb;
+        if (fstat(fd, &sb) != 0) {
+            close(fd);
+            throw Error(std::string("stat ") + path);
+        }
+        len = (size_t)sb.st_size;
+        void* m = len ? mmap(nullptr, len, PROT_READ, MAP_PRIVATE, fd, 0) : nullptr;
+        close(fd);
+        if (len && m == MAP_FAILED) throw Error(std::string("mmap ") + path);
+        data = static_cast<const uint8_t*>(m);
+    }
+    ~MappedFile() {
+        if (len) munmap(const_cast<uint8_t*>(data), len);
+    }
+    MappedFile(const MappedFile&) = delete;
+    MappedFile& operator=(const MappedFile&) = delete;
+};
+
 void load_image(qh_ctx* c, const uint8_t* data, size_t len, size_t context) {
     Gguf g = parse_gguf(data, len);
     Config cfg = config_from_gguf(g);
@@ -895,23 +920,66 @@ int qh_load_model(qh_ctx* c, const void* image, size_t len, size_t context) {
 
 int qh_load_model_file(qh_ctx* c, const char* path, size_t context) {
     return guarded(c, [&] {
-        int fd = open(path, O_RDONLY);
-        if (fd < 0) throw Error(std::string("open ") + path);
-        struct stat sb;
-        if (fstat(fd, &sb) != 0) { close(fd); throw Error(std::string("stat ") + path); }
-        size_t len = (size_t)sb.st_size;
-        void* m = len ? mmap(nullptr, len, PROT_READ, MAP_PRIVATE, fd, 0) : nullptr;
-        close(fd);
-        if (len && m == MAP_FAILED) throw Error(std::string("mmap ") + path);
-        try {
-            HIP_OK(hipSetDevice(c->device));
-            load_image(c, static_cast<const uint8_t*>(m), len, context);
-        } catch (...) {
-            if (len) munmap(m, len);
-            throw;
-        }
-        if (len) munmap(m, len);
+        const MappedFile f(path);
+        HIP_OK(hipSetDevice(c->device));
+        load_image(c, f.data, f.len, context);
     });
+}
+
+int qh_inspect(const char* path, size_t context, qh_inspect_t* out) {
+    try {
+        const MappedFile f(path);
+        const Gguf g = parse_gguf(f.data, f.len);
+        const Config cfg = config_from_gguf(g);
+        validate_tensors(cfg, g);
+        if (!(context > 0 && context <= cfg.max_context)) throw Error("invalid context");
+        // ctx * layers * kvheads * head_dim * 8 with overflow checks (src/model.rs:150-156)
+        uint64_t kv = context;
+        for (uint64_t m : {cfg.layers, cfg.kvheads, cfg.head_dim, (uint64_t)8})
+            if (__builtin_mul_overflow(kv, m, &kv)) throw Error("KV size overflow");
+        out->config = {cfg.hidden, cfg.layers, cfg.heads, cfg.kvheads, cfg.head_dim, cfg.experts, cfg.top,
+                       cfg.intermediate, cfg.vocab, cfg.max_context, cfg.eps, cfg.theta};
+        out->tensor_count = g.tensors.size();
+        out->packed_weight_bytes = g.packed_bytes();
+        out->kv_f32_bytes_at_context = kv;
+        return 0;
+    } catch (const std::exception& e) {
+        g_create_err = e.what();
+        return 1;
+    }
+}
+
+int qh_device_count(int* out) {
+    try {
+        int n = 0;
+        HIP_OK(hipGetDeviceCount(&n));
+        *out = n;
+        return 0;
+    } catch (const std::exception& e) {
+        g_create_err = e.what();
+        return 1;
+    }
+}
+
+int qh_device_name(int device, char* buf, size_t cap) {
+    try {
+        int n = 0;
+        HIP_OK(hipGetDeviceCount(&n));
+        if (device < 0 || device >= n) throw Error("HIP device " + std::to_string(device) + " not present");
+        hipDeviceProp_t p;
+        HIP_OK(hipGetDeviceProperties(&p, device));
+        char arch[sizeof(p.gcnArchName) + 1] = {};
+        std::memcpy(arch, p.gcnArchName, sizeof(p.gcnArchName));
+        if (char* colon = std::strchr(arch, ':')) *colon = 0;
+        const std::string s = std::string(p.name) + " (" + arch + ", " + std::to_string(p.multiProcessorCount) +
+                              " CUs, " + std::to_string(p.totalGlobalMem >> 30) + " GiB)";
+        if (cap == 0 || s.size() + 1 > cap) throw Error("device name buffer too small");
+        std::memcpy(buf, s.c_str(), s.size() + 1);
+        return 0;
+    } catch (const std::exception& e) {
+        g_create_err = e.what();
+        return 1;
+    }
 }
 
 int qh_model_config(const qh_ctx* c, qh_config_t* out) {

@@ -351,6 +351,20 @@ uint64_t qs_packed_bytes(const qs_spec* s) {
     return n;
 }
 
+// Writes only the header of the image (through the alignment padding before
+// the tensor data) into out[0..cap); *total receives the full image size.
+// Returns the header length, 0 on an invalid spec or a short buffer.
+size_t qs_header(const qs_spec* s, uint8_t* out, size_t cap, size_t* total) {
+    auto t = plan(s);
+    Buf b;
+    size_t ds, tot;
+    if (!header(s, t, b, ds, tot) || cap < ds) return 0;
+    std::memcpy(out, b.v.data(), b.v.size());
+    std::memset(out + b.v.size(), 0, ds - b.v.size());
+    *total = tot;
+    return ds;
+}
+
 // Writes the GGUF image into out[0..len).  Returns 0 on success.
 int qs_build(const qs_spec* s, uint8_t* out, size_t len, int threads) {
     auto t = plan(s);

@@ -126,6 +126,8 @@ def lib():
         l.qs_packed_bytes.argtypes = [C.POINTER(_Spec)]
         l.qs_build.restype = C.c_int
         l.qs_build.argtypes = [C.POINTER(_Spec), C.c_void_p, C.c_size_t, C.c_int]
+        l.qs_header.restype = C.c_size_t
+        l.qs_header.argtypes = [C.POINTER(_Spec), C.c_void_p, C.c_size_t, C.POINTER(C.c_size_t)]
         l.qs_quantize.restype = C.c_int
         l.qs_quantize.argtypes = [C.c_uint32, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]
         l.qs_normal.restype = None
@@ -155,6 +157,22 @@ def build_image(spec, threads=None):
     if lib().qs_build(C.byref(s), out.ctypes.data, n, threads) != 0:
         raise RuntimeError("qs_build failed")
     return out
+
+
+def write_header_only(spec, path):
+    """Writes the image's header to `path` and extends the file to the full
+    image size without writing the tensor data (a sparse file: the data reads
+    as zeros).  Enough for header parsing and validation at full size."""
+    s = spec._c()
+    buf = np.zeros(1 << 20, np.uint8)
+    total = C.c_size_t(0)
+    n = lib().qs_header(C.byref(s), buf.ctypes.data, buf.size, C.byref(total))
+    if n == 0:
+        raise ValueError("invalid synthetic model spec")
+    with open(path, "wb") as f:
+        f.write(buf[:n].tobytes())
+        f.truncate(total.value)
+    return total.value
 
 
 def quantize(kind, x):
