@@ -67,12 +67,12 @@ constexpr uint32_t kGatherPairs = 6;        // word pairs in flight per thread i
     }
 
 struct DecodeLds {
-    long long ck[256];        // composite top-k keys
     float big[kDSmem];        // phase scratch (x, attention tiles, h)
     float xo[8];              // this workgroup's rows of the residual stream
-    float hv[kHBlock];        // this workgroup's SwiGLU outputs
+    float hv[kHBlock];        // this workgroup's phase A rows, then its SwiGLU outputs
     float red[2 * kDW];
     float lg[256];            // router logits
+    alignas(16) long long ck[128];  // composite top-k keys
     float sv[8];
     uint32_t sid[8];
     float ex[8];
@@ -367,27 +367,44 @@ __device__ __forceinline__ void attn_prefetch(const DecodeArgs& A, const LayerW&
 }
 
 // ================================================================== A: qkv ==
-// Flat rows [q | k | v]; wave gw owns rows gw, gw + NWV, gw + 2 NWV.  q and k
-// share format KQ, v has KV.  Rows have H <= 2048 columns: lane = chunk.
-// Phase A rows go to the workgroups that are not attention workgroups this
-// step (those start on their K/V history instead), when the others can take
-// every row at kQkvPerWave rows per wave; otherwise to every workgroup.
-// Returns false for a workgroup without A rows, else its wave index gw and
-// the wave count NWV of the row assignment.
-__device__ __forceinline__ bool qkv_rows(const DecodeArgs& A, const Ctx& c, uint32_t nt, uint32_t& gw,
-                                         uint32_t& NWV) {
+// Flat rows [q | k | v]; q and k share format KQ, v has KV.  Rows have
+// H <= 2048 columns: lane = chunk.  Participating workgroup wi owns two
+// contiguous blocks, q|k rows [wi Rqk, wi Rqk + Rqk) and v rows
+// [wi Rv, wi Rv + Rv) (Rqk = ceil(nqk / workgroups), Rv likewise, so the
+// heavier v rows spread over all workgroups), Rqk + Rv <= 24 slots; wave wv
+// computes slots wv + 8 k, and the workgroup passes each block on with one
+// store instruction.  Phase A rows go to the workgroups that are not
+// attention workgroups this step (those start on their K/V history instead)
+// when the blocks fit there; otherwise to every workgroup.  Returns false for
+// a workgroup without A rows.
+struct QkvRows {
+    uint32_t qk0, nqk, v0, nv;  // first row and count of each block (counts may be 0)
+};
+
+__device__ __forceinline__ uint32_t qkv_slots(uint32_t nqk, uint32_t nv, uint32_t nw) {
+    return (nqk + nw - 1) / nw + (nv + nw - 1) / nw;
+}
+
+__device__ __forceinline__ bool qkv_rows(const DecodeArgs& A, const Ctx& c, uint32_t nqk, uint32_t nv,
+                                         QkvRows& q) {
     const AttnChunk k = attn_chunk(A, c);
     const uint32_t nattn = A.dm.kvheads * k.nch;
-    if (nt > kQkvPerWave * kDW * (c.nwg - nattn)) {
-        gw = c.gw;
-        NWV = c.NWV;
-        return true;
+    uint32_t wi, nw;
+    if (qkv_slots(nqk, nv, c.nwg - nattn) > kQkvPerWave * kDW) {
+        wi = c.b;
+        nw = c.nwg;
+    } else {
+        if (k.active) return false;
+        const uint32_t g0 = c.b / kDChunks;
+        const uint32_t below = g0 < A.dm.kvheads ? g0 * k.nch + min(c.b % kDChunks, k.nch) : nattn;
+        wi = c.b - below;
+        nw = c.nwg - nattn;
     }
-    if (k.active) return false;
-    const uint32_t g0 = c.b / kDChunks;
-    const uint32_t below = g0 < A.dm.kvheads ? g0 * k.nch + min(c.b % kDChunks, k.nch) : nattn;
-    gw = (c.b - below) * kDW + c.wv;
-    NWV = (c.nwg - nattn) * kDW;
+    const uint32_t Rqk = (nqk + nw - 1) / nw, Rv = (nv + nw - 1) / nw;
+    q.qk0 = min(wi * Rqk, nqk);
+    q.nqk = min(nqk - q.qk0, Rqk);
+    q.v0 = min(wi * Rv, nv);
+    q.nv = min(nv - q.v0, Rv);
     return true;
 }
 
@@ -396,8 +413,8 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
                                           uint32_t l, AttnPre& P) {
     const Ctx c = fresh(c0);
     const uint32_t nq = L.q.rows, nk = L.k.rows, nt = nq + nk + L.v.rows, cpr = c.H / 32;
-    uint32_t gw, NWV;
-    if (!qkv_rows(A, c, nt, gw, NWV)) {
+    QkvRows B;
+    if (!qkv_rows(A, c, nq + nk, L.v.rows, B)) {
         // attention workgroup without A rows: its residual rows are still in
         // S.xo from phase F, or come from x on the launch's first layer
         attn_prefetch(A, L, c, P);
@@ -407,9 +424,12 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
     }
     typename Fmt<KQ>::Raw wq[kQkvPerWave];
     typename Fmt<KV>::Raw wvv[kQkvPerWave];
+    // slot j: q|k row qk0 + j (j < nqk), else v row v0 + j - nqk; flat row r
 #pragma unroll
     for (uint32_t k = 0; k < kQkvPerWave; k++) {
-        const uint32_t r = gw + k * NWV;
+        const uint32_t j = c.wv + kDW * k;
+        if (j >= B.nqk + B.nv) continue;
+        const uint32_t r = j < B.nqk ? B.qk0 + j : nq + nk + B.v0 + (j - B.nqk);
         if (r < nq + nk && c.lane < cpr) {
             const DevMat& m = r < nq ? L.q : L.k;
             wq[k] = Fmt<KQ>::load(m.w + (size_t)(r < nq ? r : r - nq) * m.drb, m.geo, c.lane);
@@ -445,8 +465,9 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
     if (c.lane < cpr) x_runs<KQ>(xs, c.lane, xa, xb, sa, sb);
 #pragma unroll
     for (uint32_t k = 0; k < kQkvPerWave; k++) {
-        const uint32_t r = gw + k * NWV;
-        if (r < nt) {  // wave-uniform
+        const uint32_t j = c.wv + kDW * k;
+        const uint32_t r = j < B.nqk ? B.qk0 + j : nq + nk + B.v0 + (j - B.nqk);
+        if (j < B.nqk + B.nv) {  // wave-uniform
             float acc = 0.f;
             if (c.lane < cpr) {
                 if (r < nq + nk) {
@@ -458,12 +479,15 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
                 }
             }
             acc = wave_sum(acc);
-            if (c.lane == 0) put(A.tqkv + r, acc, tag);
+            if (c.lane == 0) S.hv[j] = acc;
         }
     }
     QH_MARK(0, 2);
     QH_MARK_LAST(2, 4);
-    __syncthreads();  // xs is reused by the next phase
+    __syncthreads();  // S.hv complete; xs is reused by the next phase
+    // the two blocks, one store instruction each (waves 0 and 1)
+    if (c.tid < B.nqk) put(A.tqkv + B.qk0 + c.tid, S.hv[c.tid], tag);
+    if (c.tid >= 64 && c.tid - 64 < B.nv) put(A.tqkv + nq + nk + B.v0 + (c.tid - 64), S.hv[B.nqk + c.tid - 64], tag);
     return true;
 }
 
@@ -628,13 +652,11 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
     const float4 o4 = wv < G ? reinterpret_cast<const float4*>(ot + wv * 128)[j4] : make_float4(0.f, 0.f, 0.f, 0.f);
     const uint32_t kh = lane >> 5;
     const uint32_t mc = A.max_chunks;
-    if (ch > 0) {  // pass the partial on to chunk 0
-        if (wv < G && kh == 0) {
+    if (ch > 0) {  // pass the partial on to chunk 0: lane writes dims lane, lane + 64
+        if (wv < G) {
             uint64_t* dst = A.tpart + ((size_t)(g * G + wv) * mc + ch) * kPartWords;
-            put(dst + 4 * j4, o4.x, tag);
-            put(dst + 4 * j4 + 1, o4.y, tag);
-            put(dst + 4 * j4 + 2, o4.z, tag);
-            put(dst + 4 * j4 + 3, o4.w, tag);
+            put(dst + lane, ot[wv * 128 + lane], tag);
+            put(dst + 64 + lane, ot[wv * 128 + 64 + lane], tag);
             if (lane < 2) put(dst + 128 + lane, lane == 0 ? mh : lh, tag);
         }
         QH_MARK(2, 6);
@@ -687,16 +709,21 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
         // the two halves (a half without chunks has M = -inf and adds 0)
         const float Mo = shfl32(M), Lo = shfl32(Ls);
         const float4 Oo = make_float4(shfl32(O.x), shfl32(O.y), shfl32(O.z), shfl32(O.w));
-        if (kh == 0) {
+        if (kh == 0) {  // back into this wave's own row of ot (read above by this wave only)
             const float Mn = fmaxf(M, Mo);
             const float f0 = expf(M - Mn), f1 = expf(Mo - Mn);
             const float inv = 1.0f / fmaf(Ls, f0, Lo * f1);
-            uint64_t* out = A.tatt + (g * G + wv) * 128 + 4 * j4;
-            put(out, fmaf(O.x, f0, Oo.x * f1) * inv, tag);
-            put(out + 1, fmaf(O.y, f0, Oo.y * f1) * inv, tag);
-            put(out + 2, fmaf(O.z, f0, Oo.z * f1) * inv, tag);
-            put(out + 3, fmaf(O.w, f0, Oo.w * f1) * inv, tag);
+            reinterpret_cast<float4*>(ot + wv * 128)[j4] =
+                make_float4(fmaf(O.x, f0, Oo.x * f1) * inv, fmaf(O.y, f0, Oo.y * f1) * inv,
+                            fmaf(O.z, f0, Oo.z * f1) * inv, fmaf(O.w, f0, Oo.w * f1) * inv);
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // each store instruction writes 64 consecutive words (whole lines)
+        uint64_t* out = A.tatt + (g * G + wv) * 128;
+        put(out + lane, ot[wv * 128 + lane], tag);
+        put(out + 64 + lane, ot[wv * 128 + 64 + lane], tag);
     }
     if (ab) S.abort = 1;
     QH_MARK(1, 3);
@@ -786,14 +813,14 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
     if (!gather(A, S, A.tlog, E, ptag(A, l, 4), S.lg, c.tid)) return false;  // router logits (phase D)
     QH_MARK(4, 1);
     // top-k by rank under the total order, lower index on ties (ops.rs:45-56;
-    // bit-exact on these logits): j outranks i iff ck[j] > ck[i]
-    const uint32_t Ep = (E + 7) & ~7u;
-    if (c.tid < E) {
-        const float lv = S.lg[c.tid];
+    // bit-exact on these logits): j outranks i iff ck[j] > ck[i], with the
+    // composite key ck = (total-order key of the logit, ~index); experts
+    // E..127 get the smallest key and outrank nothing (E <= 128)
+    if (c.tid < 128) {
+        const float lv = c.tid < E ? S.lg[c.tid] : 0.f;
         if (!finite_f(lv)) S.bad = 1;
-        S.ck[c.tid] = (long long)(((uint64_t)(uint32_t)total_key(lv) << 32) | (uint32_t)~c.tid);
-    } else if (c.tid < Ep) {
-        S.ck[c.tid] = LLONG_MIN;
+        S.ck[c.tid] = c.tid < E ? (long long)(((uint64_t)(uint32_t)total_key(lv) << 32) | (uint32_t)~c.tid)
+                                : LLONG_MIN;
     }
     __syncthreads();
     if (S.bad) {
@@ -801,10 +828,12 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         return false;  // every workgroup sees the same logits
     }
     {
-        const uint32_t i = c.tid >> 2, q = c.tid & 3, J = Ep / 4, j0 = q * J;
-        const long long ki = S.ck[min(i, Ep - 1)];
+        // thread (i, q) counts the keys of quarter q (32 of them) above expert i's
+        const uint32_t i = c.tid >> 2, q = c.tid & 3;
+        const long long ki = S.ck[i];
         int32_t rank = 0;
-        for (uint32_t j = j0; j < j0 + J; j += 2) {
+#pragma unroll
+        for (uint32_t j = 32 * q; j < 32 * q + 32; j += 2) {
             const longlong2 w2 = *reinterpret_cast<const longlong2*>(S.ck + j);
             rank += (w2.x > ki) + (w2.y > ki);
         }
@@ -816,18 +845,18 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         }
     }
     __syncthreads();
-    // softmax over the selected logits (ops.rs:29-44) on wave 0, lane k = rank k
-    if (c.wv == 0) {  // wave-uniform
+    // softmax over the selected logits (ops.rs:29-44), in every wave, lane k =
+    // rank k; wave 0 keeps the result in LDS for phase F
+    {
         const float v = c.lane < top ? S.sv[c.lane] : -INFINITY;
         const float mx = wave_max(v);
         const float e = c.lane < top ? expf(v - mx) : 0.f;
-        const float sum = wave_sum(e);
-        if (c.lane < top) {
+        const float w = e / wave_sum(e);
+        if (c.wv == 0 && c.lane < top) {
             S.ids[c.lane] = S.sid[c.lane];
-            S.wts[c.lane] = e / sum;
+            S.wts[c.lane] = w;
         }
     }
-    __syncthreads();
     QH_MARK(4, 2);
     // gate/up rows of pairs p = gw*3 + k: (slot p / ff, row p % ff)
     typename Fmt<KG>::Raw wg[kPairsPerWave], wu[kPairsPerWave];
@@ -835,7 +864,7 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
     for (uint32_t k = 0; k < kPairsPerWave; k++) {
         const uint32_t pr = c.gw * kPairsPerWave + k;
         if (pr < top * ff && c.lane < cpr) {
-            const uint32_t ex = S.ids[pr / ff], rr = pr % ff;
+            const uint32_t ex = S.sid[pr / ff], rr = pr % ff;
             wg[k] = Fmt<KG>::load(L.gate.w + (size_t)ex * L.gate.expert_stride + (size_t)rr * L.gate.drb, L.gate.geo,
                                   c.lane);
             wu[k] = Fmt<KG>::load(L.up.w + (size_t)ex * L.up.expert_stride + (size_t)rr * L.up.drb, L.up.geo, c.lane);

@@ -506,7 +506,9 @@ bool persist_supported(const qh_ctx* c, uint32_t nwg) {
         if (!(L.q.kind == Q4_K && L.k.kind == Q4_K && L.o.kind == Q4_K && L.gate.kind == Q4_K &&
               L.up.kind == Q4_K && km(L.v.kind) && km(L.down.kind) && L.router.kind == F32))
             return false;
-        if ((uint64_t)L.q.rows + L.k.rows + L.v.rows > 3ull * NWV) return false;
+        // phase A: q|k and v row blocks of every workgroup fit its 24 slots
+        const uint64_t nqk = (uint64_t)L.q.rows + L.k.rows;
+        if ((nqk + nwg - 1) / nwg + (L.v.rows + nwg - 1) / nwg > 24) return false;
     }
     return true;
 }
