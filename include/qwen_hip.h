@@ -137,6 +137,27 @@ int qh_forward(qh_ctx *ctx, uint32_t token, float *logits, uint32_t *argmax);
  * produced the last generated token. */
 int qh_generate(qh_ctx *ctx, const uint32_t *prompt, size_t n_prompt, size_t n_new,
                 uint32_t *out_tokens, float *logits_last);
+/* == Sampler (src/sampling.rs:3-65) with its rand 0.8.8 StdRng stream
+ * (ChaCha12 seeded by seed_from_u64), host-side state: qh_sampler_create
+ * replaces Sampler::new (src/sampling.rs:10-25) with its check ("invalid
+ * sampling parameters", message in qh_last_error(NULL)); top_k 0 = no
+ * truncation.  qh_sampler_draw returns the stream's next rng.gen::<f32>(). */
+typedef struct qh_sampler qh_sampler;
+int qh_sampler_create(uint64_t seed, float temperature, size_t top_k, float top_p, qh_sampler **out);
+void qh_sampler_destroy(qh_sampler *sampler);
+int qh_sampler_draw(qh_sampler *sampler, float *out);
+/* The padding-vocab mask of src/main.rs:262-266: ids with valid[id] == 0 read
+ * as f32::MIN in qh_sample (vocab bytes; NULL clears it). */
+int qh_set_valid_tokens(qh_ctx *ctx, const uint8_t *valid, size_t n);
+/* == Sampler::sample (src/sampling.rs:26-63) on the logits of the last token
+ * step, on the device: greedy at temperature 0, else top-k, temperature,
+ * top-p and one draw from the stream (consumed only on success).  Errors:
+ * "invalid logits"; more than 4096 ids with nonzero probability when top_k is
+ * 0 or above 4096 (a limit of the device sampler). */
+int qh_sample(qh_ctx *ctx, qh_sampler *sampler, uint32_t *out);
+/* The same on n caller logits with an optional mask (valid may be NULL). */
+int qh_sample_logits(qh_ctx *ctx, qh_sampler *sampler, const float *logits, const uint8_t *valid,
+                     size_t n, uint32_t *out);
 /* == Model::reset (src/model.rs:202-208). */
 int qh_reset(qh_ctx *ctx);
 /* == Model::position (src/model.rs:170). */

@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference
  * CPU path (src/quant.rs, src/ops.rs, src/gguf.rs, src/model.rs,
- * src/backend.rs `Cpu`, src/sampling.rs greedy branch).  It is the checker
+ * src/backend.rs `Cpu`, src/sampling.rs with rand's StdRng restated).  It is the checker
  * the HIP engine is compared against; it is never linked into the engine and
  * nothing in the engine calls it.  Only tests/, __graft_entry__.smoke() and
  * bench.py's CPU-baseline leg load it.
@@ -49,6 +49,18 @@ int or_attention(const float *q, const float *k, const float *v, size_t klen,
 
 /* ---- sampling.rs (greedy branch) ---------------------------------------- */
 int or_greedy(const float *logits, size_t n, uint32_t *out);          /* sampling.rs:26-35 */
+
+/* ---- sampling.rs (stochastic branch) and rand's StdRng ------------------ */
+/* ChaCha block function (djb layout: 64-bit counter in words 12-13, 64-bit
+ * stream in 14-15), `rounds` = 20 for ChaCha20, 12 for StdRng. */
+void or_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, int rounds, uint32_t out[16]);
+/* rand_core 0.6.4 SeedableRng::seed_from_u64 seed expansion (PCG32). */
+void or_stdrng_seed(uint64_t seed, uint32_t key[8]);
+typedef struct or_sampler or_sampler;
+or_sampler *or_sampler_new(uint64_t seed, float temperature, size_t top_k, float top_p); /* sampling.rs:10-25 */
+void or_sampler_free(or_sampler *s);
+float or_sampler_draw(or_sampler *s);                                 /* rng.gen::<f32>() */
+int or_sampler_sample(or_sampler *s, const float *logits, size_t n, uint32_t *out); /* sampling.rs:26-63 */
 
 /* ---- backend.rs Cpu::matvec on a packed matrix -------------------------- */
 /* threads == 0: faithful path (per-element or_value, one thread), the

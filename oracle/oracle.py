@@ -45,6 +45,12 @@ def _load():
         "or_route": (i32, [_f32p, sz, sz, _u32p, _f32p]),
         "or_attention": (i32, [_f32p, _f32p, _f32p, sz, sz, sz, sz, _f32p]),
         "or_greedy": (i32, [_f32p, sz, C.POINTER(u32)]),
+        "or_chacha_block": (None, [C.POINTER(u32 * 8), C.c_uint64, C.c_uint64, i32, C.POINTER(u32 * 16)]),
+        "or_stdrng_seed": (None, [C.c_uint64, C.POINTER(u32 * 8)]),
+        "or_sampler_new": (C.c_void_p, [C.c_uint64, f32, sz, f32]),
+        "or_sampler_free": (None, [C.c_void_p]),
+        "or_sampler_draw": (f32, [C.c_void_p]),
+        "or_sampler_sample": (i32, [C.c_void_p, _f32p, sz, C.POINTER(u32)]),
         "or_packed_matvec": (i32, [_u8p, sz, u32, sz, sz, _f32p, _f32p, i32]),
         "or_gguf_open": (C.c_void_p, [C.c_void_p, sz]),
         "or_gguf_free": (None, [C.c_void_p]),
@@ -175,6 +181,42 @@ def greedy(logits):
     out = C.c_uint32()
     _check(lib().or_greedy(logits, logits.size, C.byref(out)))
     return out.value
+
+
+def chacha_block(key, counter, stream=0, rounds=12):
+    k = (C.c_uint32 * 8)(*key)
+    out = (C.c_uint32 * 16)()
+    lib().or_chacha_block(C.byref(k), counter, stream, rounds, C.byref(out))
+    return list(out)
+
+
+def stdrng_key(seed):
+    k = (C.c_uint32 * 8)()
+    lib().or_stdrng_seed(seed, C.byref(k))
+    return list(k)
+
+
+class Sampler:
+    """sampling.rs `Sampler` (seeded StdRng stream, top-k, temperature, top-p)."""
+
+    def __init__(self, seed, temperature, top_k, top_p):
+        self._p = lib().or_sampler_new(seed, temperature, top_k, top_p)
+        if not self._p:
+            raise OracleError(_err())
+
+    def __del__(self):
+        if getattr(self, "_p", None):
+            lib().or_sampler_free(self._p)
+            self._p = None
+
+    def draw(self):
+        return lib().or_sampler_draw(self._p)
+
+    def sample(self, logits):
+        logits = np.ascontiguousarray(logits, np.float32)
+        out = C.c_uint32()
+        _check(lib().or_sampler_sample(self._p, logits, logits.size, C.byref(out)))
+        return out.value
 
 
 def packed_matvec(data, kind, rows, cols, x, threads=0):

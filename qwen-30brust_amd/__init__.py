@@ -52,6 +52,13 @@ _SIGS = {
     "qh_create": (C.c_int, [C.c_int, C.POINTER(C.c_void_p)]),
     "qh_inspect": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(_Inspect)]),
     "qh_device_count": (C.c_int, [C.POINTER(C.c_int)]),
+    "qh_sampler_create": (C.c_int, [C.c_uint64, C.c_float, C.c_size_t, C.c_float, C.POINTER(C.c_void_p)]),
+    "qh_sampler_destroy": (None, [C.c_void_p]),
+    "qh_sampler_draw": (C.c_int, [C.c_void_p, C.POINTER(C.c_float)]),
+    "qh_set_valid_tokens": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    "qh_sample": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(C.c_uint32)]),
+    "qh_sample_logits": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
+                                   C.POINTER(C.c_uint32)]),
     "qh_device_name": (C.c_int, [C.c_int, C.c_char_p, C.c_size_t]),
     "qh_destroy": (None, [C.c_void_p]),
     "qh_last_error": (C.c_char_p, [C.c_void_p]),
@@ -141,6 +148,38 @@ def devices():
             raise EngineError(lib().qh_last_error(None).decode())
         out.append(buf.value.decode())
     return out
+
+
+class Sampler:
+    """== sampling::Sampler (src/sampling.rs:3-65): seeded StdRng stream
+    (host), top-k / temperature / top-p selection on the device."""
+
+    def __init__(self, seed, temperature, top_k, top_p):
+        h = C.c_void_p()
+        if lib().qh_sampler_create(seed, temperature, top_k, top_p, C.byref(h)) != 0:
+            raise EngineError(lib().qh_last_error(None).decode())
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().qh_sampler_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def draw(self):
+        """The stream's next rng.gen::<f32>()."""
+        u = C.c_float()
+        lib().qh_sampler_draw(self.h, C.byref(u))
+        return u.value
+
+    def sample(self, dev, logits, valid=None):
+        """Sampler::sample on caller logits (uploaded), optional valid mask."""
+        lg = _f32(logits)
+        v = None if valid is None else np.ascontiguousarray(valid, np.uint8)
+        out = C.c_uint32()
+        dev._check(lib().qh_sample_logits(dev.h, self.h, _ptr(lg), _ptr(v), lg.size, C.byref(out)))
+        return out.value
 
 
 class Device:
@@ -253,6 +292,17 @@ class Model:
         self.dev._check(lib().qh_forward(self.dev.h, token, _ptr(lg), C.byref(am)))
         self.last_argmax = am.value
         return lg
+
+    def sample(self, sampler):
+        """Sampler::sample on the logits of the last step, on the device."""
+        out = C.c_uint32()
+        self.dev._check(lib().qh_sample(self.dev.h, sampler.h, C.byref(out)))
+        return out.value
+
+    def set_valid_tokens(self, valid):
+        """Padding-vocab mask (src/main.rs:262-266); None clears it."""
+        v = None if valid is None else np.ascontiguousarray(valid, np.uint8)
+        self.dev._check(lib().qh_set_valid_tokens(self.dev.h, _ptr(v), 0 if v is None else v.size))
 
     def generate(self, prompt, n_new, want_logits=False):
         """Sequential prefill of `prompt` then `n_new` greedy tokens on device."""

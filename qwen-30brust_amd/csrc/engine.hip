@@ -211,6 +211,11 @@ struct qh_ctx {
     DevBuf sa, sb, sc, sd;
     HostPinned pin;
 
+    // sampler: the padding-vocab mask of the loaded model, host-logits upload
+    // buffers and the result words
+    DevBuf valid, samp_logits, samp_valid, samp_out;
+    size_t valid_n = 0;
+
     ~qh_ctx() { drop_model(); if (s) (void)hipStreamDestroy(s); }
 
     void drop_model() {
@@ -229,6 +234,8 @@ struct qh_ctx {
         persist_ok = persist = false;
         kv.release();
         rope_buf.release();
+        valid.release();
+        valid_n = 0;
         loaded = false;
         pos = 0;
     }
@@ -883,6 +890,99 @@ double now_ms() {
 
 }  // namespace
 
+namespace {
+
+// ============================================================ sampler RNG ==
+// rand 0.8.8's StdRng (= rand_chacha 0.3.1 ChaCha12Rng) as src/sampling.rs:20
+// seeds it with `StdRng::seed_from_u64` (rand_core 0.6.4): the 32-byte key is
+// filled with PCG32 outputs (state advanced by the 64-bit LCG, then XSH-RR),
+// the keystream is ChaCha with 12 rounds, 64-bit block counter from 0 and
+// stream 0, read one 32-bit word at a time; `gen::<f32>()` is the word's top
+// 24 bits times 2^-24.
+struct ChaCha12Stream {
+    uint32_t key[8];
+    uint64_t word = 0;  // index of the next keystream word
+
+    explicit ChaCha12Stream(uint64_t seed) {
+        uint64_t st = seed;
+        for (uint32_t& k : key) {
+            st = st * 6364136223846793005ull + 11634580027462260723ull;
+            const uint32_t xs = (uint32_t)(((st >> 18) ^ st) >> 27), rot = (uint32_t)(st >> 59);
+            k = (xs >> rot) | (xs << ((32 - rot) & 31));
+        }
+    }
+    static uint32_t rotl(uint32_t v, int n) { return (v << n) | (v >> (32 - n)); }
+    static void quarter(uint32_t& a, uint32_t& b, uint32_t& c, uint32_t& d) {
+        a += b, d = rotl(d ^ a, 16);
+        c += d, b = rotl(b ^ c, 12);
+        a += b, d = rotl(d ^ a, 8);
+        c += d, b = rotl(b ^ c, 7);
+    }
+    uint32_t at(uint64_t i) const {
+        const uint64_t blk = i / 16;
+        const uint32_t in[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u, key[0], key[1], key[2],
+                                 key[3],      key[4],      key[5],      key[6],      key[7], (uint32_t)blk,
+                                 (uint32_t)(blk >> 32), 0u, 0u};
+        uint32_t x[16];
+        std::memcpy(x, in, sizeof x);
+        for (int r = 0; r < 6; r++) {  // 12 rounds
+            quarter(x[0], x[4], x[8], x[12]);
+            quarter(x[1], x[5], x[9], x[13]);
+            quarter(x[2], x[6], x[10], x[14]);
+            quarter(x[3], x[7], x[11], x[15]);
+            quarter(x[0], x[5], x[10], x[15]);
+            quarter(x[1], x[6], x[11], x[12]);
+            quarter(x[2], x[7], x[8], x[13]);
+            quarter(x[3], x[4], x[9], x[14]);
+        }
+        return x[i % 16] + in[i % 16];
+    }
+    float peek_f32() const { return (float)(at(word) >> 8) * (1.0f / 16777216.0f); }
+};
+
+}  // namespace
+
+struct qh_sampler {
+    ChaCha12Stream rng;
+    float temperature, top_p;
+    size_t top_k;
+};
+
+namespace {
+
+// Sampler::sample (src/sampling.rs:26-63) on device logits; the stream
+// advances only when a draw was used (temperature > 0 and success).
+uint32_t run_sample(qh_ctx* c, qh_sampler* sp, const float* dlogits, const uint8_t* dvalid, size_t n) {
+    if (n == 0) throw Error("invalid logits");
+    if (n > (1u << 20)) throw Error("the device sampler takes at most 1048576 logits");
+    c->samp_out.reserve(16);
+    c->pin.reserve(16);
+    SampleArgs a{};
+    a.logits = dlogits;
+    a.valid = dvalid;
+    a.n = (uint32_t)n;
+    a.top_k = (uint32_t)std::min<size_t>(sp->top_k, 0xffffffffu);
+    a.temperature = sp->temperature;
+    a.top_p = sp->top_p;
+    a.draw = sp->rng.peek_f32();
+    a.out = c->samp_out.as<uint32_t>();
+    HIP_OK(hipSetDevice(c->device));
+    launch_sample(a, c->s);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipMemcpyAsync(c->pin.p, a.out, 16, hipMemcpyDeviceToHost, c->s));
+    HIP_OK(hipStreamSynchronize(c->s));
+    const uint32_t* r = static_cast<const uint32_t*>(c->pin.p);
+    if (r[1] == kSampleBadLogits) throw Error("invalid logits");
+    if (r[1] == kSampleSupport)
+        throw Error("sampling support of " + std::to_string(r[3]) + " tokens exceeds the device sampler's " +
+                    std::to_string(kSampleMax) + "; set top_k <= " + std::to_string(kSampleMax));
+    if (r[1] != 0) throw Error("device sampler failed");
+    if (sp->temperature != 0.f) sp->rng.word++;
+    return r[0];
+}
+
+}  // namespace
+
 // ===================================================================== C ABI ==
 extern "C" {
 
@@ -949,6 +1049,64 @@ int qh_inspect(const char* path, size_t context, qh_inspect_t* out) {
         g_create_err = e.what();
         return 1;
     }
+}
+
+int qh_sampler_create(uint64_t seed, float temperature, size_t top_k, float top_p, qh_sampler** out) {
+    if (!(std::isfinite(temperature) && temperature >= 0.f && std::isfinite(top_p) && top_p > 0.f &&
+          top_p <= 1.f)) {
+        g_create_err = "invalid sampling parameters";
+        return 1;
+    }
+    *out = new qh_sampler{ChaCha12Stream(seed), temperature, top_p, top_k};
+    return 0;
+}
+
+void qh_sampler_destroy(qh_sampler* sp) { delete sp; }
+
+int qh_sampler_draw(qh_sampler* sp, float* out) {
+    *out = sp->rng.peek_f32();
+    sp->rng.word++;
+    return 0;
+}
+
+int qh_set_valid_tokens(qh_ctx* c, const uint8_t* valid, size_t n) {
+    return guarded(c, [&] {
+        need_model(c);
+        if (!valid) {
+            c->valid.release();
+            c->valid_n = 0;
+            return;
+        }
+        if (n != c->cfg.vocab) throw Error("valid-token mask length differs from the vocabulary");
+        HIP_OK(hipSetDevice(c->device));
+        c->valid.reserve(n);
+        HIP_OK(hipMemcpyAsync(c->valid.p, valid, n, hipMemcpyHostToDevice, c->s));
+        HIP_OK(hipStreamSynchronize(c->s));
+        c->valid_n = n;
+    });
+}
+
+int qh_sample(qh_ctx* c, qh_sampler* sp, uint32_t* out) {
+    return guarded(c, [&] {
+        need_model(c);
+        if (c->pos == 0) throw Error("no logits: run a token step first");
+        *out = run_sample(c, sp, c->acts.logits, c->valid_n ? c->valid.as<uint8_t>() : nullptr, c->cfg.vocab);
+    });
+}
+
+int qh_sample_logits(qh_ctx* c, qh_sampler* sp, const float* logits, const uint8_t* valid, size_t n,
+                     uint32_t* out) {
+    return guarded(c, [&] {
+        if (n == 0) throw Error("invalid logits");
+        HIP_OK(hipSetDevice(c->device));
+        c->samp_logits.reserve(n * 4);
+        HIP_OK(hipMemcpyAsync(c->samp_logits.p, logits, n * 4, hipMemcpyHostToDevice, c->s));
+        if (valid) {
+            c->samp_valid.reserve(n);
+            HIP_OK(hipMemcpyAsync(c->samp_valid.p, valid, n, hipMemcpyHostToDevice, c->s));
+        }
+        *out = run_sample(c, sp, c->samp_logits.as<float>(), valid ? c->samp_valid.as<uint8_t>() : nullptr, n);
+    });
 }
 
 int qh_device_count(int* out) {

@@ -114,6 +114,23 @@ struct DecodeArgs {
     uint32_t l0, l1, vocab;
 };
 
+// Device sampler (sample.hip): src/sampling.rs:26-63 over n logits in HBM.
+constexpr uint32_t kSampleMax = 4096;  // largest candidate list it sorts
+enum : uint32_t {
+    kSampleBadLogits = 1u,  // empty or non-finite logits ("invalid logits")
+    kSampleSupport = 2u,    // more than kSampleMax ids with nonzero probability
+    kSampleInternal = 3u,   // the candidate selection did not yield the expected count
+};
+struct SampleArgs {
+    const float* logits;   // [n]
+    const uint8_t* valid;  // [n] 0 = masked to f32::MIN, or null
+    uint32_t n, top_k;     // top_k 0 = no truncation
+    float temperature, top_p;
+    float draw;            // rand's gen::<f32>() for this call (unused at temperature 0)
+    uint32_t* out;         // [4] id, status, kept count, candidate count
+};
+void launch_sample(const SampleArgs& a, hipStream_t s);
+
 // Expert work list of the batched-prefill grouped GEMMs (prefill.hip): tile
 // y covers rows [tm, tm + 128) of expert te; the rows of expert e are
 // [goff[e], goff[e+1]) of the assignments sorted by expert.

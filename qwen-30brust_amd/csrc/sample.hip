@@ -1,0 +1,280 @@
+// Device sampler: src/sampling.rs:26-63 (greedy, top-k, temperature, top-p
+// and the seeded draw) over the logits in HBM, with the padding-vocab mask of
+// src/main.rs:262-266 applied on the fly.  One workgroup of 1024 threads:
+//
+//   1. one pass over the masked logits: finiteness ("invalid logits") and the
+//      first id under the sort of sampling.rs:31 (descending total order,
+//      lowest index on ties); temperature 0 returns it (sampling.rs:32-35);
+//   2. the candidate count P: K = top_k (or every id when top_k is 0 or
+//      above the vocabulary) when K <= kSampleMax; otherwise the ids whose
+//      probability exp((l - max) / T) is nonzero (the rest of the sorted list
+//      adds exact zeros to every sum below), at most kSampleMax;
+//   3. the composite key of rank P - 1 by radix selection (three digit passes
+//      over the 32-bit total-order key, two over the index when the rank
+//      falls inside a run of equal logits), the P candidates collected into
+//      LDS and sorted there (bitonic, descending);
+//   4. the probabilities in parallel, then one lane runs the sequential f32
+//      folds of sampling.rs:44-62 (total, cumulative top-p cut, the draw
+//      scaled by the kept mass, the walk) in the reference's order.
+// The draw itself (rand's gen::<f32>()) comes from the host's ChaCha12
+// stream and is passed in.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+
+#include "kernels.hpp"
+#include "qh_device.hpp"
+
+namespace qh {
+
+namespace {
+
+constexpr uint32_t kST = 1024;         // threads of the sampling workgroup
+constexpr uint32_t kSW = kST / 64;     // its waves
+constexpr uint32_t kBins = 2048;       // widest digit: 11 bits
+
+struct SampleLds {
+    unsigned long long cand[kSampleMax];  // composite keys of the candidates
+    float p[kSampleMax];                  // their probabilities, in sorted order
+    uint32_t hist[kBins];
+    uint32_t wsum[kSW];
+    unsigned long long top;
+    uint32_t ncand, digit, rank, count, bad, flag;
+};
+
+// Unsigned key with the order of f32::total_cmp.
+__device__ __forceinline__ uint32_t ukey(float v) { return (uint32_t)total_key(v) ^ 0x80000000u; }
+// Composite key: larger = earlier in the sampler's sort (key, then lower index).
+__device__ __forceinline__ unsigned long long ckey(float v, uint32_t i) {
+    return ((unsigned long long)ukey(v) << 32) | (uint32_t)~i;
+}
+__device__ __forceinline__ uint32_t ck_index(unsigned long long k) { return ~(uint32_t)k; }
+
+__device__ __forceinline__ float masked(const float* lg, const uint8_t* valid, uint32_t i) {
+    return (valid && !valid[i]) ? -FLT_MAX : lg[i];  // f32::MIN (main.rs:262-266)
+}
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, uint32_t lane) {
+#pragma unroll
+    for (uint32_t o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(v, o, 64);
+        if (lane >= o) v += t;
+    }
+    return v;
+}
+
+// The bin holding rank `rr` when bins [0, nb) are walked from the top bin
+// down (desc) or from bin 0 up: S.digit, and S.rank = rr minus the counts
+// walked before it.  rr must be below the histogram's total.
+__device__ void find_bin(SampleLds& S, uint32_t nb, uint32_t rr, bool desc) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint32_t p0 = 2 * tid, p1 = 2 * tid + 1;
+    const uint32_t b0 = desc ? nb - 1 - p0 : p0, b1 = desc ? nb - 1 - p1 : p1;
+    const uint32_t c0 = p0 < nb ? S.hist[b0] : 0u, c1 = p1 < nb ? S.hist[b1] : 0u;
+    const uint32_t s = c0 + c1, incl = wave_incl_scan(s, lane);
+    if (lane == 63) S.wsum[wv] = incl;
+    __syncthreads();
+    if (wv == 0) {
+        const uint32_t w = lane < kSW ? S.wsum[lane] : 0u;
+        const uint32_t wi = wave_incl_scan(w, lane);
+        if (lane < kSW) S.wsum[lane] = wi - w;
+    }
+    __syncthreads();
+    const uint32_t excl = S.wsum[wv] + incl - s;
+    if (rr >= excl && rr < excl + s) {
+        if (rr < excl + c0) {
+            S.digit = b0;
+            S.rank = rr - excl;
+        } else {
+            S.digit = b1;
+            S.rank = rr - excl - c0;
+        }
+    }
+    __syncthreads();
+}
+
+// Composite key of the element of rank r (0 = first in the sampler's sort).
+__device__ unsigned long long select_rank(SampleLds& S, const float* lg, const uint8_t* valid, uint32_t n,
+                                          uint32_t r) {
+    const uint32_t tid = threadIdx.x;
+    uint32_t prefix = 0, pmask = 0, rr = r, neq = 0;
+    // key digits, most significant first: bits 31..21, 20..10, 9..0
+    const uint32_t shifts[3] = {21, 10, 0}, widths[3] = {11, 11, 10};
+    for (int ps = 0; ps < 3; ps++) {
+        const uint32_t sh = shifts[ps], nb = 1u << widths[ps];
+        for (uint32_t b = tid; b < nb; b += kST) S.hist[b] = 0;
+        __syncthreads();
+        for (uint32_t i = tid; i < n; i += kST) {
+            const uint32_t u = ukey(masked(lg, valid, i));
+            if ((u & pmask) == prefix) atomicAdd(&S.hist[(u >> sh) & (nb - 1)], 1u);
+        }
+        __syncthreads();
+        find_bin(S, nb, rr, true);
+        neq = S.hist[S.digit];
+        prefix |= S.digit << sh;
+        pmask |= (nb - 1) << sh;
+        rr = S.rank;
+        __syncthreads();
+    }
+    // prefix is the key; rr ranks the run of equal keys by ascending index
+    if (rr + 1 == neq) return (unsigned long long)prefix << 32;  // the whole run
+    uint32_t iprefix = 0, imask = 0;
+    const uint32_t ishift[2] = {10, 0};
+    for (int ps = 0; ps < 2; ps++) {
+        const uint32_t sh = ishift[ps], nb = 1024;
+        for (uint32_t b = tid; b < nb; b += kST) S.hist[b] = 0;
+        __syncthreads();
+        for (uint32_t i = tid; i < n; i += kST)
+            if (ukey(masked(lg, valid, i)) == prefix && (i & imask) == iprefix)
+                atomicAdd(&S.hist[(i >> sh) & (nb - 1)], 1u);
+        __syncthreads();
+        find_bin(S, nb, rr, false);
+        iprefix |= S.digit << sh;
+        imask |= (nb - 1) << sh;
+        rr = S.rank;
+        __syncthreads();
+    }
+    return ((unsigned long long)prefix << 32) | (uint32_t)~iprefix;
+}
+
+__global__ __launch_bounds__(kST) void k_sample(SampleArgs a) {
+    __shared__ SampleLds S;
+    const uint32_t tid = threadIdx.x, n = a.n;
+    const float* lg = a.logits;
+    if (tid == 0) {
+        S.top = 0;
+        S.bad = 0;
+        S.ncand = 0;
+        S.count = 0;
+        S.flag = 0;
+    }
+    __syncthreads();
+    // 1. finiteness and the first id
+    unsigned long long best = 0;
+    bool bad = false;
+    for (uint32_t i = tid; i < n; i += kST) {
+        const float v = masked(lg, a.valid, i);
+        bad |= !finite_f(v);
+        const unsigned long long k = ckey(v, i);
+        best = k > best ? k : best;
+    }
+    if (bad) S.bad = 1;
+    atomicMax(&S.top, best);
+    __syncthreads();
+    if (S.bad || n == 0) {
+        if (tid == 0) a.out[1] = kSampleBadLogits;
+        return;
+    }
+    const uint32_t first = ck_index(S.top);
+    if (a.temperature == 0.f) {
+        if (tid == 0) {
+            a.out[0] = first;
+            a.out[1] = 0;
+            a.out[2] = 1;
+            a.out[3] = 1;
+        }
+        return;
+    }
+    const float T = a.temperature, mx = masked(lg, a.valid, first);
+    const uint32_t K = (a.top_k > 0 && a.top_k < n) ? a.top_k : n;
+    // 2. candidate count
+    uint32_t P = K;
+    if (K > kSampleMax) {
+        uint32_t cnt = 0;
+        for (uint32_t i = tid; i < n; i += kST) cnt += expf((masked(lg, a.valid, i) - mx) / T) > 0.f;
+        atomicAdd(&S.count, cnt);
+        __syncthreads();
+        P = S.count;
+        if (P > kSampleMax) {
+            if (tid == 0) {
+                a.out[1] = kSampleSupport;
+                a.out[3] = P;
+            }
+            return;
+        }
+    }
+    // 3. the P first ids, sorted
+    const unsigned long long theta = select_rank(S, lg, a.valid, n, P - 1);
+    for (uint32_t i = tid; i < n; i += kST) {
+        const unsigned long long k = ckey(masked(lg, a.valid, i), i);
+        if (k >= theta) {
+            const uint32_t slot = atomicAdd(&S.ncand, 1u);
+            if (slot < kSampleMax) S.cand[slot] = k;
+        }
+    }
+    uint32_t np = 1;
+    while (np < P) np <<= 1;
+    __syncthreads();
+    if (S.ncand != P) {  // the selection must yield exactly the P first ids
+        if (tid == 0) a.out[1] = kSampleInternal;
+        return;
+    }
+    for (uint32_t i = P + tid; i < np; i += kST) S.cand[i] = 0;  // below every finite key
+    __syncthreads();
+    for (uint32_t k = 2; k <= np; k <<= 1) {
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            for (uint32_t i = tid; i < np; i += kST) {
+                const uint32_t l = i ^ j;
+                if (l > i) {
+                    const unsigned long long x = S.cand[i], y = S.cand[l];
+                    const bool down = (i & k) == 0;  // descending runs first: overall descending
+                    if (down ? x < y : x > y) {
+                        S.cand[i] = y;
+                        S.cand[l] = x;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    // 4. probabilities (sampling.rs:43-46), then the sequential folds
+    for (uint32_t i = tid; i < P; i += kST) {
+#pragma clang fp contract(off)
+        S.p[i] = expf((masked(lg, a.valid, ck_index(S.cand[i])) - mx) / T);
+    }
+    __syncthreads();
+    if (tid == 0) {
+#pragma clang fp contract(off)
+        float total = -0.0f;
+        for (uint32_t i = 0; i < P; i++) total += S.p[i];
+        float cumulative = 0.f;
+        uint32_t m = K;
+        for (uint32_t i = 0; i < P; i++) {
+            cumulative += S.p[i] / total;
+            if (cumulative >= a.top_p) {
+                m = i + 1;
+                break;
+            }
+        }
+        const uint32_t mp = m < P ? m : P;
+        float kept = -0.0f;
+        for (uint32_t i = 0; i < mp; i++) kept += S.p[i];
+        float draw = a.draw * kept;
+        uint32_t pick = 0xffffffffu;
+        for (uint32_t i = 0; i < mp; i++) {
+            if (draw < S.p[i]) {
+                pick = ck_index(S.cand[i]);
+                break;
+            }
+            draw -= S.p[i];
+        }
+        if (pick == 0xffffffffu && m <= P) pick = ck_index(S.cand[m - 1]);  // ids.last()
+        if (pick == 0xffffffffu) S.flag = m;  // the last kept id lies past the candidates
+        a.out[0] = pick;
+        a.out[1] = 0;
+        a.out[2] = m;
+        a.out[3] = P;
+    }
+    __syncthreads();
+    if (S.flag) {  // rank m - 1 (= K - 1: every later probability is 0)
+        const unsigned long long k = select_rank(S, lg, a.valid, n, S.flag - 1);
+        if (tid == 0) a.out[0] = ck_index(k);
+    }
+}
+
+}  // namespace
+
+void launch_sample(const SampleArgs& a, hipStream_t s) { k_sample<<<1, kST, 0, s>>>(a); }
+
+}  // namespace qh

@@ -1,0 +1,107 @@
+"""The sampler of src/sampling.rs with rand 0.8.8's StdRng stream: the
+oracle's restatement pinned by published ChaCha keystreams, the reference's
+own sampler tests (tests/core.rs:28-42) and closed forms; the engine's host
+stream against it (no GPU needed)."""
+import importlib
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+
+engine = importlib.import_module("qwen-30brust_amd")
+
+
+def le_bytes(words):
+    return b"".join(int(w).to_bytes(4, "little") for w in words).hex()
+
+
+def test_chacha_core_against_published_keystreams():
+    # all-zero key and nonce, block 0: ChaCha20 (RFC 7539 A.1 test vector 1)
+    # and the reduced-round ChaCha12 / ChaCha8 keystreams published with it
+    assert le_bytes(oracle.chacha_block([0] * 8, 0, 0, 20)) == (
+        "76b8e0ada0f13d90405d6ae55386bd28bdd219b8a08ded1aa836efcc8b770dc7"
+        "da41597c5157488d7724e03fb8d84a376a43b8f41518a11cc387b669b2ee6586")
+    assert le_bytes(oracle.chacha_block([0] * 8, 0, 0, 12)) == (
+        "9bf49a6a0755f953811fce125f2683d50429c3bb49e074147e0089a52eae155f"
+        "0564f879d27ae3c02ce82834acfa8c793a629f2ca0de6919610be82f411326be")
+    assert le_bytes(oracle.chacha_block([0] * 8, 0, 0, 8)) == (
+        "3e00ef2f895f40d67f5bb8e81f09a5a12c840ec3ce9a7f3b181be188ef711a1e"
+        "984ce172b9216f419f445367456d5619314a42a3da86b001387bfdb80e0cfe42")
+
+
+def test_seed_expansion_is_pcg32_xsh_rr():
+    # rand_core 0.6.4 seed_from_u64: LCG step, then XSH-RR of the new state,
+    # restated here with Python integers for two seeds
+    def expand(seed):
+        st, out = seed, []
+        for _ in range(8):
+            st = (st * 6364136223846793005 + 11634580027462260723) % 2**64
+            xs = (((st >> 18) ^ st) >> 27) % 2**32
+            rot = st >> 59
+            out.append(((xs >> rot) | (xs << ((32 - rot) % 32))) % 2**32)
+        return out
+    for seed in (0, 42, 77, 2**64 - 1):
+        assert oracle.stdrng_key(seed) == expand(seed)
+
+
+def test_reference_sampler_tests():  # tests/core.rs:28-42
+    s = oracle.Sampler(42, 0.0, 0, 1.0)
+    assert s.sample([0.0, 4.0, 2.0]) == 1
+    with pytest.raises(oracle.OracleError, match="invalid logits"):
+        s.sample([float("nan")])
+    with pytest.raises(oracle.OracleError, match="invalid sampling parameters"):
+        oracle.Sampler(1, 1.0, 1, 0.0)
+    a, b = oracle.Sampler(77, 1.0, 0, 1.0), oracle.Sampler(77, 1.0, 0, 1.0)
+    for _ in range(40):
+        assert a.sample([1.0, 2.0, 3.0]) == b.sample([1.0, 2.0, 3.0])
+
+
+def test_sampler_walk_closed_form():
+    # logits [0, ln 3] at T = 1: sorted ids [1, 0] with probabilities [1, 1/3];
+    # the draw u * 4/3 picks id 1 iff it is below 1, i.e. u < 3/4
+    peek, s = oracle.Sampler(5, 1.0, 0, 1.0), oracle.Sampler(5, 1.0, 0, 1.0)
+    lg = np.array([0.0, math.log(3.0)], np.float32)
+    for _ in range(300):
+        u = peek.draw()
+        assert s.sample(lg) == (1 if u < 0.75 else 0)
+    # top_k = 1 and a tiny top_p both keep only the first id
+    for k, p in ((1, 1.0), (0, 1e-9)):
+        s = oracle.Sampler(9, 1.5, k, p)
+        assert all(s.sample([0.5, 3.0, 2.9, -1.0]) == 1 for _ in range(50))
+
+
+def test_sampler_frequencies():
+    # p(id) proportional to exp(l / T) over the kept ids
+    s = oracle.Sampler(123, 0.5, 0, 1.0)
+    lg = np.array([0.0, 0.2, 0.4, -0.3], np.float32)
+    n = 20000
+    counts = np.bincount([s.sample(lg) for _ in range(n)], minlength=4) / n
+    p = np.exp(lg / 0.5)
+    p /= p.sum()
+    assert np.max(np.abs(counts - p)) < 0.015
+    # top_p 0.5 keeps the ids whose cumulative mass reaches 0.5 in sorted order
+    s = oracle.Sampler(321, 0.5, 0, 0.5)
+    picked = {s.sample(lg) for _ in range(2000)}
+    order = np.argsort(-p, kind="stable")
+    keep = order[:int(np.searchsorted(np.cumsum(p[order]), 0.5) + 1)]
+    assert picked == set(keep.tolist())
+
+
+@pytest.mark.parametrize("seed", [0, 42, 77, 2**63 + 5])
+def test_engine_stream_matches_oracle(seed):
+    # the engine's host-side ChaCha12 stream (no device work) over 300 draws,
+    # crossing many 16-word blocks
+    a, b = engine.Sampler(seed, 1.0, 0, 1.0), oracle.Sampler(seed, 1.0, 0, 1.0)
+    got = [a.draw() for _ in range(300)]
+    want = [b.draw() for _ in range(300)]
+    assert got == want
+    assert all(0.0 <= u < 1.0 for u in got)
+
+
+def test_engine_sampler_parameter_check():
+    for t, p in ((-1.0, 0.5), (float("nan"), 0.5), (1.0, 0.0), (1.0, 1.5), (float("inf"), 1.0)):
+        with pytest.raises(engine.EngineError, match="invalid sampling parameters"):
+            engine.Sampler(1, t, 0, p)
+    engine.Sampler(1, 0.0, 0, 1.0)  # greedy is valid
