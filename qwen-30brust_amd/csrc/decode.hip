@@ -73,6 +73,7 @@ struct DecodeLds {
     float red[2 * kDW];
     float lg[256];            // router logits
     alignas(16) long long ck[128];  // composite top-k keys
+    float ra;                 // router workgroup: sum_j router[e][j] ffn_norm[j] x[j] of this layer
     float sv[8];
     uint32_t sid[8];
     float ex[8];
@@ -306,6 +307,32 @@ __device__ __forceinline__ float4 norm_in_lds(const Ctx& c, float* xs, float4 w,
     return xv;
 }
 
+// Router workgroups follow every possible attention workgroup: workgroup
+// kvheads * kDChunks + e folds router row e (e < experts) into phases A and C.
+__device__ __forceinline__ bool router_wg(const DecodeArgs& A, const Ctx& c, uint32_t& e) {
+    e = c.b - A.dm.kvheads * kDChunks;
+    return c.b >= A.dm.kvheads * kDChunks && e < c.E;
+}
+
+// norm_in_lds that also reduces sum_i rw[i] x[i] (raw x) in the same round.
+__device__ __forceinline__ float4 norm_in_lds_dot(const Ctx& c, float* xs, float4 w, float eps, float* red,
+                                                  float4 rw, float& rdot) {
+    float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (4 * c.tid < c.H) xv = reinterpret_cast<const float4*>(xs)[c.tid];
+    const float dt = fmaf(rw.w, xv.w, fmaf(rw.z, xv.z, fmaf(rw.y, xv.y, rw.x * xv.x)));
+    const float2 r = dsum2(sumsq4(xv), dt, red);
+    const float scale = 1.0f / sqrtf(r.x / (float)c.H + eps);
+    if (4 * c.tid < c.H) {
+        xs[4 * c.tid] = xv.x * (scale * w.x);
+        xs[4 * c.tid + 1] = xv.y * (scale * w.y);
+        xs[4 * c.tid + 2] = xv.z * (scale * w.z);
+        xs[4 * c.tid + 3] = xv.w * (scale * w.w);
+    }
+    __syncthreads();
+    rdot = r.y;
+    return xv;
+}
+
 // Tag of phase k (1..6) of layer l.
 __device__ __forceinline__ uint32_t ptag(const DecodeArgs& A, uint32_t l, uint32_t k) {
     return A.base + 6 * (l - A.l0) + k;
@@ -439,6 +466,15 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
     }
     float4 nw = make_float4(0.f, 0.f, 0.f, 0.f);
     if (4 * c.tid < c.H) nw = gld<float4>(L.attn_norm + 4 * c.tid);
+    // router workgroup e: router[e] * ffn_norm, for its share of logit e
+    uint32_t re;
+    const bool rt = router_wg(A, c, re);
+    float4 rw = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (rt && 4 * c.tid < c.H) {
+        const float4 wr = gld<float4>(L.router.w + (size_t)re * L.router.drb + 16 * c.tid);
+        const float4 fw = gld<float4>(L.ffn_norm + 4 * c.tid);
+        rw = make_float4(wr.x * fw.x, wr.y * fw.y, wr.z * fw.z, wr.w * fw.w);
+    }
     attn_prefetch(A, L, c, P);
     float* xs = S.big;
     QH_MARK(0, 0);
@@ -450,7 +486,9 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
         return false;  // x'' of the previous layer (phase F)
     }
     QH_MARK(0, 1);
-    const float4 xv = norm_in_lds(c, xs, nw, A.dm.eps, S.red);
+    float rdot;
+    const float4 xv = norm_in_lds_dot(c, xs, nw, A.dm.eps, S.red, rw, rdot);
+    if (rt && c.tid == 0) S.ra = rdot;
     // this workgroup's residual rows, kept in LDS through the layer
     if (4 * c.tid < c.H) {
         const float e4[4] = {xv.x, xv.y, xv.z, xv.w};
@@ -745,6 +783,15 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
         if (c.lane < ocpr) w0 = Fmt<KO>::load(orow, L.o.geo, c.lane);
         if (c.lane + 64 < ocpr) w1 = Fmt<KO>::load(orow, L.o.geo, c.lane + 64);
     }
+    // router workgroup e: row e of the fold, elements 8 tid .. 8 tid + 7
+    uint32_t re;
+    const bool rt = router_wg(A, c, re);
+    float4 f0 = make_float4(0.f, 0.f, 0.f, 0.f), f1 = f0;
+    if (rt && 8 * c.tid < c.qd) {
+        const float* fr = L.rfold + (size_t)re * c.qd + 8 * c.tid;
+        f0 = gld<float4>(fr);
+        f1 = gld<float4>(fr + 4);
+    }
     QH_MARK(2, 0);
     float* xs = S.big;
     if (!gather_s(A, S, A.tatt, c.qd, ptag(A, l, 2), xs, c.tid, c.qd / 128, 127, 128))
@@ -764,53 +811,49 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
         acc = wave_sum(acc);
         if (c.lane == 0) S.xo[c.wv] += acc;  // residual (model.rs:246-248)
     }
+    if (rt) {  // workgroup-uniform
+        float fd = 0.f;
+        if (8 * c.tid < c.qd) {
+            const float4 a0 = reinterpret_cast<const float4*>(xs)[2 * c.tid];
+            const float4 a1 = reinterpret_cast<const float4*>(xs)[2 * c.tid + 1];
+            fd = fmaf(f0.w, a0.w, fmaf(f0.z, a0.z, fmaf(f0.y, a0.y, f0.x * a0.x)));
+            fd = fmaf(f1.w, a1.w, fmaf(f1.z, a1.z, fmaf(f1.y, a1.y, fmaf(f1.x, a1.x, fd))));
+        }
+        fd = wave_sum(fd);
+        if (c.lane == 0) S.red[c.wv] = fd;
+    }
     QH_MARK(2, 2);
     __syncthreads();
     if (c.tid < c.nr) put(A.tx1 + c.r0 + c.tid, S.xo[c.tid], ptag(A, l, 3));  // one store instruction
+    if (rt && c.tid == 64) {
+        // unscaled router logit e of x' (model.rs:249-256 with the RMS scale left out)
+        float u = S.ra;
+#pragma unroll
+        for (uint32_t w = 0; w < kDW; w++) u += S.red[w];
+        put(A.tx1 + c.H + re, u, ptag(A, l, 3));
+    }
     return true;
 }
 
-// ================================================================ D: router ==
-// Every workgroup gathers x' into LDS and computes the ffn RMSNorm scale
-// s = 1/sqrt(mean(x'^2) + eps) (ops.rs:3-15); workgroup e < E also computes
-// logit e = s * sum_i Wr[e][i] (x'[i] w[i]) (model.rs:249-256) and passes it on.
-// Returns s (negative when the step was aborted).
-__device__ __forceinline__ float phase_router(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
-                                              uint32_t l) {
-    const Ctx c = fresh(c0);
-    const bool rt = c.b < c.E;
-    float4 wr = make_float4(0.f, 0.f, 0.f, 0.f), fw = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (rt && 4 * c.tid < c.H) {
-        wr = gld<float4>(L.router.w + (size_t)c.b * L.router.drb + 16 * c.tid);
-        fw = gld<float4>(L.ffn_norm + 4 * c.tid);
-    }
-    QH_MARK(3, 0);
-    float* xs = S.big;
-    if (!gather_s(A, S, A.tx1, c.H, ptag(A, l, 3), xs, c.tid, c.nwg, 0, c.rpw)) return -1.f;  // x' (phase C)
-    QH_MARK(3, 1);
-    float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (4 * c.tid < c.H) xv = reinterpret_cast<const float4*>(xs)[c.tid];
-    const float dt =
-        fmaf(wr.w, xv.w * fw.w, fmaf(wr.z, xv.z * fw.z, fmaf(wr.y, xv.y * fw.y, wr.x * (xv.x * fw.x))));
-    const float2 r = dsum2(sumsq4(xv), dt, S.red);
-    const float s = 1.0f / sqrtf(r.x / (float)c.H + A.dm.eps);
-    if (rt && c.tid == 0) put(A.tlog + c.b, s * r.y, ptag(A, l, 4));
-    QH_MARK(3, 2);
-    return s;
-}
-
-// ============================================== E + F: routed expert FFN ==
-// x' (raw) is in LDS from phase D, s its RMS scale.
+// ============================================ D-F: routing, routed expert FFN ==
+// Gathers x' and the unscaled router logits u (phase C); the ffn RMSNorm
+// scale s = 1/sqrt(mean(x'^2) + eps) (ops.rs:3-15) gives logit e = s u_e.
 template <uint32_t KG, uint32_t KD>
 __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
-                                          uint32_t l, float s, bool last) {
+                                          uint32_t l, bool last) {
     const Ctx c = fresh(c0);
     const Acts& a = A.a;
     const uint32_t E = c.E, top = c.top, ff = c.ff, H = c.H, cpr = H / 32;
     float4 fn = make_float4(0.f, 0.f, 0.f, 0.f);
     if (4 * c.tid < H) fn = gld<float4>(L.ffn_norm + 4 * c.tid);
     QH_MARK(4, 0);
-    if (!gather(A, S, A.tlog, E, ptag(A, l, 4), S.lg, c.tid)) return false;  // router logits (phase D)
+    float* xs = S.big;
+    if (!gather_s(A, S, A.tx1, H + E, ptag(A, l, 3), xs, c.tid, c.nwg, 0, c.rpw))
+        return false;  // x' and u (phase C)
+    float4 x1 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (4 * c.tid < H) x1 = reinterpret_cast<const float4*>(xs)[c.tid];
+    const float s = 1.0f / sqrtf(dsum(sumsq4(x1), S.red) / (float)H + A.dm.eps);
+    if (c.tid < E) S.lg[c.tid] = s * xs[H + c.tid];  // router logits (model.rs:249-256)
     QH_MARK(4, 1);
     // top-k by rank under the total order, lower index on ties (ops.rs:45-56;
     // bit-exact on these logits): j outranks i iff ck[j] > ck[i], with the
@@ -871,13 +914,11 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         }
     }
     // xn = x' * (s * ffn_norm), in place (each thread rewrites its own float4)
-    float* xs = S.big;
     if (4 * c.tid < H) {
-        const float4 xv = reinterpret_cast<const float4*>(xs)[c.tid];
-        xs[4 * c.tid] = xv.x * (s * fn.x);
-        xs[4 * c.tid + 1] = xv.y * (s * fn.y);
-        xs[4 * c.tid + 2] = xv.z * (s * fn.z);
-        xs[4 * c.tid + 3] = xv.w * (s * fn.w);
+        xs[4 * c.tid] = x1.x * (s * fn.x);
+        xs[4 * c.tid + 1] = x1.y * (s * fn.y);
+        xs[4 * c.tid + 2] = x1.z * (s * fn.z);
+        xs[4 * c.tid + 3] = x1.w * (s * fn.w);
     }
     __syncthreads();
     if (c.b == 0) {
@@ -1117,9 +1158,7 @@ __global__ __launch_bounds__(kDT) void k_decode(DecodeArgs A) {
         QH_DISPATCH_KM(L.v.kind, KV, ok = phase_qkv<Q4_K, KV>(A, S, L, c, l, P));
         if (!ok || !phase_attn(A, S, L, c, l, P)) return;
         if (!phase_oproj<Q4_K>(A, S, L, c, l)) return;
-        const float s = phase_router(A, S, L, c, l);
-        if (s < 0.f) return;
-        QH_DISPATCH_KM(L.down.kind, KD, ok = phase_moe<Q4_K, KD>(A, S, L, c, l, s, l + 1 == A.l1));
+        QH_DISPATCH_KM(L.down.kind, KD, ok = phase_moe<Q4_K, KD>(A, S, L, c, l, l + 1 == A.l1));
         if (!ok) return;
     }
     if (A.vocab) QH_DISPATCH_KM(A.out.kind, KV, phase_vocab<KV>(A, S, c));

@@ -27,6 +27,7 @@ namespace qh {
 // Kernels (kernels.hip).
 __global__ void k_repack(const uint8_t*, uint8_t*, uint32_t, uint32_t, size_t, size_t, size_t);
 __global__ void k_dequant(DevMat, size_t, size_t, float*);
+__global__ void k_router_fold(DevMat, const float*, const float*, uint32_t, uint32_t, uint32_t, float*);
 template <int R> __global__ void k_matvec(DevMat, const float*, float*, int);
 __global__ void k_route(const float*, uint32_t, uint32_t, uint32_t*, float*, uint32_t*);
 __global__ void k_argmax(const float*, uint32_t, int32_t*, uint32_t*, uint32_t*, uint32_t*, uint32_t*);
@@ -186,6 +187,7 @@ struct qh_ctx {
     uint32_t nwg = 0;         // workgroups of k_decode (one per CU)
     uint32_t flag_base = 0;   // tag of the last phase launched
     DevBuf layers_dev, sync_buf;  // sync_buf: abort flag and tagged exchange words
+    DevBuf rfold;                 // router folds of every layer ([layers][experts][heads*d])
     size_t sync_bytes = 0;
     DecodeArgs dargs{};
 
@@ -231,6 +233,7 @@ struct qh_ctx {
         pf.cap = 0;
         layers_dev.release();
         sync_buf.release();
+        rfold.release();
         persist_ok = persist = false;
         kv.release();
         rope_buf.release();
@@ -500,7 +503,9 @@ bool persist_supported(const qh_ctx* c, uint32_t nwg) {
     const ModelDims& d = c->dm;
     const uint32_t G = d.heads / d.kvheads, NWV = nwg * 8;
     auto km = [](uint32_t k) { return k == Q4_K || k == Q6_K; };
-    if (!(d.head_dim == 128 && G >= 1 && G <= 8 && d.heads * 128 <= 4096 && d.kvheads * 32 <= nwg)) return false;
+    // attention workgroups are < kvheads * 32; the router workgroups follow them
+    if (!(d.head_dim == 128 && G >= 1 && G <= 8 && d.heads * 128 <= 4096 && d.kvheads * 32 + d.experts <= nwg))
+        return false;
     // every workgroup owns rows of x: the tagged exchange relies on it
     const uint32_t rpw = (d.hidden + nwg - 1) / nwg;
     if (!(d.hidden % 256 == 0 && d.hidden <= 2048 && rpw <= 8 && (nwg - 1) * rpw < d.hidden)) return false;
@@ -532,6 +537,24 @@ void setup_persist(qh_ctx* c) {
     if (!c->persist_ok) return;
     c->nwg = nwg;
     const ModelDims& d = c->dm;
+    {
+        // router folds: F = (router * ffn_norm) Wo per layer, from the
+        // dequantised attn_output (one f32 copy of it at a time)
+        const uint32_t H = d.hidden, qd = d.heads * 128, E = d.experts;
+        const size_t per = (size_t)E * qd;
+        c->rfold.alloc(c->layers.size() * per * 4);
+        DevBuf wo;
+        wo.alloc((size_t)H * qd * 4);
+        for (size_t l = 0; l < c->layers.size(); l++) {
+            LayerW& L = c->layers[l];
+            hipLaunchKernelGGL(k_dequant, dim3(1024), dim3(kBlock), 0, c->s, L.o, (size_t)0, (size_t)H, wo.as<float>());
+            hipLaunchKernelGGL(k_router_fold, dim3((qd + kBlock - 1) / kBlock, (E + 7) / 8), dim3(kBlock), 0, c->s,
+                               L.router, L.ffn_norm, wo.as<const float>(), H, qd, E, c->rfold.as<float>() + l * per);
+            HIP_OK(hipGetLastError());
+            L.rfold = c->rfold.as<const float>() + l * per;
+        }
+        HIP_OK(hipStreamSynchronize(c->s));
+    }
     c->layers_dev.alloc(c->layers.size() * sizeof(LayerW));
     HIP_OK(hipMemcpy(c->layers_dev.p, c->layers.data(), c->layers.size() * sizeof(LayerW), hipMemcpyHostToDevice));
     DecodeArgs& A = c->dargs;
@@ -549,12 +572,11 @@ void setup_persist(qh_ctx* c) {
         uint64_t words;
         uint64_t** dst;
     } regions[] = {
-        {d.hidden, &A.tx1},
+        {(uint64_t)d.hidden + d.experts, &A.tx1},  // x' rows, then the unscaled router logits
         {d.hidden, &A.tx2},
         {qd + 2 * kvd, &A.tqkv},
         {qd, &A.tatt},
         {(uint64_t)d.heads * c->max_chunks * kPartWords, &A.tpart},
-        {d.experts, &A.tlog},
         {(uint64_t)d.top * d.ff, &A.th},
         {2ull * nwg, &A.tfin},
     };

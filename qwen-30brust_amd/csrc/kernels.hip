@@ -34,6 +34,31 @@ __global__ __launch_bounds__(kBlock) void k_dequant(DevMat m, size_t row0, size_
     }
 }
 
+// Router fold of one layer: F[e][k] = sum_j (router[e][j] ffn_norm[j]) wo[j][k]
+// for 8 experts e0..e0+7 per workgroup and one column k per thread, f64
+// accumulation of exact f64 products, rounded once to f32.  wo is the
+// dequantised attn_output ([rows][cols] f32).
+__global__ __launch_bounds__(kBlock) void k_router_fold(DevMat router, const float* __restrict__ norm,
+                                                        const float* __restrict__ wo, uint32_t rows, uint32_t cols,
+                                                        uint32_t experts, float* __restrict__ out) {
+    const uint32_t k = blockIdx.x * kBlock + threadIdx.x, e0 = blockIdx.y * 8;
+    if (k >= cols) return;
+    double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (uint32_t j = 0; j < rows; j++) {
+        const double w = (double)wo[(size_t)j * cols + k], g = (double)norm[j];
+#pragma unroll
+        for (uint32_t i = 0; i < 8; i++) {
+            if (e0 + i < experts) {
+                const float r = reinterpret_cast<const float*>(router.w + (size_t)(e0 + i) * router.drb)[j];
+                acc[i] = fma((double)r * g, w, acc[i]);
+            }
+        }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < 8; i++)
+        if (e0 + i < experts) out[(size_t)(e0 + i) * cols + k] = (float)acc[i];
+}
+
 // y = W x for one matrix (Backend::matvec, src/backend.rs:29-52).  x is
 // staged in LDS (x_global = false) or read from a zero-padded global copy.
 template <int R>

@@ -46,6 +46,10 @@ struct LayerW {
     const float* ffn_norm;
     float* kcache;  // [kvheads][ctx][d]
     float* vcache;
+    // persistent step only: F[e][k] = sum_j router[e][j] ffn_norm[j] attn_output[j][k]
+    // ([experts][heads*d] f32), so that router logit e of x' = x + Wo a is
+    // s (sum_j router[e][j] ffn_norm[j] x[j] + F[e] . a)
+    const float* rfold;
 };
 
 struct ModelDims {
@@ -102,12 +106,11 @@ struct DecodeArgs {
     ModelDims dm;
     uint32_t max_chunks;   // attention chunks per KV head (<= 32)
     uint32_t* abort_flag;  // set when a wait times out; every wait then returns
-    uint64_t* tx1;         // [hidden]  x after attention (x')
+    uint64_t* tx1;         // [hidden + experts] x after attention (x'), then the unscaled router logits
     uint64_t* tx2;         // [hidden]  x after the MoE block (x'')
     uint64_t* tqkv;        // [heads*d + 2*kvheads*d] q | k | v projections
     uint64_t* tatt;        // [heads*d] attention output
     uint64_t* tpart;       // [heads][max_chunks][d + 2] attention chunk partials (o, m, l)
-    uint64_t* tlog;        // [experts] router logits
     uint64_t* th;          // [top][ff] SwiGLU outputs
     uint64_t* tfin;        // [gridDim.x][2] vocab argmax partials (key, index)
     uint32_t base;         // tag before this launch's first phase
