@@ -49,7 +49,7 @@ def build_engine():
     with ThreadPoolExecutor(max_workers=len(ENGINE_SOURCES)) as ex:
         objs = list(ex.map(compile_one, ENGINE_SOURCES))
     tmp = ENGINE_SO + ".tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, "-lhipblaslt"])
     os.replace(tmp, ENGINE_SO)
     build_cli()
     return ENGINE_SO

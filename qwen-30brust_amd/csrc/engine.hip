@@ -1,6 +1,7 @@
 // Host side of the decode engine: model upload, the captured token-step
 // graph, and the C ABI declared in include/qwen_hip.h.
 #include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
 
 #include <algorithm>
 #include <array>
@@ -46,9 +47,9 @@ __global__ void k_finish(Acts, ModelDims, uint32_t);
 __global__ void k_embed(DevMat, Acts, ModelDims);
 __global__ void k_decode(DecodeArgs);
 // Batched prefill (prefill.hip).
-template <uint32_t K> __global__ void k_gemm(const _Float16*, uint32_t, uint32_t, DevMat, float*, uint32_t, uint32_t);
 template <uint32_t K> __global__ void k_gemm_gateup(const _Float16*, uint32_t, ExpertTiles, DevMat, DevMat, _Float16*);
 template <uint32_t K> __global__ void k_gemm_down(const _Float16*, ExpertTiles, DevMat, float*);
+template <uint32_t K> __global__ void k_dequant16(DevMat, uint32_t, uint32_t, _Float16*);
 __global__ void k_pf_embed(DevMat, const uint32_t*, uint32_t, uint32_t, float*, DevState*);
 __global__ void k_pf_norm(const float*, const float*, uint32_t, float, _Float16*, float*);
 __global__ void k_pf_qkrope(const float*, const float*, const float*, const float2*, uint32_t, uint32_t, uint32_t,
@@ -207,7 +208,19 @@ struct qh_ctx {
         uint32_t *ids = nullptr, *goff = nullptr, *tok = nullptr, *asg = nullptr, *te = nullptr, *tm = nullptr,
                  *ntile = nullptr;
         uint32_t max_tiles = 0;
+        _Float16* W16 = nullptr;  // fp16 copy of one layer's q|k|v or o weights
     } pf;
+
+    // library GEMMs of the prefill's dense projections (hipBLASLt): one plan
+    // (descriptors + chosen algorithm) per (N, K, tokens, accumulate) shape
+    struct GemmPlan {
+        hipblasLtMatmulDesc_t desc = nullptr;
+        hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+        hipblasLtMatmulAlgo_t algo{};
+    };
+    hipblasLtHandle_t blt = nullptr;
+    DevBuf blt_ws;
+    std::map<std::array<uint32_t, 4>, GemmPlan> plans;
 
     // scratch for the API surfaces
     DevBuf sa, sb, sc, sd;
@@ -218,7 +231,17 @@ struct qh_ctx {
     DevBuf valid, samp_logits, samp_valid, samp_out;
     size_t valid_n = 0;
 
-    ~qh_ctx() { drop_model(); if (s) (void)hipStreamDestroy(s); }
+    ~qh_ctx() {
+        drop_model();
+        for (auto& kv : plans) {
+            (void)hipblasLtMatrixLayoutDestroy(kv.second.la);
+            (void)hipblasLtMatrixLayoutDestroy(kv.second.lb);
+            (void)hipblasLtMatrixLayoutDestroy(kv.second.lc);
+            (void)hipblasLtMatmulDescDestroy(kv.second.desc);
+        }
+        if (blt) (void)hipblasLtDestroy(blt);
+        if (s) (void)hipStreamDestroy(s);
+    }
 
     void drop_model() {
         if (exec) (void)hipGraphExecDestroy(exec);
@@ -838,6 +861,7 @@ void prefill_alloc(qh_ctx* c, uint32_t cap) {
         {4, (void**)&P.ntile},
         {(uint64_t)d.kvheads * d.ctx * 128 * 2, (void**)&P.Kh},
         {(uint64_t)d.kvheads * 128 * ((d.ctx + 63) / 64 * 64) * 2, (void**)&P.Vth},
+        {std::max((qd + 2 * kvd) * H, H * qd) * 2, (void**)&P.W16},
     };
     uint64_t total = 0;
     for (const R& r : regs) total += up(r.bytes);
@@ -857,11 +881,55 @@ template <class F> void dispatch_km(uint32_t kind, F f) {
     else f(std::integral_constant<uint32_t, Q6_K>{});
 }
 
-void pf_gemm(qh_ctx* c, const DevMat& W, const _Float16* A, uint32_t lda, uint32_t M, float* C, uint32_t ldc,
-             bool add) {
-    const dim3 grid((W.rows + 127) / 128, (M + 127) / 128);
-    dispatch_km(W.kind, [&](auto K) {
-        hipLaunchKernelGGL(k_gemm<decltype(K)::value>, grid, dim3(256), 0, c->s, A, lda, M, W, C, ldc, add ? 1u : 0u);
+#define BLT_OK(x)                                                                              \
+    do {                                                                                       \
+        const hipblasStatus_t st_ = (x);                                                       \
+        if (st_ != HIPBLAS_STATUS_SUCCESS) throw Error(std::string(#x) + " failed: status " + std::to_string((int)st_)); \
+    } while (0)
+
+// C[S][N] (= or +=) X16[S][K] W16[N][K]^T on the matrix cores: fp16 operands,
+// f32 accumulation and output (hipBLASLt, column-major C^T = W X^T).
+void pf_dense(qh_ctx* c, const _Float16* W16, uint32_t N, uint32_t K, const _Float16* X16, uint32_t S, float* C,
+              bool accumulate) {
+    if (!c->blt) {
+        BLT_OK(hipblasLtCreate(&c->blt));
+        c->blt_ws.alloc(32u << 20);
+    }
+    const std::array<uint32_t, 4> key{N, K, S, accumulate ? 1u : 0u};
+    auto it = c->plans.find(key);
+    if (it == c->plans.end()) {
+        qh_ctx::GemmPlan g;
+        BLT_OK(hipblasLtMatmulDescCreate(&g.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F));
+        const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+        BLT_OK(hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta));
+        BLT_OK(hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb));
+        BLT_OK(hipblasLtMatrixLayoutCreate(&g.la, HIP_R_16F, K, N, K));
+        BLT_OK(hipblasLtMatrixLayoutCreate(&g.lb, HIP_R_16F, K, S, K));
+        BLT_OK(hipblasLtMatrixLayoutCreate(&g.lc, HIP_R_32F, N, S, N));
+        hipblasLtMatmulPreference_t pref;
+        BLT_OK(hipblasLtMatmulPreferenceCreate(&pref));
+        const uint64_t wsz = c->blt_ws.n;
+        BLT_OK(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz, sizeof wsz));
+        hipblasLtMatmulHeuristicResult_t res{};
+        int n = 0;
+        const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(c->blt, g.desc, g.la, g.lb, g.lc, g.lc, pref, 1, &res, &n);
+        (void)hipblasLtMatmulPreferenceDestroy(pref);
+        if (st != HIPBLAS_STATUS_SUCCESS || n < 1) throw Error("no hipBLASLt algorithm for a prefill projection");
+        g.algo = res.algo;
+        it = c->plans.emplace(key, g).first;
+    }
+    const qh_ctx::GemmPlan& g = it->second;
+    const float alpha = 1.f, beta = accumulate ? 1.f : 0.f;
+    BLT_OK(hipblasLtMatmul(c->blt, g.desc, &alpha, W16, g.la, X16, g.lb, &beta, C, g.lc, C, g.lc, &g.algo,
+                           c->blt_ws.p, c->blt_ws.n, c->s));
+}
+
+// fp16 copy of a Q4_K / Q6_K matrix into rows [r0, r0 + m.rows) of dst
+void pf_dequant16(qh_ctx* c, const DevMat& m, uint32_t r0, _Float16* dst) {
+    const uint32_t units = m.rows * (m.cols / 32);
+    dispatch_km(m.kind, [&](auto K) {
+        hipLaunchKernelGGL(k_dequant16<decltype(K)::value>, dim3((units + kBlock - 1) / kBlock), dim3(kBlock), 0, c->s,
+                           m, m.rows, r0, dst);
     });
 }
 
@@ -874,9 +942,11 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
     const uint32_t H = d.hidden, qd = d.heads * 128, kvd = d.kvheads * 128, row = qd + 2 * kvd;
     hipLaunchKernelGGL(k_pf_norm, dim3(S), dim3(kBlock), 0, c->s, P.X, L.attn_norm, H, d.eps, P.Xn16,
                        (float*)nullptr);
-    pf_gemm(c, L.q, P.Xn16, H, S, P.QKV, row, false);
-    pf_gemm(c, L.k, P.Xn16, H, S, P.QKV + qd, row, false);
-    pf_gemm(c, L.v, P.Xn16, H, S, P.QKV + qd + kvd, row, false);
+    // q | k | v as one library GEMM over the fp16 copy of the three matrices
+    pf_dequant16(c, L.q, 0, P.W16);
+    pf_dequant16(c, L.k, qd, P.W16);
+    pf_dequant16(c, L.v, qd + kvd, P.W16);
+    pf_dense(c, P.W16, row, H, P.Xn16, S, P.QKV, false);
     const uint32_t vp = (d.ctx + 63) / 64 * 64;  // row pitch of the transposed V copy
     if (p0 > 0)  // fp16 copies of this layer's earlier positions
         hipLaunchKernelGGL(k_pf_kvh, dim3(p0), dim3(kBlock), 0, c->s, L.kcache, L.vcache, 0u, d.kvheads, d.ctx, vp,
@@ -885,7 +955,8 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
                        d.heads, d.kvheads, d.ctx, d.eps, P.Q16, L.kcache, L.vcache, P.Kh, P.Vth, vp);
     hipLaunchKernelGGL(k_pf_attn, dim3((S + 31) / 32, 2 * d.kvheads), dim3(256), 0, c->s, P.Q16, P.Kh, P.Vth, p0, S,
                        d.heads / d.kvheads, d.ctx, vp, qd, P.O16);
-    pf_gemm(c, L.o, P.O16, qd, S, P.X, H, true);
+    pf_dequant16(c, L.o, 0, P.W16);
+    pf_dense(c, P.W16, H, qd, P.O16, S, P.X, true);  // residual add (model.rs:246-248)
     hipLaunchKernelGGL(k_pf_norm, dim3(S), dim3(kBlock), 0, c->s, P.X, L.ffn_norm, H, d.eps, P.Xn16, P.Xn32);
     hipLaunchKernelGGL(k_pf_router, dim3((S + 15) / 16), dim3(kBlock), 0, c->s, P.Xn32, L.router, S, H, d.experts,
                        P.LR);

@@ -183,36 +183,6 @@ __device__ __forceinline__ uint32_t acc_col(uint32_t nt) {
     return 64 * wn + 16 * nt + (lane & 15);
 }
 
-// Dense: C[m][n] (=, or += when add) A[m] . W[n] for m < M, n < W.rows.
-// Grid (ceil(N/128), ceil(M/128)).
-template <uint32_t KIND>
-__global__ __launch_bounds__(kGT) void k_gemm(const _Float16* A, uint32_t lda, uint32_t M, DevMat W, float* C,
-                                              uint32_t ldc, uint32_t add) {
-    __shared__ __align__(16) _Float16 smem[2 * kGM * kGL];
-    const uint32_t n0 = blockIdx.x * kGN, m0 = blockIdx.y * kGM, r = threadIdx.x >> 1;
-    const _Float16* arow = m0 + r < M ? A + (size_t)(m0 + r) * lda : nullptr;
-    const uint8_t* const wrow[1] = {n0 + r < W.rows ? W.w + (size_t)(n0 + r) * W.drb : nullptr};
-    f4v acc[1][4][4];
-#pragma unroll
-    for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-        for (int nt = 0; nt < 4; nt++) acc[0][mt][nt] = f4v{0.f, 0.f, 0.f, 0.f};
-    gemm_tile<KIND, 1>(arow, wrow, W.geo, W.cols, acc, smem, smem + kGM * kGL);
-#pragma unroll
-    for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-        for (int nt = 0; nt < 4; nt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t m = m0 + acc_row(mt, i), n = n0 + acc_col(nt);
-                if (m < M && n < W.rows) {
-                    float* p = C + (size_t)m * ldc + n;
-                    *p = add ? *p + acc[0][mt][nt][i] : acc[0][mt][nt][i];
-                }
-            }
-}
-
-
 // gate/up of the routed experts + SwiGLU (model.rs:266-274):
 // Hs[goff[e] + r][n] = silu(g) * u, fp16, for the sorted assignments.
 template <uint32_t KIND>
@@ -724,10 +694,29 @@ __global__ __launch_bounds__(kBlock) void k_pf_kvh(const float* kcache, const fl
     }
 }
 
+// fp16 copy of rows [0, rows) of a Q4_K / Q6_K matrix into dst rows
+// [r0, r0 + rows) (row pitch = cols), for the dense projections that run as
+// library GEMMs.  One thread per (row, super-block, 64-column slice, half):
+// the same dequantisation as the fused GEMM tiles (WSlice).
+template <uint32_t KIND>
+__global__ __launch_bounds__(kBlock) void k_dequant16(DevMat W, uint32_t rows, uint32_t r0, _Float16* dst) {
+    const uint32_t per_row = W.cols / 32;  // (super-block, slice, half) units
+    const uint32_t i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= rows * per_row) return;
+    const uint32_t r = i / per_row, u = i % per_row, b = u >> 3, sl = (u >> 1) & 3, h = u & 1;
+    WSlice<KIND> w;
+    w.load(W.w + (size_t)r * W.drb, W.geo, b, sl, h);
+    _Float16 lo[16], hi[16];
+    w.dequant(sl, h, lo, hi);
+    _Float16* o = dst + (size_t)(r0 + r) * W.cols + 256 * b + 64 * sl + 16 * h;
+    st_h16(o, lo);
+    st_h16(o + 32, hi);
+}
+
 #define QH_INSTANTIATE_PREFILL_GEMM(K)                                                                          \
-    template __global__ void k_gemm<K>(const _Float16*, uint32_t, uint32_t, DevMat, float*, uint32_t, uint32_t); \
     template __global__ void k_gemm_gateup<K>(const _Float16*, uint32_t, ExpertTiles, DevMat, DevMat, _Float16*);     \
-    template __global__ void k_gemm_down<K>(const _Float16*, ExpertTiles, DevMat, float*);
+    template __global__ void k_gemm_down<K>(const _Float16*, ExpertTiles, DevMat, float*);                          \
+    template __global__ void k_dequant16<K>(DevMat, uint32_t, uint32_t, _Float16*);
 QH_INSTANTIATE_PREFILL_GEMM(Q4_K)
 QH_INSTANTIATE_PREFILL_GEMM(Q6_K)
 
