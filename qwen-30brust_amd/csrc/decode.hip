@@ -854,6 +854,14 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
     if (4 * c.tid < H) x1 = reinterpret_cast<const float4*>(xs)[c.tid];
     const float s = 1.0f / sqrtf(dsum(sumsq4(x1), S.red) / (float)H + A.dm.eps);
     if (c.tid < E) S.lg[c.tid] = s * xs[H + c.tid];  // router logits (model.rs:249-256)
+    // xn = x' * (s * ffn_norm), in place (each thread rewrites its own float4;
+    // the routing barriers below order it before the dots)
+    if (4 * c.tid < H) {
+        xs[4 * c.tid] = x1.x * (s * fn.x);
+        xs[4 * c.tid + 1] = x1.y * (s * fn.y);
+        xs[4 * c.tid + 2] = x1.z * (s * fn.z);
+        xs[4 * c.tid + 3] = x1.w * (s * fn.w);
+    }
     QH_MARK(4, 1);
     // top-k by rank under the total order, lower index on ties (ops.rs:45-56;
     // bit-exact on these logits): j outranks i iff ck[j] > ck[i], with the
@@ -901,26 +909,18 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         }
     }
     QH_MARK(4, 2);
-    // gate/up rows of pairs p = gw*3 + k: (slot p / ff, row p % ff)
+    // gate/up rows of pairs p = gw*3 + k: (slot p / ff, row p % ff); the
+    // loads are unconditional (pair and chunk clamped, results of clamped
+    // pairs dropped) so that each pair's dots wait only for that pair
     typename Fmt<KG>::Raw wg[kPairsPerWave], wu[kPairsPerWave];
+    const uint32_t gch = min(c.lane, cpr - 1);
 #pragma unroll
     for (uint32_t k = 0; k < kPairsPerWave; k++) {
-        const uint32_t pr = c.gw * kPairsPerWave + k;
-        if (pr < top * ff && c.lane < cpr) {
-            const uint32_t ex = S.sid[pr / ff], rr = pr % ff;
-            wg[k] = Fmt<KG>::load(L.gate.w + (size_t)ex * L.gate.expert_stride + (size_t)rr * L.gate.drb, L.gate.geo,
-                                  c.lane);
-            wu[k] = Fmt<KG>::load(L.up.w + (size_t)ex * L.up.expert_stride + (size_t)rr * L.up.drb, L.up.geo, c.lane);
-        }
+        const uint32_t pr = min(c.gw * kPairsPerWave + k, top * ff - 1);
+        const uint32_t ex = S.sid[pr / ff], rr = pr % ff;
+        wg[k] = Fmt<KG>::load(L.gate.w + (size_t)ex * L.gate.expert_stride + (size_t)rr * L.gate.drb, L.gate.geo, gch);
+        wu[k] = Fmt<KG>::load(L.up.w + (size_t)ex * L.up.expert_stride + (size_t)rr * L.up.drb, L.up.geo, gch);
     }
-    // xn = x' * (s * ffn_norm), in place (each thread rewrites its own float4)
-    if (4 * c.tid < H) {
-        xs[4 * c.tid] = x1.x * (s * fn.x);
-        xs[4 * c.tid + 1] = x1.y * (s * fn.y);
-        xs[4 * c.tid + 2] = x1.z * (s * fn.z);
-        xs[4 * c.tid + 3] = x1.w * (s * fn.w);
-    }
-    __syncthreads();
     if (c.b == 0) {
         if (c.tid < top) {
             a.ids[c.tid] = S.ids[c.tid];
@@ -1010,11 +1010,15 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
     const uint32_t V = A.dm.vocab, ngrp = (V + kVocabRows - 1) / kVocabRows, cpr = c.H / 32;
     const uint32_t tag = A.base + 6 * (A.l1 - A.l0) + 1;
     using Raw = typename Fmt<KV>::Raw;
+    // unconditional loads (row and chunk clamped into the matrix; results of
+    // clamped rows are dropped): the compiler then waits for exactly the group
+    // it computes, not for the prefetched one behind it
+    const uint32_t ch = min(c.lane, cpr - 1);
     auto load_group = [&](Raw (&t)[kVocabRows], uint32_t gi) {
 #pragma unroll
         for (uint32_t k = 0; k < kVocabRows; k++) {
-            const uint32_t r = gi * kVocabRows + k;
-            if (gi < ngrp && r < V && c.lane < cpr) t[k] = Fmt<KV>::load(mv.w + (size_t)r * mv.drb, mv.geo, c.lane);
+            const uint32_t r = min(gi * kVocabRows + k, V - 1);
+            t[k] = Fmt<KV>::load(mv.w + (size_t)r * mv.drb, mv.geo, ch);
         }
     };
     Raw cur[kVocabRows], nxt[kVocabRows];
@@ -1033,7 +1037,7 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
     uint32_t bi = 0xffffffffu;
     bool nf = false;
     for (uint32_t gi = c.gw; gi < ngrp; gi += c.NWV) {
-        if (gi + c.NWV < ngrp) load_group(nxt, gi + c.NWV);
+        load_group(nxt, min(gi + c.NWV, ngrp - 1));
         float acc[kVocabRows];
 #pragma unroll
         for (uint32_t k = 0; k < kVocabRows; k++) {
