@@ -77,8 +77,8 @@ Args parse(int argc, char** argv) {
         std::exit(0);
     }
     if (a.command == "chat")
-        throw Fail("the chat command needs the tokenizer front end, which this engine does not include; "
-                   "drive it with token ids (logits)");
+        throw Fail("chat is the tokenizer front end qwen-30brust_amd/chat.py (same arguments): "
+                   "python qwen-30brust_amd/chat.py --model M --tokenizer T --prompt P");
     if (a.command != "devices" && a.command != "inspect" && a.command != "logits")
         throw Usage("unrecognized subcommand '" + a.command + "'");
     const bool compute = a.command == "logits";

@@ -1224,7 +1224,8 @@ int qh_device_name(int device, char* buf, size_t cap) {
         char arch[sizeof(p.gcnArchName) + 1] = {};
         std::memcpy(arch, p.gcnArchName, sizeof(p.gcnArchName));
         if (char* colon = std::strchr(arch, ':')) *colon = 0;
-        const std::string s = std::string(p.name) + " (" + arch + ", " + std::to_string(p.multiProcessorCount) +
+        const std::string name = p.name[0] ? std::string(p.name) : "HIP device " + std::to_string(device);
+        const std::string s = name + " (" + arch + ", " + std::to_string(p.multiProcessorCount) +
                               " CUs, " + std::to_string(p.totalGlobalMem >> 30) + " GiB)";
         if (cap == 0 || s.size() + 1 > cap) throw Error("device name buffer too small");
         std::memcpy(buf, s.c_str(), s.size() + 1);
