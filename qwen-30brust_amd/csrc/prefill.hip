@@ -33,28 +33,61 @@ constexpr int kGL = kGK + 8;  // LDS row pitch in halfs (144 bytes)
 // lo[i] = column 256 b + 64 s + 16 h + i, hi[i] = column 256 b + 64 s + 32 + 16 h + i.
 template <uint32_t KIND> struct WSlice;
 
+// fp16 pairs straight from small integers: v (< 64) in bits 0-7 and 16-23 of
+// p becomes 1024 + v in each half (0x6400 is 1024.0), exact; subtracting the
+// bias (1024 plus the format's offset) leaves the integer, also exact.
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ h2v int_pair(uint32_t p, _Float16 bias) {
+    const h2v v = __builtin_bit_cast(h2v, p | 0x64006400u);
+    return v - h2v{bias, bias};
+}
+// An f32 value as an fp16 head plus the fp16 rounding of the rest, each
+// broadcast to both halves of a pair.
+struct SplitH {
+    h2v hi, lo;
+    __device__ __forceinline__ explicit SplitH(float v) {
+        const _Float16 h = (_Float16)v, l = (_Float16)(v - (float)h);
+        hi = h2v{h, h};
+        lo = h2v{l, l};
+    }
+};
+// q a + b and q a for a pair of exact integers q
+__device__ __forceinline__ uint32_t affine(h2v q, const SplitH& a, const SplitH& b) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, a.hi, b.hi) + __builtin_elementwise_fma(q, a.lo, b.lo));
+}
+__device__ __forceinline__ uint32_t scale(h2v q, const SplitH& a) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, a.hi, q * a.lo));
+}
+// bytes i0 and i1 of w into bits 0-7 and 16-23 (v_perm_b32; selector 0x0c = zero byte)
+template <uint32_t SEL>
+__device__ __forceinline__ uint32_t byte_pair(uint32_t w) { return __builtin_amdgcn_perm(0u, w, SEL); }
+constexpr uint32_t kPair01 = 0x0c010c00u, kPair23 = 0x0c030c02u;
+
 template <> struct WSlice<Q4_K> {
     uint4 q, hdr;
     __device__ __forceinline__ void load(const uint8_t* row, const RowGeo& g, uint32_t b, uint32_t s, uint32_t h) {
         hdr = ld16(row + g.off_a + b * 16);
         q = ld16(row + g.off_b + b * 128 + s * 32 + h * 16);
     }
-    // d*sc*q - dmin*m (src/quant.rs:50-62), sub-blocks 2s (low nibbles) and 2s+1
-    __device__ __forceinline__ void dequant(uint32_t s, uint32_t, _Float16 (&lo)[16], _Float16 (&hi)[16]) const {
+    // d*sc*q - dmin*m (src/quant.rs:50-62), sub-blocks 2s (low nibbles) and
+    // 2s+1, as packed fp16 pairs: lo[i] = columns 2i, 2i+1 of the thread's 16.
+    // q is exact; d*sc and dmin*m (exact in f32) are split into fp16 head and
+    // tail so that no rounding of theirs is shared by the sub-block:
+    // v = fma(q, a_hi, -b_hi) + fma(q, a_lo, -b_lo), two roundings of v.
+    __device__ __forceinline__ void dequant(uint32_t s, uint32_t, uint32_t (&lo)[8], uint32_t (&hi)[8]) const {
         uint32_t scp, mp;
         kscale_pair(hdr.y, hdr.z, hdr.w, s, scp, mp);
         const float d = h2f(hdr.x & 0xffffu), dm = h2f(hdr.x >> 16);
-        const float a0 = d * (float)(scp & 0xffu), b0 = dm * (float)(mp & 0xffu);
-        const float a1 = d * (float)(scp >> 8), b1 = dm * (float)(mp >> 8);
+        const SplitH a0(d * (float)(scp & 0xffu)), b0(-(dm * (float)(mp & 0xffu)));
+        const SplitH a1(d * (float)(scp >> 8)), b1(-(dm * (float)(mp >> 8)));
         const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t byte = (w[k] >> (8 * j)) & 0xffu;
-                lo[4 * k + j] = (_Float16)(a0 * (float)(byte & 15u) - b0);
-                hi[4 * k + j] = (_Float16)(a1 * (float)(byte >> 4) - b1);
-            }
+            const uint32_t p01 = byte_pair<kPair01>(w[k]), p23 = byte_pair<kPair23>(w[k]);
+            lo[2 * k] = affine(int_pair(p01 & 0x000f000fu, 1024), a0, b0);
+            lo[2 * k + 1] = affine(int_pair(p23 & 0x000f000fu, 1024), a0, b0);
+            hi[2 * k] = affine(int_pair((p01 >> 4) & 0x000f000fu, 1024), a1, b1);
+            hi[2 * k + 1] = affine(int_pair((p23 >> 4) & 0x000f000fu, 1024), a1, b1);
         }
     }
 };
@@ -71,85 +104,75 @@ template <> struct WSlice<Q6_K> {
         sc = gld<uint2>(row + g.off_c + b * 16 + c * 8);
         d = ld_u16(row + g.off_d + b * 2);
     }
-    // d*sc*(q-32) (src/quant.rs:63-77): quarters q0 = 2 (s & 1) and q0 + 1 of chunk s/2
-    __device__ __forceinline__ void dequant(uint32_t s, uint32_t h, _Float16 (&lo)[16], _Float16 (&hi)[16]) const {
+    // d*sc*(q-32) (src/quant.rs:63-77): quarters q0 = 2 (s & 1) and q0 + 1 of
+    // chunk s/2, as packed fp16 pairs (6-bit q exact; d*sc as head + tail:
+    // v = fma(q, a_hi, q a_lo), one rounding of v)
+    __device__ __forceinline__ void dequant(uint32_t s, uint32_t h, uint32_t (&lo)[8], uint32_t (&hi)[8]) const {
         const uint32_t q0 = 2 * (s & 1), sh = (s & 1) * 4;
         const uint32_t i0 = q0 * 2 + h, i1 = (q0 + 1) * 2 + h;  // scale bytes
         const uint32_t s0 = i0 < 4 ? sc.x >> (8 * i0) : sc.y >> (8 * (i0 - 4));
         const uint32_t s1 = i1 < 4 ? sc.x >> (8 * i1) : sc.y >> (8 * (i1 - 4));
         const float df = h2f(d);
-        const float a0 = df * (float)(int8_t)(s0 & 0xffu), a1 = df * (float)(int8_t)(s1 & 0xffu);
+        const SplitH a0(df * (float)(int8_t)(s0 & 0xffu)), a1(df * (float)(int8_t)(s1 & 0xffu));
         const uint32_t L0[4] = {l0.x, l0.y, l0.z, l0.w}, L1[4] = {l1.x, l1.y, l1.z, l1.w};
         const uint32_t QH[4] = {qh.x, qh.y, qh.z, qh.w};
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t hb = (QH[k] >> (8 * j)) & 0xffu;
-                const int qa = (int)(((L0[k] >> (8 * j + sh)) & 15u) | (((hb >> (2 * q0)) & 3u) << 4)) - 32;
-                const int qb = (int)(((L1[k] >> (8 * j + sh)) & 15u) | (((hb >> (2 * q0 + 2)) & 3u) << 4)) - 32;
-                lo[4 * k + j] = (_Float16)(a0 * (float)qa);
-                hi[4 * k + j] = (_Float16)(a1 * (float)qb);
-            }
+            // four 6-bit values per word: low nibble | two high bits << 4
+            const uint32_t va = ((L0[k] >> sh) & 0x0f0f0f0fu) | (((QH[k] >> (2 * q0)) & 0x03030303u) << 4);
+            const uint32_t vb = ((L1[k] >> sh) & 0x0f0f0f0fu) | (((QH[k] >> (2 * q0 + 2)) & 0x03030303u) << 4);
+            lo[2 * k] = scale(int_pair(byte_pair<kPair01>(va), 1056), a0);
+            lo[2 * k + 1] = scale(int_pair(byte_pair<kPair23>(va), 1056), a0);
+            hi[2 * k] = scale(int_pair(byte_pair<kPair01>(vb), 1056), a1);
+            hi[2 * k + 1] = scale(int_pair(byte_pair<kPair23>(vb), 1056), a1);
         }
     }
 };
 
-__device__ __forceinline__ void st_h16(_Float16* dst, const _Float16 (&v)[16]) {
-    h8v a, b;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        a[i] = v[i];
-        b[i] = v[8 + i];
-    }
-    *reinterpret_cast<h8v*>(dst) = a;
-    *reinterpret_cast<h8v*>(dst + 8) = b;
+// 16 fp16 values (8 packed pairs) to LDS / global, two 16-byte stores
+__device__ __forceinline__ void st_p16(_Float16* dst, const uint32_t (&v)[8]) {
+    *reinterpret_cast<uint4*>(dst) = make_uint4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<uint4*>(dst + 8) = make_uint4(v[4], v[5], v[6], v[7]);
 }
 
 // ---------------------------------------------------------------- GEMM --
 // acc[nb][mt][nt] += A[m0 .. m0+128) x W_nb[n0 .. n0+128)^T over K columns.
-// arow(r): pointer to the fp16 row of tile row r (nullptr: zero row).
-// wrow[nb]: this thread's weight row (row n0 + tid/2 of matrix nb; nullptr:
-// zero row).  Wave w owns output rows 64 (w & 1) .., columns 64 (w >> 1) ..
-template <uint32_t KIND, int NB>
+// arow: pointer to the fp16 row of tile row r (any valid row when r is past
+// the tile's rows: those outputs are not stored).  wrow[nb]: this thread's
+// weight row (row n0 + tid/2 of matrix nb; likewise any valid row past the
+// matrix).  Wave w owns output rows 64 (w & 1) .., columns 64 (w >> 1) ..
+// STAGES register stages of global loads run ahead of the LDS tile: with 2,
+// the loads of slice k + 2 are in flight while slice k is multiplied.  The
+// loads are unconditional, so each wait covers exactly one stage.
+template <uint32_t KIND, int NB, int STAGES = 1>
 __device__ __forceinline__ void gemm_tile(const _Float16* arow, const uint8_t* const (&wrow)[NB], const RowGeo& g,
                                           uint32_t K, f4v (&acc)[NB][4][4], _Float16* As, _Float16* Ws) {
     const uint32_t tid = threadIdx.x, r = tid >> 1, h = tid & 1, lane = tid & 63, w = tid >> 6;
     const uint32_t wm = w & 1, wn = w >> 1;
-    uint4 av[4];
-    WSlice<KIND> ws[NB];
-    auto gload = [&](uint32_t k0) {
+    uint4 av[STAGES][4];
+    WSlice<KIND> ws[STAGES][NB];
+    auto gload = [&](int st, uint32_t k0) {
+        k0 = min(k0, K - kGK);  // past the end: a harmless reload of the last slice
         const uint32_t b = k0 >> 8, s = (k0 >> 6) & 3;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            av[i] = arow ? gld<uint4>(arow + k0 + 32 * h + 8 * i) : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < 4; i++) av[st][i] = gld<uint4>(arow + k0 + 32 * h + 8 * i);
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++)
-            if (wrow[nb]) ws[nb].load(wrow[nb], g, b, s, h);
+        for (int nb = 0; nb < NB; nb++) ws[st][nb].load(wrow[nb], g, b, s, h);
     };
-    auto lstore = [&](uint32_t k0) {
+    auto lstore = [&](int st, uint32_t k0) {
         const uint32_t s = (k0 >> 6) & 3;
 #pragma unroll
-        for (int i = 0; i < 4; i++) *reinterpret_cast<uint4*>(As + r * kGL + 32 * h + 8 * i) = av[i];
+        for (int i = 0; i < 4; i++) *reinterpret_cast<uint4*>(As + r * kGL + 32 * h + 8 * i) = av[st][i];
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) {
-            _Float16 lo[16], hi[16];
-            if (wrow[nb]) {
-                ws[nb].dequant(s, h, lo, hi);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 16; i++) lo[i] = hi[i] = (_Float16)0.f;
-            }
+            uint32_t lo[8], hi[8];
+            ws[st][nb].dequant(s, h, lo, hi);
             _Float16* dst = Ws + nb * kGN * kGL + r * kGL;
-            st_h16(dst + 16 * h, lo);
-            st_h16(dst + 32 + 16 * h, hi);
+            st_p16(dst + 16 * h, lo);
+            st_p16(dst + 32 + 16 * h, hi);
         }
     };
-    gload(0);
-    for (uint32_t k0 = 0; k0 < K; k0 += kGK) {
-        lstore(k0);
-        __syncthreads();
-        if (k0 + kGK < K) gload(k0 + kGK);
+    auto mma = [&]() {
 #pragma unroll
         for (uint32_t ks = 0; ks < 2; ks++) {
             const uint32_t kc = 32 * ks + 8 * (lane >> 4);
@@ -169,7 +192,21 @@ __device__ __forceinline__ void gemm_tile(const _Float16* arow, const uint8_t* c
                 }
             }
         }
-        __syncthreads();
+    };
+#pragma unroll
+    for (int st = 0; st < STAGES; st++) gload(st, st * kGK);
+    for (uint32_t k0 = 0; k0 < K; k0 += STAGES * kGK) {
+#pragma unroll
+        for (int st = 0; st < STAGES; st++) {
+            const uint32_t kk = k0 + st * kGK;
+            if (kk < K) {  // uniform
+                lstore(st, kk);
+                __syncthreads();
+                gload(st, kk + STAGES * kGK);
+                mma();
+                __syncthreads();
+            }
+        }
     }
 }
 
@@ -193,10 +230,10 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_gateup(const _Float16* Xn, uint
     const uint32_t e = G.te[blockIdx.y], mt0 = G.tm[blockIdx.y];
     const uint32_t base = G.goff[e], rows = G.goff[e + 1] - base;
     const uint32_t n0 = blockIdx.x * kGN, r = threadIdx.x >> 1, ff = Wg.rows;
-    const _Float16* arow = mt0 + r < rows ? Xn + (size_t)G.tok[base + mt0 + r] * H : nullptr;
-    const bool nok = n0 + r < ff;
-    const uint8_t* const wrow[2] = {nok ? Wg.w + e * Wg.expert_stride + (size_t)(n0 + r) * Wg.drb : nullptr,
-                                    nok ? Wu.w + e * Wu.expert_stride + (size_t)(n0 + r) * Wu.drb : nullptr};
+    const _Float16* arow = Xn + (size_t)(mt0 + r < rows ? G.tok[base + mt0 + r] : 0u) * H;
+    const uint32_t wr = min(n0 + r, ff - 1);
+    const uint8_t* const wrow[2] = {Wg.w + e * Wg.expert_stride + (size_t)wr * Wg.drb,
+                                    Wu.w + e * Wu.expert_stride + (size_t)wr * Wu.drb};
     f4v acc[2][4][4];
 #pragma unroll
     for (int nb = 0; nb < 2; nb++)
@@ -228,14 +265,14 @@ __global__ __launch_bounds__(kGT) void k_gemm_down(const _Float16* Hs, ExpertTil
     const uint32_t e = G.te[blockIdx.y], mt0 = G.tm[blockIdx.y];
     const uint32_t base = G.goff[e], rows = G.goff[e + 1] - base;
     const uint32_t n0 = blockIdx.x * kGN, r = threadIdx.x >> 1, ff = Wd.cols, N = Wd.rows;
-    const _Float16* arow = mt0 + r < rows ? Hs + (size_t)(base + mt0 + r) * ff : nullptr;
-    const uint8_t* const wrow[1] = {n0 + r < N ? Wd.w + e * Wd.expert_stride + (size_t)(n0 + r) * Wd.drb : nullptr};
+    const _Float16* arow = Hs + (size_t)(base + min(mt0 + r, rows - 1)) * ff;
+    const uint8_t* const wrow[1] = {Wd.w + e * Wd.expert_stride + (size_t)min(n0 + r, N - 1) * Wd.drb};
     f4v acc[1][4][4];
 #pragma unroll
     for (int mt = 0; mt < 4; mt++)
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) acc[0][mt][nt] = f4v{0.f, 0.f, 0.f, 0.f};
-    gemm_tile<KIND, 1>(arow, wrow, Wd.geo, ff, acc, smem, smem + kGM * kGL);
+    gemm_tile<KIND, 1, 2>(arow, wrow, Wd.geo, ff, acc, smem, smem + kGM * kGL);
 #pragma unroll
     for (int mt = 0; mt < 4; mt++)
 #pragma unroll
@@ -706,11 +743,11 @@ __global__ __launch_bounds__(kBlock) void k_dequant16(DevMat W, uint32_t rows, u
     const uint32_t r = i / per_row, u = i % per_row, b = u >> 3, sl = (u >> 1) & 3, h = u & 1;
     WSlice<KIND> w;
     w.load(W.w + (size_t)r * W.drb, W.geo, b, sl, h);
-    _Float16 lo[16], hi[16];
+    uint32_t lo[8], hi[8];
     w.dequant(sl, h, lo, hi);
     _Float16* o = dst + (size_t)(r0 + r) * W.cols + 256 * b + 64 * sl + 16 * h;
-    st_h16(o, lo);
-    st_h16(o + 32, hi);
+    st_p16(o, lo);
+    st_p16(o + 32, hi);
 }
 
 #define QH_INSTANTIATE_PREFILL_GEMM(K)                                                                          \
