@@ -2,14 +2,17 @@
 // src/sampling.rs:26-35) as ONE launch of one 512-thread workgroup per CU,
 // preceded by k_embed (the embedding row of tokens[pos], model.rs:225).
 //
-// Per layer the workgroups run six phases:
-//   A  RMSNorm + q/k/v projections
+// Per layer the workgroups run five phases:
+//   A  RMSNorm + q/k/v projections; router workgroup e also reduces
+//      sum_j router[e][j] ffn_norm[j] x[j]
 //   B  Q/K RMSNorm, RoPE, KV append, split-T GQA attention; chunk 0 of each
 //      KV head merges the other chunks' partials
-//   C  output projection + residual for this workgroup's rows of x
-//   D  every workgroup reads all of x' and its RMS scale; workgroup e < E
-//      computes router logit e
-//   E  top-k routing (every workgroup, identically), gate/up + SwiGLU rows
+//   C  output projection + residual for this workgroup's rows of x; router
+//      workgroup e adds its row of the precomputed router fold times the
+//      attention output, giving the unscaled router logit e of x'
+//   E  every workgroup reads x' and the unscaled logits, scales them by the
+//      RMS scale of x', top-k routing (identically everywhere), gate/up +
+//      SwiGLU rows
 //   F  down projections + routing-weighted combine + residual, own rows
 // then V: final RMSNorm, vocab projection and argmax partials, and the
 // argmax / next token / position advance by workgroup 0.
@@ -17,7 +20,7 @@
 // Hand-over without flags or barriers: every value one workgroup passes to
 // another is a 64-bit word (tag << 32) | bits written through to memory with
 // a system-scope store, where tag = base + the number of the writing phase
-// (6 per layer, 1 for V; base grows by the launch's phase count, so tags
+// (6 numbers per layer, 1 for V; base grows by the launch's phase count, so tags
 // never repeat between launches).  A reader polls exactly the words it needs
 // until each carries the tag it expects: a phase starts as soon as its own
 // inputs exist, and no producer waits for its stores to complete.  Before it
