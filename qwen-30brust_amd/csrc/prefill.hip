@@ -193,19 +193,19 @@ __device__ __forceinline__ void gemm_tile(const _Float16* arow, const uint8_t* c
             }
         }
     };
+    // K is a multiple of STAGES * 64 (the caller checks), so every stage of
+    // every round runs: straight-line code the compiler can count loads in
 #pragma unroll
     for (int st = 0; st < STAGES; st++) gload(st, st * kGK);
     for (uint32_t k0 = 0; k0 < K; k0 += STAGES * kGK) {
 #pragma unroll
         for (int st = 0; st < STAGES; st++) {
             const uint32_t kk = k0 + st * kGK;
-            if (kk < K) {  // uniform
-                lstore(st, kk);
-                __syncthreads();
-                gload(st, kk + STAGES * kGK);
-                mma();
-                __syncthreads();
-            }
+            lstore(st, kk);
+            __syncthreads();
+            gload(st, kk + STAGES * kGK);
+            mma();
+            __syncthreads();
         }
     }
 }
@@ -267,6 +267,13 @@ __global__ __launch_bounds__(kGT) void k_gemm_down(const _Float16* Hs, ExpertTil
     const uint32_t n0 = blockIdx.x * kGN, r = threadIdx.x >> 1, ff = Wd.cols, N = Wd.rows;
     const _Float16* arow = Hs + (size_t)(base + min(mt0 + r, rows - 1)) * ff;
     const uint8_t* const wrow[1] = {Wd.w + e * Wd.expert_stride + (size_t)min(n0 + r, N - 1) * Wd.drb};
+    // output rows of this lane's accumulators: their assignment indices,
+    // fetched now so the epilogue does not wait on them one by one
+    uint32_t dst[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) dst[mt][i] = G.asg[base + min(mt0 + acc_row(mt, i), rows - 1)];
     f4v acc[1][4][4];
 #pragma unroll
     for (int mt = 0; mt < 4; mt++)
@@ -280,7 +287,7 @@ __global__ __launch_bounds__(kGT) void k_gemm_down(const _Float16* Hs, ExpertTil
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t m = mt0 + acc_row(mt, i), n = n0 + acc_col(nt);
-                if (m < rows && n < N) Y[(size_t)G.asg[base + m] * N + n] = acc[0][mt][nt][i];
+                if (m < rows && n < N) Y[(size_t)dst[mt][i] * N + n] = acc[0][mt][nt][i];
             }
 }
 
