@@ -924,13 +924,6 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         wg[k] = Fmt<KG>::load(L.gate.w + (size_t)ex * L.gate.expert_stride + (size_t)rr * L.gate.drb, L.gate.geo, gch);
         wu[k] = Fmt<KG>::load(L.up.w + (size_t)ex * L.up.expert_stride + (size_t)rr * L.up.drb, L.up.geo, gch);
     }
-    if (c.b == 0) {
-        if (c.tid < top) {
-            a.ids[c.tid] = S.ids[c.tid];
-            a.wts[c.tid] = S.wts[c.tid];
-        }
-        if (c.tid < E) a.logits_r[c.tid] = S.lg[c.tid];
-    }
     QH_MARK(4, 4);
     const uint32_t tag_h = ptag(A, l, 5);
     {
@@ -954,7 +947,7 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
             }
         }
     }
-    QH_MARK(4, 5);
+    QH_MARK_LAST(4, 5);
     __syncthreads();  // S.hv complete; every wave is done with xn, which the gather overwrites
     {
         // this workgroup's outputs [slot][ff] flat at b * kHBlock, one store instruction
@@ -962,17 +955,19 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         if (c.tid < kHBlock && i < top * ff) put(A.th + i, S.hv[c.tid], tag_h);
     }
     // down rows of phase F (row r0 + wv of each routed expert), requested
-    // before the wait for the SwiGLU outputs: lane units u = lane + 64 i = (slot u / dcpr, chunk u % dcpr)
+    // before the wait for the SwiGLU outputs, so that they arrive during the
+    // hand-over (issued with the gate/up rows they slowed those down): lane
+    // units u = lane + 64 i = (slot u / dcpr, chunk u % dcpr).  Unconditional,
+    // in straight-line code (row and unit clamped, results of clamped units
+    // dropped): loads issued under a branch made the compiler wait for each
+    // unit's loads before issuing the next, one memory round trip per unit.
     const uint32_t dcpr = ff / 32, U = top * dcpr;
+    const uint8_t* dbase = L.down.w + (size_t)min(c.r0 + c.wv, H - 1) * L.down.drb;
     typename Fmt<KD>::Raw wd[kDownUnits];
 #pragma unroll
     for (uint32_t i = 0; i < kDownUnits; i++) {
-        const uint32_t u = c.lane + 64 * i;
-        if (c.wv < c.nr && u < U) {
-            const uint8_t* drow = L.down.w + (size_t)S.ids[u / dcpr] * L.down.expert_stride +
-                                  (size_t)(c.r0 + c.wv) * L.down.drb;
-            wd[i] = Fmt<KD>::load(drow, L.down.geo, u % dcpr);
-        }
+        const uint32_t u = min(c.lane + 64 * i, U - 1);
+        wd[i] = Fmt<KD>::load(dbase + (size_t)S.sid[u / dcpr] * L.down.expert_stride, L.down.geo, u % dcpr);
     }
     QH_MARK(4, 3);
     // ================================================ F: down + combine
@@ -995,11 +990,20 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         acc = wave_sum(acc);
         if (c.lane == 0) S.xo[c.wv] += acc;  // x += sum_s w_s down_s (model.rs:281-287)
     }
-    QH_MARK(5, 2);
+    QH_MARK_LAST(5, 2);
     __syncthreads();
     if (c.tid < c.nr) {
         put(A.tx2 + c.r0 + c.tid, S.xo[c.tid], ptag(A, l, 6));  // one store instruction
         if (last) a.x[c.r0 + c.tid] = S.xo[c.tid];            // x after the launch, for the host
+    }
+    // the routing of the layer, for the host (stored last: a later use of a
+    // store's registers waits for the store, and these wait for nothing else)
+    if (c.b == 0) {
+        if (c.tid < top) {
+            a.ids[c.tid] = S.ids[c.tid];
+            a.wts[c.tid] = S.wts[c.tid];
+        }
+        if (c.tid < E) a.logits_r[c.tid] = S.lg[c.tid];
     }
     return true;
 }
