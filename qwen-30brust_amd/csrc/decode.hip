@@ -472,11 +472,11 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
     // router workgroup e: router[e] * ffn_norm, for its share of logit e
     uint32_t re;
     const bool rt = router_wg(A, c, re);
-    float4 rw = make_float4(0.f, 0.f, 0.f, 0.f);
+    // (multiplied after the wait for x'': a product here made the loads wait)
+    float4 wr = make_float4(0.f, 0.f, 0.f, 0.f), fw = wr;
     if (rt && 4 * c.tid < c.H) {
-        const float4 wr = gld<float4>(L.router.w + (size_t)re * L.router.drb + 16 * c.tid);
-        const float4 fw = gld<float4>(L.ffn_norm + 4 * c.tid);
-        rw = make_float4(wr.x * fw.x, wr.y * fw.y, wr.z * fw.z, wr.w * fw.w);
+        wr = gld<float4>(L.router.w + (size_t)re * L.router.drb + 16 * c.tid);
+        fw = gld<float4>(L.ffn_norm + 4 * c.tid);
     }
     attn_prefetch(A, L, c, P);
     float* xs = S.big;
@@ -489,6 +489,7 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
         return false;  // x'' of the previous layer (phase F)
     }
     QH_MARK(0, 1);
+    const float4 rw = make_float4(wr.x * fw.x, wr.y * fw.y, wr.z * fw.z, wr.w * fw.w);
     float rdot;
     const float4 xv = norm_in_lds_dot(c, xs, nw, A.dm.eps, S.red, rw, rdot);
     if (rt && c.tid == 0) S.ra = rdot;
@@ -1030,6 +1031,8 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
     };
     Raw cur[kVocabRows], nxt[kVocabRows];
     load_group(cur, c.gw);
+    // read now, used by workgroup 0 after the argmax hand-over
+    const uint32_t n_given = a.st->n_given;
     float4 on = make_float4(0.f, 0.f, 0.f, 0.f);
     if (4 * c.tid < c.H) on = gld<float4>(A.onorm + 4 * c.tid);
     QH_MARK(6, 0);
@@ -1104,7 +1107,7 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
         uint32_t i0 = S.bi[0];
         for (int w = 1; w < kDW; w++) best_merge(k0, i0, S.bk[w], S.bi[w]);
         a.st->argmax = i0;
-        if (c.pos + 1 >= a.st->n_given && c.pos + 1 <= A.dm.ctx) a.tokens[c.pos + 1] = i0;
+        if (c.pos + 1 >= n_given && c.pos + 1 <= A.dm.ctx) a.tokens[c.pos + 1] = i0;
         a.st->pos = c.pos + 1;
     }
     QH_MARK(6, 3);

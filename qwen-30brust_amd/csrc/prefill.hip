@@ -486,28 +486,51 @@ __global__ __launch_bounds__(kBlock) void k_pf_topk(const float* LR, uint32_t S,
 __global__ __launch_bounds__(1024) void k_pf_group(const uint32_t* ids, uint32_t n, uint32_t top, uint32_t E,
                                                    uint32_t* goff, uint32_t* tok, uint32_t* asg, uint32_t* te,
                                                    uint32_t* tm, uint32_t* ntile) {
-    __shared__ uint32_t cnt[256], cur[256];
-    for (uint32_t e = threadIdx.x; e < E; e += 1024) cnt[e] = 0;
+    __shared__ uint32_t cnt[256], cur[256], tb[256];  // E <= 255
+    for (uint32_t e = threadIdx.x; e < 256; e += 1024) cnt[e] = 0;
     __syncthreads();
     for (uint32_t a = threadIdx.x; a < n; a += 1024)
         if (ids[a] < E) atomicAdd(&cnt[ids[a]], 1u);  // ids < E unless routing failed (reported)
     __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t off = 0, nt = 0;
-        for (uint32_t e = 0; e < E; e++) {
-            goff[e] = off;
-            cur[e] = off;
-            for (uint32_t m = 0; m < cnt[e]; m += kGM) {
-                te[nt] = e;
-                tm[nt] = m;
-                nt++;
-            }
-            off += cnt[e];
+    if (threadIdx.x < 64) {
+        // wave 0: exclusive prefix sums of the counts and of the tile counts,
+        // lane l holding experts 4l .. 4l + 3
+        const uint32_t lane = threadIdx.x;
+        uint32_t c4[4], t4[4], cs = 0, ts = 0;
+#pragma unroll
+        for (uint32_t k = 0; k < 4; k++) {
+            c4[k] = cnt[4 * lane + k];  // zero past E
+            t4[k] = (c4[k] + kGM - 1) / kGM;
+            cs += c4[k];
+            ts += t4[k];
         }
-        goff[E] = off;
-        *ntile = nt;
+        uint32_t ci = cs, ti = ts;
+#pragma unroll
+        for (uint32_t o = 1; o < 64; o <<= 1) {
+            const uint32_t cu = __shfl_up(ci, o, 64), tu = __shfl_up(ti, o, 64);
+            if (lane >= o) {
+                ci += cu;
+                ti += tu;
+            }
+        }
+        uint32_t off = ci - cs, toff = ti - ts;
+#pragma unroll
+        for (uint32_t k = 0; k < 4; k++) {
+            const uint32_t e = 4 * lane + k;
+            if (e <= E) goff[e] = off;  // goff[E] = total
+            cur[e] = off;
+            tb[e] = toff;
+            off += c4[k];
+            toff += t4[k];
+        }
+        if (lane == 63) *ntile = ti;
     }
     __syncthreads();
+    for (uint32_t e = threadIdx.x; e < E; e += 1024)
+        for (uint32_t m = 0, t = tb[e]; m < cnt[e]; m += kGM, t++) {
+            te[t] = e;
+            tm[t] = m;
+        }
     for (uint32_t a = threadIdx.x; a < n; a += 1024) {
         if (ids[a] >= E) continue;
         const uint32_t p = atomicAdd(&cur[ids[a]], 1u);

@@ -181,7 +181,9 @@ template <> struct Fmt<Q6_K> {
         const uint32_t rsc = ((r.s8.x >> sh) & 0xffu) | (((r.s8.y >> sh) & 0xffu) << 8);
         uint32_t j = c & 7, qa = (j & 3) >> 1;
         float sca = (float)(int8_t)(rsc & 0xffu), scb = (float)(int8_t)(rsc >> 8);
-        float d = h2f(r.d);
+        // opaque: the conversion stays here, after the caller's waits; hoisted
+        // next to the load it made the loading code wait for the load
+        float d = h2f(opaque(r.d));
         uint32_t l[4] = {r.ql.x, r.ql.y, r.ql.z, r.ql.w};
         uint32_t h[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
         float pa = 0.f, pb = 0.f;
