@@ -58,7 +58,7 @@ __global__ void k_pf_attn(const _Float16*, const _Float16*, const _Float16*, uin
                           uint32_t, uint32_t, _Float16*);
 __global__ void k_pf_kvh(const float*, const float*, uint32_t, uint32_t, uint32_t, uint32_t, _Float16*, _Float16*);
 __global__ void k_pf_router(const float*, DevMat, uint32_t, uint32_t, uint32_t, float*);
-__global__ void k_pf_topk(const float*, uint32_t, uint32_t, uint32_t, uint32_t*, float*, DevState*);
+__global__ void k_pf_topk(const float*, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t*, float*, DevState*);
 __global__ void k_pf_group(const uint32_t*, uint32_t, uint32_t, uint32_t, uint32_t*, uint32_t*, uint32_t*, uint32_t*,
                            uint32_t*, uint32_t*);
 __global__ void k_pf_combine(float*, const float*, const float*, uint32_t, uint32_t);
@@ -844,6 +844,9 @@ std::string prefill_gap(const qh_ctx* c) {
     return "";
 }
 
+// column splits of the prefill router logits (partial sums added in order)
+constexpr uint32_t kPfRouterSplit = 4;
+
 void prefill_alloc(qh_ctx* c, uint32_t cap) {
     auto& P = c->pf;
     if (P.cap >= cap) return;
@@ -857,7 +860,7 @@ void prefill_alloc(qh_ctx* c, uint32_t cap) {
         void** dst;
     } regs[] = {
         {cap * H * 4, (void**)&P.X},           {cap * H * 4, (void**)&P.Xn32},
-        {cap * (qd + 2 * kvd) * 4, (void**)&P.QKV}, {(uint64_t)cap * d.experts * 4, (void**)&P.LR},
+        {cap * (qd + 2 * kvd) * 4, (void**)&P.QKV}, {(uint64_t)cap * d.experts * 4 * kPfRouterSplit, (void**)&P.LR},
         {n_asg * 4, (void**)&P.wts},           {n_asg * H * 4, (void**)&P.Y},
         {cap * H * 2, (void**)&P.Xn16},        {(uint64_t)d.heads * cap * 128 * 2, (void**)&P.Q16},
         {cap * qd * 2, (void**)&P.O16},        {n_asg * d.ff * 2, (void**)&P.Hs},
@@ -981,10 +984,10 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
                        d.heads / d.kvheads, d.ctx, vp, qd, P.O16);
     pf_dense(c, P.wo16[l], H, qd, P.O16, S, P.X, true);  // residual add (model.rs:246-248)
     hipLaunchKernelGGL(k_pf_norm, dim3(S), dim3(kBlock), 0, c->s, P.X, L.ffn_norm, H, d.eps, P.Xn16, P.Xn32);
-    hipLaunchKernelGGL(k_pf_router, dim3((S + 15) / 16), dim3(kBlock), 0, c->s, P.Xn32, L.router, S, H, d.experts,
-                       P.LR);
-    hipLaunchKernelGGL(k_pf_topk, dim3((S + kWaves - 1) / kWaves), dim3(kBlock), 0, c->s, P.LR, S, d.experts, d.top,
-                       P.ids, P.wts, c->acts.st);
+    hipLaunchKernelGGL(k_pf_router, dim3((S + 15) / 16, kPfRouterSplit), dim3(kBlock), 0, c->s, P.Xn32, L.router,
+                       S, H, d.experts, P.LR);
+    hipLaunchKernelGGL(k_pf_topk, dim3((S + kWaves - 1) / kWaves), dim3(kBlock), 0, c->s, P.LR, kPfRouterSplit, S,
+                       d.experts, d.top, P.ids, P.wts, c->acts.st);
     hipLaunchKernelGGL(k_pf_group, dim3(1), dim3(1024), 0, c->s, P.ids, S * d.top, d.top, d.experts, P.goff, P.tok,
                        P.asg, P.te, P.tm, P.ntile);
     const ExpertTiles T{P.goff, P.tok, P.asg, P.te, P.tm, P.ntile};

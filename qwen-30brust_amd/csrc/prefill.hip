@@ -376,7 +376,10 @@ __global__ __launch_bounds__(kBlock) void k_pf_qkrope(const float* QKV, const fl
 // (v_mfma_f32_16x16x4_f32: fp32 operands and accumulation): 16 tokens per
 // workgroup, wave w takes experts [32 w, 32 w + 32) (E <= 128); 64-column
 // slices of x and of the F32 router rows are staged in LDS, the next slice's
-// loads issued before the current slice's MFMAs.
+// loads issued before the current slice's MFMAs.  The columns are split over
+// gridDim.y workgroups (split ks writes its partial sums to LR + ks S E;
+// k_pf_topk adds them in split order): a slice is too little work to cover
+// its load latency, so more workgroups per CU take turns.
 __global__ __launch_bounds__(kBlock) void k_pf_router(const float* Xn, DevMat R, uint32_t S, uint32_t H, uint32_t E,
                                                       float* LR) {
     constexpr uint32_t kP = 65;  // LDS pitch (floats)
@@ -395,8 +398,11 @@ __global__ __launch_bounds__(kBlock) void k_pf_router(const float* Xn, DevMat R,
         }
     };
     f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
-    gload(0);
-    for (uint32_t k0 = 0; k0 < H; k0 += 64) {
+    const uint32_t nsl = H / 64, per = (nsl + gridDim.y - 1) / gridDim.y;
+    const uint32_t kb = min(blockIdx.y * per, nsl) * 64, ke = min((blockIdx.y + 1) * per, nsl) * 64;
+    LR += (size_t)blockIdx.y * S * E;
+    if (kb < ke) gload(kb);
+    for (uint32_t k0 = kb; k0 < ke; k0 += 64) {
         {
             const uint32_t tt = tid >> 4, kk = 4 * (tid & 15);
             float* xd = xs + tt * kP + kk;
@@ -415,7 +421,7 @@ __global__ __launch_bounds__(kBlock) void k_pf_router(const float* Xn, DevMat R,
             }
         }
         __syncthreads();
-        if (k0 + 64 < H) gload(k0 + 64);
+        if (k0 + 64 < ke) gload(k0 + 64);
 #pragma unroll 4
         for (uint32_t kk = 0; kk < 64; kk += 4) {
             const float av = xs[col * kP + kk + grp];
@@ -437,13 +443,18 @@ __global__ __launch_bounds__(kBlock) void k_pf_router(const float* Xn, DevMat R,
 
 // Top-k routing of one token per wave (ops.rs:45-56): the k largest logits
 // under the total order, lower index on ties; softmax over the chosen logits
-// in rank order (ops.rs:29-44).  E <= 128.
-__global__ __launch_bounds__(kBlock) void k_pf_topk(const float* LR, uint32_t S, uint32_t E, uint32_t top,
-                                                    uint32_t* ids, float* wts, DevState* st) {
+// in rank order (ops.rs:29-44).  E <= 128.  The logits are the sum of the
+// router's nks partial sums, added in split order.
+__global__ __launch_bounds__(kBlock) void k_pf_topk(const float* LR, uint32_t nks, uint32_t S, uint32_t E,
+                                                    uint32_t top, uint32_t* ids, float* wts, DevState* st) {
     const uint32_t lane = threadIdx.x & 63, t = blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (t >= S) return;  // wave-uniform
-    const float* lg = LR + (size_t)t * E;
-    const float v0 = lane < E ? lg[lane] : 0.f, v1 = lane + 64 < E ? lg[lane + 64] : 0.f;
+    float v0 = lane < E ? LR[(size_t)t * E + lane] : 0.f, v1 = lane + 64 < E ? LR[(size_t)t * E + lane + 64] : 0.f;
+    for (uint32_t ks = 1; ks < nks; ks++) {
+        const float* lg = LR + ((size_t)ks * S + t) * E;
+        v0 += lane < E ? lg[lane] : 0.f;
+        v1 += lane + 64 < E ? lg[lane + 64] : 0.f;
+    }
     const bool bad = (lane < E && !finite_f(v0)) || (lane + 64 < E && !finite_f(v1));
     if (__any(bad)) {
         if (lane == 0) atomicOr(&st->err, kErrRouter);
@@ -460,9 +471,10 @@ __global__ __launch_bounds__(kBlock) void k_pf_topk(const float* LR, uint32_t S,
         wave_best(bk, bi);
         if (bi == lane) u0 = true;
         if (bi == lane + 64) u1 = true;
+        const float w0 = __shfl(v0, bi & 63, 64), w1 = __shfl(v1, bi & 63, 64);
         if (lane == k) {
             sid = bi;
-            sel = lg[bi];
+            sel = bi < 64 ? w0 : w1;
         }
     }
     // softmax in rank order, sequential like ops.rs
