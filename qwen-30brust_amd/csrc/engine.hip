@@ -61,7 +61,7 @@ __global__ void k_pf_router(const float*, DevMat, uint32_t, uint32_t, uint32_t, 
 __global__ void k_pf_topk(const float*, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t*, float*, DevState*);
 __global__ void k_pf_group(const uint32_t*, uint32_t, uint32_t, uint32_t, uint32_t*, uint32_t*, uint32_t*, uint32_t*,
                            uint32_t*, uint32_t*);
-__global__ void k_pf_combine(float*, const float*, const float*, uint32_t, uint32_t);
+__global__ void k_pf_combine(float*, const float*, const float*, uint32_t, uint32_t, const float*, float, _Float16*);
 }  // namespace qh
 
 using namespace qh;
@@ -970,8 +970,9 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
     const ModelDims& d = c->dm;
     const LayerW& L = c->layers[l];
     const uint32_t H = d.hidden, qd = d.heads * 128, kvd = d.kvheads * 128, row = qd + 2 * kvd;
-    hipLaunchKernelGGL(k_pf_norm, dim3(S), dim3(kBlock), 0, c->s, P.X, L.attn_norm, H, d.eps, P.Xn16,
-                       (float*)nullptr);
+    if (l == 0)  // later layers: written by the previous layer's combine
+        hipLaunchKernelGGL(k_pf_norm, dim3(S), dim3(kBlock), 0, c->s, P.X, L.attn_norm, H, d.eps, P.Xn16,
+                           (float*)nullptr);
     // q | k | v as one library GEMM over the fp16 copy of the three matrices
     pf_dense(c, P.wqkv16[l], row, H, P.Xn16, S, P.QKV, false);
     const uint32_t vp = (d.ctx + 63) / 64 * 64;  // row pitch of the transposed V copy
@@ -1000,7 +1001,10 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
         hipLaunchKernelGGL(k_gemm_down<decltype(K)::value>, dim3((H + 127) / 128, tiles), dim3(256), 0, c->s, P.Hs, T,
                            L.down, P.Y);
     });
-    hipLaunchKernelGGL(k_pf_combine, dim3(S), dim3(kBlock), 0, c->s, P.X, P.Y, P.wts, H, d.top);
+    // + the next layer's attention RMSNorm (fp16 operand of its q|k|v GEMM)
+    const float* next_norm = l + 1 < c->layers.size() ? c->layers[l + 1].attn_norm : nullptr;
+    hipLaunchKernelGGL(k_pf_combine, dim3(S), dim3(kBlock), 0, c->s, P.X, P.Y, P.wts, H, d.top, next_norm, d.eps,
+                       P.Xn16);
 }
 
 double now_ms() {

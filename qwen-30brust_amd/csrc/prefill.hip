@@ -552,16 +552,28 @@ __global__ __launch_bounds__(1024) void k_pf_group(const uint32_t* ids, uint32_t
 }
 
 // MoE combine + residual (model.rs:281-287): moe = sum_k w_k down_k in rank
-// order, then x += moe.
+// order, then x += moe.  With nw (the next layer's attention RMSNorm
+// weights) the block also writes that norm's fp16 output (k_pf_norm's
+// arithmetic, in the same order), so the next layer starts on its GEMM.
 __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y, const float* wts, uint32_t H,
-                                                       uint32_t top) {
+                                                       uint32_t top, const float* nw, float eps, _Float16* Xn16) {
+    __shared__ float red[kWaves];
     const size_t t = blockIdx.x;
+    float ss = 0.f;
     for (uint32_t i = threadIdx.x; i < H; i += kBlock) {
-#pragma clang fp contract(off)
         float moe = 0.f;
-        for (uint32_t k = 0; k < top; k++) moe += wts[t * top + k] * Y[(t * top + k) * H + i];
-        X[t * H + i] += moe;
+        {
+#pragma clang fp contract(off)
+            for (uint32_t k = 0; k < top; k++) moe += wts[t * top + k] * Y[(t * top + k) * H + i];
+        }
+        const float xv = X[t * H + i] + moe;
+        X[t * H + i] = xv;
+        ss = fmaf(xv, xv, ss);
     }
+    if (!nw) return;  // uniform
+    const float scale = 1.0f / sqrtf(block_sum(ss, red) / (float)H + eps);
+    for (uint32_t i = threadIdx.x; i < H; i += kBlock)  // this thread's own x values
+        Xn16[t * H + i] = (_Float16)(X[t * H + i] * (scale * nw[i]));
 }
 
 // ----------------------------------------------------------- attention --
