@@ -191,9 +191,17 @@ __device__ __forceinline__ void poll_words(const DecodeArgs& A, const uint64_t* 
     }
 }
 
-// dst[i] = value of src[i] for i < n, every word awaited with `tag` (src is
-// 16-byte aligned with room for an even number of words).  Ends with a
-// barrier; false when the step was aborted.
+// LDS layout of the gathered activation vectors: element i at px(i) =
+// i + 4 (i / 64).  The lanes of one read take the 16-float runs of
+// neighbouring chunks of a Q4_K/Q6_K row, 16-64 floats apart; unpadded, four
+// of every eight lanes of a 16-byte read met in the same banks.  A run never
+// crosses a 64-float block, so it stays contiguous.
+__device__ __forceinline__ uint32_t px(uint32_t i) { return i + ((i >> 6) << 2); }
+
+// dst[i] (dst[px(i)] with PAD) = value of src[i] for i < n, every word
+// awaited with `tag` (src is 16-byte aligned with room for an even number of
+// words).  Ends with a barrier; false when the step was aborted.
+template <bool PAD = false>
 __device__ __forceinline__ bool gather(const DecodeArgs& A, DecodeLds& S, const uint64_t* src, uint32_t n,
                                        uint32_t tag, float* dst, uint32_t tid) {
     const uint32_t np = (n + 1) / 2;
@@ -213,9 +221,9 @@ __device__ __forceinline__ bool gather(const DecodeArgs& A, DecodeLds& S, const 
         if (ab) break;
 #pragma unroll
         for (uint32_t k = 0; k < kGatherPairs; k++) {
-            const uint32_t p = p0 + k * kDT;
-            if (p < np) dst[2 * p] = v[2 * k];
-            if (2 * p + 1 < n) dst[2 * p + 1] = v[2 * k + 1];
+            const uint32_t p = p0 + k * kDT, d = PAD ? px(2 * p) : 2 * p;  // a pair stays adjacent
+            if (p < np) dst[d] = v[2 * k];
+            if (2 * p + 1 < n) dst[d + 1] = v[2 * k + 1];
         }
     }
     if (ab) S.abort = 1;
@@ -223,7 +231,7 @@ __device__ __forceinline__ bool gather(const DecodeArgs& A, DecodeLds& S, const 
     return S.abort == 0;
 }
 
-// gather() preceded by a cheap readiness check: wave 0 polls ns <= 256
+// gather<true>() (padded layout) preceded by a cheap readiness check: wave 0 polls ns <= 256
 // sample words src[first + j * stride] (one per producer block, each block
 // written by one store instruction) until three quarters of the producers
 // have written, and only then does the workgroup read all n words (gather()
@@ -260,7 +268,7 @@ __device__ __forceinline__ bool gather_s(const DecodeArgs& A, DecodeLds& S, cons
     }
     __syncthreads();
     if (S.abort) return false;
-    return gather(A, S, src, n, tag, dst, tid);
+    return gather<true>(A, S, src, n, tag, dst, tid);
 }
 
 __device__ __forceinline__ float dsum(float v, float* red) {
@@ -294,17 +302,39 @@ __device__ __forceinline__ float2 dsum2(float u, float v, float* red) {
 
 __device__ __forceinline__ float sumsq4(float4 v) { return fmaf(v.w, v.w, fmaf(v.z, v.z, fmaf(v.y, v.y, v.x * v.x))); }
 
-// RMSNorm (ops.rs:3-15) of the raw x in LDS xs[0..H), in place, with weights
-// w (this thread's float4); returns this thread's raw float4.  H <= 2048.
+// x_runs (the two 16-float runs of chunk c and their sums) of the vector
+// that starts at element `base` of a padded LDS vector.
+template <uint32_t KIND>
+__device__ __forceinline__ void x_runs_p(const float* xs, uint32_t base, uint32_t c, float* xa, float* xb, float& sa,
+                                         float& sb) {
+    const uint32_t fa = base + Fmt<KIND>::xoff_a(c), fb = base + Fmt<KIND>::xoff_b(c);
+    const float4* pa = reinterpret_cast<const float4*>(xs + px(fa));
+    const float4* pb = reinterpret_cast<const float4*>(xs + px(fb));
+    sa = 0.f;
+    sb = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float4 a = pa[k], b = pb[k];
+        xa[4 * k] = a.x; xa[4 * k + 1] = a.y; xa[4 * k + 2] = a.z; xa[4 * k + 3] = a.w;
+        xb[4 * k] = b.x; xb[4 * k + 1] = b.y; xb[4 * k + 2] = b.z; xb[4 * k + 3] = b.w;
+        sa += (a.x + a.y) + (a.z + a.w);
+        sb += (b.x + b.y) + (b.z + b.w);
+    }
+}
+
+// RMSNorm (ops.rs:3-15) of the raw x in LDS (padded layout, elements
+// [0, H)), in place, with weights w (this thread's float4); returns this
+// thread's raw float4.  H <= 2048.
 __device__ __forceinline__ float4 norm_in_lds(const Ctx& c, float* xs, float4 w, float eps, float* red) {
     float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (4 * c.tid < c.H) xv = reinterpret_cast<const float4*>(xs)[c.tid];
+    float* x4 = xs + px(4 * c.tid);
+    if (4 * c.tid < c.H) xv = *reinterpret_cast<const float4*>(x4);
     const float scale = 1.0f / sqrtf(dsum(sumsq4(xv), red) / (float)c.H + eps);
     if (4 * c.tid < c.H) {
-        xs[4 * c.tid] = xv.x * (scale * w.x);
-        xs[4 * c.tid + 1] = xv.y * (scale * w.y);
-        xs[4 * c.tid + 2] = xv.z * (scale * w.z);
-        xs[4 * c.tid + 3] = xv.w * (scale * w.w);
+        x4[0] = xv.x * (scale * w.x);
+        x4[1] = xv.y * (scale * w.y);
+        x4[2] = xv.z * (scale * w.z);
+        x4[3] = xv.w * (scale * w.w);
     }
     __syncthreads();
     return xv;
@@ -321,15 +351,16 @@ __device__ __forceinline__ bool router_wg(const DecodeArgs& A, const Ctx& c, uin
 __device__ __forceinline__ float4 norm_in_lds_dot(const Ctx& c, float* xs, float4 w, float eps, float* red,
                                                   float4 rw, float& rdot) {
     float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (4 * c.tid < c.H) xv = reinterpret_cast<const float4*>(xs)[c.tid];
+    float* x4 = xs + px(4 * c.tid);
+    if (4 * c.tid < c.H) xv = *reinterpret_cast<const float4*>(x4);
     const float dt = fmaf(rw.w, xv.w, fmaf(rw.z, xv.z, fmaf(rw.y, xv.y, rw.x * xv.x)));
     const float2 r = dsum2(sumsq4(xv), dt, red);
     const float scale = 1.0f / sqrtf(r.x / (float)c.H + eps);
     if (4 * c.tid < c.H) {
-        xs[4 * c.tid] = xv.x * (scale * w.x);
-        xs[4 * c.tid + 1] = xv.y * (scale * w.y);
-        xs[4 * c.tid + 2] = xv.z * (scale * w.z);
-        xs[4 * c.tid + 3] = xv.w * (scale * w.w);
+        x4[0] = xv.x * (scale * w.x);
+        x4[1] = xv.y * (scale * w.y);
+        x4[2] = xv.z * (scale * w.z);
+        x4[3] = xv.w * (scale * w.w);
     }
     __syncthreads();
     rdot = r.y;
@@ -483,7 +514,8 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
     QH_MARK(0, 0);
     if (l == A.l0) {
         // x as the embedding kernel (or the host) left it before this launch
-        if (4 * c.tid < c.H) reinterpret_cast<float4*>(xs)[c.tid] = ld_sys4(buf_rsrc(A.a.x, c.H * 4), c.tid * 16);
+        if (4 * c.tid < c.H)
+            *reinterpret_cast<float4*>(xs + px(4 * c.tid)) = ld_sys4(buf_rsrc(A.a.x, c.H * 4), c.tid * 16);
         __syncthreads();
     } else if (!gather_s(A, S, A.tx2, c.H, ptag(A, l - 1, 6), xs, c.tid, c.nwg, 0, c.rpw)) {
         return false;  // x'' of the previous layer (phase F)
@@ -504,7 +536,7 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
     }
     const uint32_t tag = ptag(A, l, 1);
     float xa[16], xb[16], sa, sb;
-    if (c.lane < cpr) x_runs<KQ>(xs, c.lane, xa, xb, sa, sb);
+    if (c.lane < cpr) x_runs_p<KQ>(xs, 0, c.lane, xa, xb, sa, sb);
 #pragma unroll
     for (uint32_t k = 0; k < kQkvPerWave; k++) {
         const uint32_t j = c.wv + kDW * k;
@@ -516,7 +548,7 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
                     acc = Fmt<KQ>::dot(wq[k], c.lane, xa, xb, sa, sb);
                 } else {
                     float ya[16], yb[16], ta, tb;
-                    x_runs<KV>(xs, c.lane, ya, yb, ta, tb);
+                    x_runs_p<KV>(xs, 0, c.lane, ya, yb, ta, tb);
                     acc = Fmt<KV>::dot(wvv[k], c.lane, ya, yb, ta, tb);
                 }
             }
@@ -805,11 +837,11 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
         float acc = 0.f;
         float xa[16], xb[16], sa, sb;
         if (c.lane < ocpr) {
-            x_runs<KO>(xs, c.lane, xa, xb, sa, sb);
+            x_runs_p<KO>(xs, 0, c.lane, xa, xb, sa, sb);
             acc = Fmt<KO>::dot(w0, c.lane, xa, xb, sa, sb);
         }
         if (c.lane + 64 < ocpr) {
-            x_runs<KO>(xs, c.lane + 64, xa, xb, sa, sb);
+            x_runs_p<KO>(xs, 0, c.lane + 64, xa, xb, sa, sb);
             acc += Fmt<KO>::dot(w1, c.lane + 64, xa, xb, sa, sb);
         }
         acc = wave_sum(acc);
@@ -818,8 +850,8 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
     if (rt) {  // workgroup-uniform
         float fd = 0.f;
         if (8 * c.tid < c.qd) {
-            const float4 a0 = reinterpret_cast<const float4*>(xs)[2 * c.tid];
-            const float4 a1 = reinterpret_cast<const float4*>(xs)[2 * c.tid + 1];
+            const float4 a0 = *reinterpret_cast<const float4*>(xs + px(8 * c.tid));
+            const float4 a1 = *reinterpret_cast<const float4*>(xs + px(8 * c.tid + 4));
             fd = fmaf(f0.w, a0.w, fmaf(f0.z, a0.z, fmaf(f0.y, a0.y, f0.x * a0.x)));
             fd = fmaf(f1.w, a1.w, fmaf(f1.z, a1.z, fmaf(f1.y, a1.y, fmaf(f1.x, a1.x, fd))));
         }
@@ -855,16 +887,17 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
     if (!gather_s(A, S, A.tx1, H + E, ptag(A, l, 3), xs, c.tid, c.nwg, 0, c.rpw))
         return false;  // x' and u (phase C)
     float4 x1 = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (4 * c.tid < H) x1 = reinterpret_cast<const float4*>(xs)[c.tid];
+    float* x4 = xs + px(4 * c.tid);
+    if (4 * c.tid < H) x1 = *reinterpret_cast<const float4*>(x4);
     const float s = 1.0f / sqrtf(dsum(sumsq4(x1), S.red) / (float)H + A.dm.eps);
-    if (c.tid < E) S.lg[c.tid] = s * xs[H + c.tid];  // router logits (model.rs:249-256)
+    if (c.tid < E) S.lg[c.tid] = s * xs[px(H + c.tid)];  // router logits (model.rs:249-256)
     // xn = x' * (s * ffn_norm), in place (each thread rewrites its own float4;
     // the routing barriers below order it before the dots)
     if (4 * c.tid < H) {
-        xs[4 * c.tid] = x1.x * (s * fn.x);
-        xs[4 * c.tid + 1] = x1.y * (s * fn.y);
-        xs[4 * c.tid + 2] = x1.z * (s * fn.z);
-        xs[4 * c.tid + 3] = x1.w * (s * fn.w);
+        x4[0] = x1.x * (s * fn.x);
+        x4[1] = x1.y * (s * fn.y);
+        x4[2] = x1.z * (s * fn.z);
+        x4[3] = x1.w * (s * fn.w);
     }
     QH_MARK(4, 1);
     // top-k by rank under the total order, lower index on ties (ops.rs:45-56;
@@ -929,7 +962,7 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
     const uint32_t tag_h = ptag(A, l, 5);
     {
         float xa[16], xb[16], sa, sb;
-        if (c.lane < cpr) x_runs<KG>(xs, c.lane, xa, xb, sa, sb);
+        if (c.lane < cpr) x_runs_p<KG>(xs, 0, c.lane, xa, xb, sa, sb);
 #pragma unroll
         for (uint32_t k = 0; k < kPairsPerWave; k++) {
             const uint32_t pr = c.gw * kPairsPerWave + k;
@@ -984,7 +1017,7 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
             if (u < U) {
                 const uint32_t sl = u / dcpr, chn = u % dcpr;
                 float xa[16], xb[16], sa, sb;
-                x_runs<KD>(xs + sl * ff, chn, xa, xb, sa, sb);
+                x_runs_p<KD>(xs, sl * ff, chn, xa, xb, sa, sb);
                 acc = fmaf(S.wts[sl], Fmt<KD>::dot(wd[i], chn, xa, xb, sa, sb), acc);
             }
         }
@@ -1042,7 +1075,7 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
     QH_MARK(6, 1);
     norm_in_lds(c, xs, on, A.dm.eps, S.red);
     float xa[16], xb[16], sa, sb;
-    if (c.lane < cpr) x_runs<KV>(xs, c.lane, xa, xb, sa, sb);
+    if (c.lane < cpr) x_runs_p<KV>(xs, 0, c.lane, xa, xb, sa, sb);
     int32_t bk = INT32_MIN;
     uint32_t bi = 0xffffffffu;
     bool nf = false;
@@ -1087,7 +1120,7 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
     QH_MARK(6, 4);
     if (c.b != 0) return;
     // workgroup 0: argmax over every workgroup's partial
-    float* fin = S.big + 2048;
+    float* fin = S.big + 4096;  // clear of the padded x (px(2047) = 2171)
     if (!gather(A, S, A.tfin, 2 * c.nwg, tag, fin, c.tid)) return;
     QH_MARK(6, 5);
     int32_t k1 = INT32_MIN;
