@@ -812,13 +812,12 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
                                             uint32_t l) {
     const Ctx c = fresh(c0);
     const uint32_t ocpr = c.qd / 32;
-    typename Fmt<KO>::Raw w0, w1;
+    // chunks lane and lane + 64 of the row, loaded unconditionally (row and
+    // chunks clamped, results of clamped ones dropped)
     const bool rowok = c.wv < c.nr;
-    const uint8_t* orow = L.o.w + (size_t)(c.r0 + c.wv) * L.o.drb;
-    if (rowok) {
-        if (c.lane < ocpr) w0 = Fmt<KO>::load(orow, L.o.geo, c.lane);
-        if (c.lane + 64 < ocpr) w1 = Fmt<KO>::load(orow, L.o.geo, c.lane + 64);
-    }
+    const uint8_t* orow = L.o.w + (size_t)min(c.r0 + c.wv, c.H - 1) * L.o.drb;
+    const uint32_t ch0 = min(c.lane, ocpr - 1), ch1 = min(c.lane + 64, ocpr - 1);
+    const typename Fmt<KO>::Raw w0 = Fmt<KO>::load(orow, L.o.geo, ch0), w1 = Fmt<KO>::load(orow, L.o.geo, ch1);
     // router workgroup e: row e of the fold, elements 8 tid .. 8 tid + 7
     uint32_t re;
     const bool rt = router_wg(A, c, re);
@@ -834,16 +833,13 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
         return false;  // attention output (phase B)
     QH_MARK(2, 1);
     if (rowok) {  // wave-uniform
-        float acc = 0.f;
-        float xa[16], xb[16], sa, sb;
-        if (c.lane < ocpr) {
-            x_runs_p<KO>(xs, 0, c.lane, xa, xb, sa, sb);
-            acc = Fmt<KO>::dot(w0, c.lane, xa, xb, sa, sb);
-        }
-        if (c.lane + 64 < ocpr) {
-            x_runs_p<KO>(xs, 0, c.lane + 64, xa, xb, sa, sb);
-            acc += Fmt<KO>::dot(w1, c.lane + 64, xa, xb, sa, sb);
-        }
+        // both chunks' x runs read before either dot (no branch between them)
+        float xa[16], xb[16], sa, sb, ya[16], yb[16], ta, tb;
+        x_runs_p<KO>(xs, 0, ch0, xa, xb, sa, sb);
+        x_runs_p<KO>(xs, 0, ch1, ya, yb, ta, tb);
+        const float d0 = Fmt<KO>::dot(w0, ch0, xa, xb, sa, sb), d1 = Fmt<KO>::dot(w1, ch1, ya, yb, ta, tb);
+        float acc = c.lane < ocpr ? d0 : 0.f;
+        if (c.lane + 64 < ocpr) acc += d1;
         acc = wave_sum(acc);
         if (c.lane == 0) S.xo[c.wv] += acc;  // residual (model.rs:246-248)
     }
@@ -1010,16 +1006,16 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         return false;  // SwiGLU outputs (phase E)
     QH_MARK(5, 1);
     if (c.wv < c.nr) {  // wave-uniform
+        // every unit computed (clamped ones dropped by the select), so that the
+        // x runs of all units are read without a branch between them
         float acc = 0.f;
 #pragma unroll
         for (uint32_t i = 0; i < kDownUnits; i++) {
-            const uint32_t u = c.lane + 64 * i;
-            if (u < U) {
-                const uint32_t sl = u / dcpr, chn = u % dcpr;
-                float xa[16], xb[16], sa, sb;
-                x_runs_p<KD>(xs, sl * ff, chn, xa, xb, sa, sb);
-                acc = fmaf(S.wts[sl], Fmt<KD>::dot(wd[i], chn, xa, xb, sa, sb), acc);
-            }
+            const uint32_t u = min(c.lane + 64 * i, U - 1), sl = u / dcpr, chn = u % dcpr;
+            float xa[16], xb[16], sa, sb;
+            x_runs_p<KD>(xs, sl * ff, chn, xa, xb, sa, sb);
+            const float d = fmaf(S.wts[sl], Fmt<KD>::dot(wd[i], chn, xa, xb, sa, sb), acc);
+            acc = c.lane + 64 * i < U ? d : acc;
         }
         acc = wave_sum(acc);
         if (c.lane == 0) S.xo[c.wv] += acc;  // x += sum_s w_s down_s (model.rs:281-287)
