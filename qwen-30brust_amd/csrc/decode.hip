@@ -659,12 +659,14 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
         }
         // scores: thread (key kt, 16-dim part) holds its K slice in registers;
         // the 8 parts of each head reduce on DPP
+        // (heads past G read head G - 1 and are dropped: no branch between the
+        // q reads, so they are issued together)
         float mine = 0.f;
 #pragma unroll
         for (uint32_t h = 0; h < 8; h++) {
             float acc = 0.f;
-            if (h < G) {
-                const float4* q4 = reinterpret_cast<const float4*>(qs + h * 160 + part * 20);
+            {
+                const float4* q4 = reinterpret_cast<const float4*>(qs + min(h, G - 1) * 160 + part * 20);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const float4 q = q4[i];
