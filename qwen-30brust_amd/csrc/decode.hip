@@ -86,6 +86,7 @@ struct DecodeLds {
     uint32_t bi[kDW];
     uint32_t abort;
     uint32_t bad;
+    uint32_t vq;              // next vocab row group of this workgroup to hand out
 };
 
 // Per-workgroup constants of one launch.
@@ -1060,8 +1061,15 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
             t[k] = Fmt<KV>::load(mv.w + (size_t)r * mv.drb, mv.geo, ch);
         }
     };
+    // the workgroup's groups [g0, g1): the first kDW to its waves in turn, the
+    // rest to whichever wave asks first (LDS counter), so that a wave whose
+    // rows arrive late does not hold the workgroup's argmax partial back
+    const uint32_t per = (ngrp + c.nwg - 1) / c.nwg;
+    const uint32_t g0 = min(c.b * per, ngrp), g1 = min(g0 + per, ngrp);
+    if (c.tid == 0) S.vq = g0 + kDW;  // ordered before use by the gather's barriers
+    uint32_t gi = g0 + c.wv;
     Raw cur[kVocabRows], nxt[kVocabRows];
-    load_group(cur, c.gw);
+    load_group(cur, min(gi, ngrp - 1));
     // read now, used by workgroup 0 after the argmax hand-over
     const uint32_t n_given = a.st->n_given;
     float4 on = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1077,8 +1085,11 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
     int32_t bk = INT32_MIN;
     uint32_t bi = 0xffffffffu;
     bool nf = false;
-    for (uint32_t gi = c.gw; gi < ngrp; gi += c.NWV) {
-        load_group(nxt, min(gi + c.NWV, ngrp - 1));
+    while (gi < g1) {  // wave-uniform
+        uint32_t gn = 0;
+        if (c.lane == 0) gn = atomicAdd(&S.vq, 1u);
+        gn = __builtin_amdgcn_readfirstlane(gn);
+        load_group(nxt, min(gn, ngrp - 1));
         float acc[kVocabRows];
 #pragma unroll
         for (uint32_t k = 0; k < kVocabRows; k++) {
@@ -1098,6 +1109,7 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
         }
 #pragma unroll
         for (uint32_t k = 0; k < kVocabRows; k++) cur[k] = nxt[k];
+        gi = gn;
     }
     QH_MARK(6, 2);
     if (nf) S.bad = 1;
