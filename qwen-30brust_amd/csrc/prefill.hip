@@ -552,28 +552,69 @@ __global__ __launch_bounds__(1024) void k_pf_group(const uint32_t* ids, uint32_t
 }
 
 // MoE combine + residual (model.rs:281-287): moe = sum_k w_k down_k in rank
-// order, then x += moe.  With nw (the next layer's attention RMSNorm
-// weights) the block also writes that norm's fp16 output (k_pf_norm's
-// arithmetic, in the same order), so the next layer starts on its GEMM.
+// order, then x += moe; 4 consecutive elements per thread.  With nw (the
+// next layer's attention RMSNorm weights) the block also writes that norm's
+// fp16 output (k_pf_norm's arithmetic, with the sum of squares taken in this
+// kernel's element order), so the next layer starts on its GEMM.
 __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y, const float* wts, uint32_t H,
                                                        uint32_t top, const float* nw, float eps, _Float16* Xn16) {
     __shared__ float red[kWaves];
     const size_t t = blockIdx.x;
+    const uint32_t tk = min(top, 8u);  // ranks held in registers; more (top > 8) are read in a loop
+    float w[8];
+#pragma unroll
+    for (uint32_t k = 0; k < 8; k++) w[k] = wts[t * top + min(k, top - 1)];
     float ss = 0.f;
-    for (uint32_t i = threadIdx.x; i < H; i += kBlock) {
-        float moe = 0.f;
+    for (uint32_t i4 = threadIdx.x; 4 * i4 < H; i4 += kBlock) {  // H % 64 == 0
+        const size_t i = 4 * (size_t)i4;
+        // every rank's row requested before the sum (rows past top clamped,
+        // their values unused)
+        float4 y[8];
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++) y[k] = *reinterpret_cast<const float4*>(Y + (t * top + min(k, top - 1)) * H + i);
+        float4 xv = *reinterpret_cast<const float4*>(X + t * H + i);
+        float4 moe = make_float4(0.f, 0.f, 0.f, 0.f);
         {
 #pragma clang fp contract(off)
-            for (uint32_t k = 0; k < top; k++) moe += wts[t * top + k] * Y[(t * top + k) * H + i];
+#pragma unroll
+            for (uint32_t k = 0; k < 8; k++)
+                if (k < tk) {
+                    moe.x += w[k] * y[k].x;
+                    moe.y += w[k] * y[k].y;
+                    moe.z += w[k] * y[k].z;
+                    moe.w += w[k] * y[k].w;
+                }
+            for (uint32_t k = 8; k < top; k++) {
+                const float wk = wts[t * top + k];
+                const float4 yk = *reinterpret_cast<const float4*>(Y + (t * top + k) * H + i);
+                moe.x += wk * yk.x;
+                moe.y += wk * yk.y;
+                moe.z += wk * yk.z;
+                moe.w += wk * yk.w;
+            }
+            xv.x += moe.x;
+            xv.y += moe.y;
+            xv.z += moe.z;
+            xv.w += moe.w;
         }
-        const float xv = X[t * H + i] + moe;
-        X[t * H + i] = xv;
-        ss = fmaf(xv, xv, ss);
+        *reinterpret_cast<float4*>(X + t * H + i) = xv;
+        ss = fmaf(xv.x, xv.x, ss);
+        ss = fmaf(xv.y, xv.y, ss);
+        ss = fmaf(xv.z, xv.z, ss);
+        ss = fmaf(xv.w, xv.w, ss);
     }
     if (!nw) return;  // uniform
     const float scale = 1.0f / sqrtf(block_sum(ss, red) / (float)H + eps);
-    for (uint32_t i = threadIdx.x; i < H; i += kBlock)  // this thread's own x values
-        Xn16[t * H + i] = (_Float16)(X[t * H + i] * (scale * nw[i]));
+    for (uint32_t i4 = threadIdx.x; 4 * i4 < H; i4 += kBlock) {  // this thread's own x values
+        const size_t i = 4 * (size_t)i4;
+        const float4 xv = *reinterpret_cast<const float4*>(X + t * H + i);
+        const float4 w4 = *reinterpret_cast<const float4*>(nw + i);
+        _Float16* o = Xn16 + t * H + i;
+        o[0] = (_Float16)(xv.x * (scale * w4.x));
+        o[1] = (_Float16)(xv.y * (scale * w4.y));
+        o[2] = (_Float16)(xv.z * (scale * w4.z));
+        o[3] = (_Float16)(xv.w * (scale * w4.w));
+    }
 }
 
 // ----------------------------------------------------------- attention --
