@@ -324,8 +324,8 @@ __global__ __launch_bounds__(kBlock) void k_pf_norm(const float* X, const float*
 // (ops.rs:16-28), KV append (model.rs:241-243).  Row t of QKV is
 // [q (heads*128) | k (kvheads*128) | v (kvheads*128)].  Q goes to
 // Q16[head][t][128] (fp16), K and V to the fp32 cache [kvhead][ctx][128].
-// Wave w takes head slots w, w + 4, ...: 0..heads-1 q, then k, then v; lane
-// l holds elements l and l + 64, the rotated pair.
+// Wave w takes head slots w, w + kWaves, ...: 0..heads-1 q, then k, then v;
+// lane l holds elements l and l + 64, the rotated pair.
 __global__ __launch_bounds__(kBlock) void k_pf_qkrope(const float* QKV, const float* qn, const float* kn,
                                                       const float2* rope, uint32_t p0, uint32_t S, uint32_t heads,
                                                       uint32_t kvheads, uint32_t ctx, float eps, _Float16* Q16,
@@ -335,39 +335,54 @@ __global__ __launch_bounds__(kBlock) void k_pf_qkrope(const float* QKV, const fl
     const uint32_t row = (heads + 2 * kvheads) * 128;
     const float* x = QKV + (size_t)t * row;
     const float2 cs = rope[(size_t)pos * 64 + lane];
-    for (uint32_t slot = w; slot < heads + 2 * kvheads; slot += kWaves) {  // wave-uniform
-        const float xa = x[slot * 128 + lane], xb = x[slot * 128 + lane + 64];
-        if (slot >= heads + kvheads) {
-            const uint32_t g = slot - heads - kvheads;
-            float* dst = vcache + ((size_t)g * ctx + pos) * 128;
-            dst[lane] = xa;
-            dst[lane + 64] = xb;
-            Vth[((size_t)g * 128 + lane) * vp + pos] = (_Float16)xa;
-            Vth[((size_t)g * 128 + lane + 64) * vp + pos] = (_Float16)xb;
-            continue;
+    const uint32_t nslot = heads + 2 * kvheads;
+    const float qw0 = qn[lane], qw1 = qn[lane + 64], kw0 = kn[lane], kw1 = kn[lane + 64];
+    constexpr uint32_t kSW = 5;  // slots per wave per round, their loads issued together
+    for (uint32_t s0 = w; s0 < nslot; s0 += kSW * kWaves) {  // wave-uniform
+        float xa_[kSW], xb_[kSW];
+#pragma unroll
+        for (uint32_t j = 0; j < kSW; j++) {
+            const uint32_t sl = min(s0 + j * kWaves, nslot - 1);
+            xa_[j] = x[sl * 128 + lane];
+            xb_[j] = x[sl * 128 + lane + 64];
         }
-        const bool isq = slot < heads;
-        const float* nw = isq ? qn : kn;
-        const float ssq = wave_sum(fmaf(xb, xb, xa * xa));
-        const float sc = 1.0f / sqrtf(ssq / 128.0f + eps);
-        const float y0 = xa * (sc * nw[lane]), y1 = xb * (sc * nw[lane + 64]);
-        float o0, o1;
-        {
+#pragma unroll
+        for (uint32_t j = 0; j < kSW; j++) {
+            const uint32_t slot = s0 + j * kWaves;
+            if (slot >= nslot) break;
+            const float xa = xa_[j], xb = xb_[j];
+            if (slot >= heads + kvheads) {
+                const uint32_t g = slot - heads - kvheads;
+                float* dst = vcache + ((size_t)g * ctx + pos) * 128;
+                dst[lane] = xa;
+                dst[lane + 64] = xb;
+                Vth[((size_t)g * 128 + lane) * vp + pos] = (_Float16)xa;
+                Vth[((size_t)g * 128 + lane + 64) * vp + pos] = (_Float16)xb;
+                continue;
+            }
+            const bool isq = slot < heads;
+            const float w0 = isq ? qw0 : kw0, w1 = isq ? qw1 : kw1;
+            const float ssq = wave_sum(fmaf(xb, xb, xa * xa));
+            const float sc = 1.0f / sqrtf(ssq / 128.0f + eps);
+            const float y0 = xa * (sc * w0), y1 = xb * (sc * w1);
+            float o0, o1;
+            {
 #pragma clang fp contract(off)
-            o0 = y0 * cs.x - y1 * cs.y;
-            o1 = y0 * cs.y + y1 * cs.x;
-        }
-        if (isq) {
-            _Float16* dst = Q16 + ((size_t)slot * S + t) * 128;
-            dst[lane] = (_Float16)o0;
-            dst[lane + 64] = (_Float16)o1;
-        } else {
-            float* dst = kcache + ((size_t)(slot - heads) * ctx + pos) * 128;
-            dst[lane] = o0;
-            dst[lane + 64] = o1;
-            _Float16* dh = Kh + ((size_t)(slot - heads) * ctx + pos) * 128;
-            dh[lane] = (_Float16)o0;
-            dh[lane + 64] = (_Float16)o1;
+                o0 = y0 * cs.x - y1 * cs.y;
+                o1 = y0 * cs.y + y1 * cs.x;
+            }
+            if (isq) {
+                _Float16* dst = Q16 + ((size_t)slot * S + t) * 128;
+                dst[lane] = (_Float16)o0;
+                dst[lane + 64] = (_Float16)o1;
+            } else {
+                float* dst = kcache + ((size_t)(slot - heads) * ctx + pos) * 128;
+                dst[lane] = o0;
+                dst[lane + 64] = o1;
+                _Float16* dh = Kh + ((size_t)(slot - heads) * ctx + pos) * 128;
+                dh[lane] = (_Float16)o0;
+                dh[lane + 64] = (_Float16)o1;
+            }
         }
     }
 }
