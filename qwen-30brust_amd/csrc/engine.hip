@@ -918,12 +918,51 @@ void pf_dense(qh_ctx* c, const _Float16* W16, uint32_t N, uint32_t K, const _Flo
         BLT_OK(hipblasLtMatmulPreferenceCreate(&pref));
         const uint64_t wsz = c->blt_ws.n;
         BLT_OK(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz, sizeof wsz));
-        hipblasLtMatmulHeuristicResult_t res{};
+        // the library's first candidates, each timed once on this shape (into a
+        // scratch output: an accumulating projection must not see the trials)
+        constexpr int kCand = 8;
+        hipblasLtMatmulHeuristicResult_t res[kCand] = {};
         int n = 0;
-        const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(c->blt, g.desc, g.la, g.lb, g.lc, g.lc, pref, 1, &res, &n);
+        const hipblasStatus_t st =
+            hipblasLtMatmulAlgoGetHeuristic(c->blt, g.desc, g.la, g.lb, g.lc, g.lc, pref, kCand, res, &n);
         (void)hipblasLtMatmulPreferenceDestroy(pref);
         if (st != HIPBLAS_STATUS_SUCCESS || n < 1) throw Error("no hipBLASLt algorithm for a prefill projection");
-        g.algo = res.algo;
+        int best = 0;
+        if (n > 1) {
+            DevBuf trial;
+            trial.alloc((size_t)N * S * 4);
+            HIP_OK(hipMemsetAsync(trial.p, 0, (size_t)N * S * 4, c->s));
+            hipEvent_t e0, e1;
+            HIP_OK(hipEventCreate(&e0));
+            HIP_OK(hipEventCreate(&e1));
+            const float one = 1.f, zero = 0.f;
+            const float* beta_t = accumulate ? &one : &zero;
+            float best_ms = 0.f;
+            bool found = false;
+            for (int i = 0; i < n; i++) {
+                if (res[i].state != HIPBLAS_STATUS_SUCCESS) continue;
+                auto run = [&] {
+                    return hipblasLtMatmul(c->blt, g.desc, &one, W16, g.la, X16, g.lb, beta_t, trial.p, g.lc, trial.p,
+                                           g.lc, &res[i].algo, c->blt_ws.p, c->blt_ws.n, c->s);
+                };
+                if (run() != HIPBLAS_STATUS_SUCCESS) continue;  // warm-up; a failing candidate is skipped
+                HIP_OK(hipEventRecord(e0, c->s));
+                for (int r = 0; r < 3; r++) (void)run();
+                HIP_OK(hipEventRecord(e1, c->s));
+                HIP_OK(hipEventSynchronize(e1));
+                float ms = 0.f;
+                HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+                if (!found || ms < best_ms) {
+                    best = i;
+                    best_ms = ms;
+                    found = true;
+                }
+            }
+            (void)hipEventDestroy(e0);
+            (void)hipEventDestroy(e1);
+            HIP_OK(hipStreamSynchronize(c->s));  // trials done before the scratch output is freed
+        }
+        g.algo = res[best].algo;
         it = c->plans.emplace(key, g).first;
     }
     const qh_ctx::GemmPlan& g = it->second;
