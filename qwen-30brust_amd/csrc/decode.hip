@@ -274,6 +274,8 @@ __device__ __forceinline__ bool gather_s(const DecodeArgs& A, DecodeLds& S, cons
     return gather<true>(A, S, src, n, tag, dst, tid);
 }
 
+// Block sum.  It ends without a barrier: every caller reaches another
+// barrier before anything writes red again.
 __device__ __forceinline__ float dsum(float v, float* red) {
     v = wave_sum(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
@@ -281,10 +283,9 @@ __device__ __forceinline__ float dsum(float v, float* red) {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < kDW; i++) s += red[i];
-    __syncthreads();
     return s;
 }
-// Two block sums in one round.
+// Two block sums in one round (the same rule for red).
 __device__ __forceinline__ float2 dsum2(float u, float v, float* red) {
     u = wave_sum(u);
     v = wave_sum(v);
@@ -299,7 +300,6 @@ __device__ __forceinline__ float2 dsum2(float u, float v, float* red) {
         su += red[i];
         sv += red[kDW + i];
     }
-    __syncthreads();
     return make_float2(su, sv);
 }
 
