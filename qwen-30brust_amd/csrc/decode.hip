@@ -91,7 +91,7 @@ struct DecodeLds {
 
 // Per-workgroup constants of one launch.
 struct Ctx {
-    uint32_t b, nwg, tid, wv, lane, gw, NWV;
+    uint32_t b, nwg, tid, wv, lane, gw;
     uint32_t pos, T, H, E, top, ff, G, qd, kvd, ctx;
     uint32_t r0, nr, rpw;  // this workgroup's rows of x: [r0, r0 + nr), rpw per workgroup
 };
@@ -1182,7 +1182,6 @@ __global__ __launch_bounds__(kDT) void k_decode(DecodeArgs A) {
     // wave-uniform: derived values stay in scalar registers
     c.wv = __builtin_amdgcn_readfirstlane(c.tid >> 6);
     c.gw = c.b * kDW + c.wv;
-    c.NWV = c.nwg * kDW;
     const ModelDims& dm = A.dm;
     if (c.tid == 0) {
         S.abort = 0;
