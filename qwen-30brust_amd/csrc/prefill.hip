@@ -310,13 +310,27 @@ __global__ __launch_bounds__(kBlock) void k_pf_norm(const float* X, const float*
     __shared__ float red[kWaves];
     const size_t t = blockIdx.x;
     const float* x = X + t * H;
+    // 4 consecutive elements per thread (H % 64 == 0), the sum of squares in
+    // the same element order as k_pf_combine's
     float ss = 0.f;
-    for (uint32_t i = threadIdx.x; i < H; i += kBlock) ss = fmaf(x[i], x[i], ss);
+    for (uint32_t i4 = threadIdx.x; 4 * i4 < H; i4 += kBlock) {
+        const float4 v = reinterpret_cast<const float4*>(x)[i4];
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+    }
     const float scale = 1.0f / sqrtf(block_sum(ss, red) / (float)H + eps);
-    for (uint32_t i = threadIdx.x; i < H; i += kBlock) {
-        const float v = x[i] * (scale * w[i]);
-        Y16[t * H + i] = (_Float16)v;
-        if (Y32) Y32[t * H + i] = v;
+    for (uint32_t i4 = threadIdx.x; 4 * i4 < H; i4 += kBlock) {
+        const float4 v = reinterpret_cast<const float4*>(x)[i4], w4 = reinterpret_cast<const float4*>(w)[i4];
+        const float4 y = make_float4(v.x * (scale * w4.x), v.y * (scale * w4.y), v.z * (scale * w4.z),
+                                     v.w * (scale * w4.w));
+        _Float16* o = Y16 + t * H + 4 * i4;
+        o[0] = (_Float16)y.x;
+        o[1] = (_Float16)y.y;
+        o[2] = (_Float16)y.z;
+        o[3] = (_Float16)y.w;
+        if (Y32) reinterpret_cast<float4*>(Y32 + t * H)[i4] = y;
     }
 }
 
