@@ -28,6 +28,7 @@ namespace qh {
 // Kernels (kernels.hip).
 __global__ void k_repack(const uint8_t*, uint8_t*, uint32_t, uint32_t, size_t, size_t, size_t);
 __global__ void k_dequant(DevMat, size_t, size_t, float*);
+__global__ void k_fill_u32(uint32_t*, size_t, uint32_t);
 __global__ void k_router_fold(DevMat, const float*, const float*, uint32_t, uint32_t, uint32_t, float*);
 template <int R> __global__ void k_matvec(DevMat, const float*, float*, int);
 __global__ void k_route(const float*, uint32_t, uint32_t, uint32_t*, float*, uint32_t*);
@@ -46,6 +47,7 @@ __global__ void k_finish(Acts, ModelDims, uint32_t);
 // Persistent token step (decode.hip).
 __global__ void k_embed(DevMat, Acts, ModelDims);
 __global__ void k_decode(DecodeArgs);
+__global__ void k_xcd_map(uint32_t*);
 // Batched prefill (prefill.hip).
 template <uint32_t K> __global__ void k_gemm_gateup(const _Float16*, uint32_t, ExpertTiles, DevMat, DevMat, _Float16*);
 template <uint32_t K> __global__ void k_gemm_down(const _Float16*, ExpertTiles, DevMat, float*);
@@ -525,32 +527,40 @@ void capture_graph(qh_ctx* c) {
     HIP_OK(hipGraphInstantiate(&c->exec, c->graph, nullptr, nullptr, 0));
 }
 
-// Whether k_decode covers this model: the Q4_K_M formats (q/k/o/gate/up
-// Q4_K; v/down/vocab Q4_K or Q6_K; F32 router) and the row splits of its
-// phases over one 512-thread workgroup per CU.
+// Whether k_decode covers this model: the Qwen3-30B-A3B shapes (hidden
+// 2048, 32 query / 4 KV heads of 128, 128 experts, top 8, expert FFN 768),
+// the Q4_K_M formats (q/k/o/gate/up Q4_K; v/down/vocab Q4_K or Q6_K; F32
+// router), and a device of 8 XCDs x 32 CUs running one 512-thread workgroup
+// per CU.
 bool persist_supported(const qh_ctx* c, uint32_t nwg) {
     const ModelDims& d = c->dm;
-    const uint32_t G = d.heads / d.kvheads, NWV = nwg * 8;
     auto km = [](uint32_t k) { return k == Q4_K || k == Q6_K; };
-    // attention workgroups are < kvheads * 32; the router workgroups follow them
-    if (!(d.head_dim == 128 && G >= 1 && G <= 8 && d.heads * 128 <= 4096 && d.kvheads * 32 + d.experts <= nwg))
-        return false;
-    // every workgroup owns rows of x: the tagged exchange relies on it
-    const uint32_t rpw = (d.hidden + nwg - 1) / nwg;
-    if (!(d.hidden % 256 == 0 && d.hidden <= 2048 && rpw <= 8 && (nwg - 1) * rpw < d.hidden)) return false;
-    if (!(d.experts <= 128 && d.experts + 1 <= nwg && d.top >= 1 && d.top <= 8)) return false;
-    if (!(d.ff % 256 == 0 && (uint64_t)d.top * d.ff <= 3ull * NWV && d.top * (d.ff / 32) <= 192 &&
-          d.top * pad32h(d.ff) <= 8192))
-        return false;
-    if (!km(c->out.kind) || c->out.cols != d.hidden || c->max_chunks > 32 || nwg > kMaxGrid || nwg > 512) return false;
+    if (nwg != kDecodeXcds * kDecodeWgPerXcd) return false;
+    if (!(d.hidden == 2048 && d.heads == 32 && d.kvheads == 4 && d.head_dim == 128)) return false;
+    if (!(d.experts >= 8 && d.experts <= 128 && d.top == kDecodeXcds && d.ff == 768)) return false;
+    if (!km(c->out.kind) || c->out.cols != d.hidden) return false;
     for (const LayerW& L : c->layers) {
         if (!(L.q.kind == Q4_K && L.k.kind == Q4_K && L.o.kind == Q4_K && L.gate.kind == Q4_K &&
               L.up.kind == Q4_K && km(L.v.kind) && km(L.down.kind) && L.router.kind == F32))
             return false;
-        // phase A: q|k and v row blocks of every workgroup fit its 24 slots
-        const uint64_t nqk = (uint64_t)L.q.rows + L.k.rows;
-        if ((nqk + nwg - 1) / nwg + (L.v.rows + nwg - 1) / nwg > 24) return false;
     }
+    return true;
+}
+
+// Whether workgroup b of a 256-workgroup launch runs on XCD b % 8 (read from
+// the hardware register by a probe kernel): the persistent step's exchanges
+// inside an XCD rely on it.
+bool xcd_placement_ok(qh_ctx* c, uint32_t nwg) {
+    DevBuf m;
+    m.alloc(nwg * 4);
+    uint32_t* out = m.as<uint32_t>();
+    void* args[] = {&out};
+    HIP_OK(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_xcd_map), dim3(nwg), dim3(512), args, 0, c->s));
+    std::vector<uint32_t> h(nwg);
+    HIP_OK(hipMemcpyAsync(h.data(), m.p, nwg * 4, hipMemcpyDeviceToHost, c->s));
+    HIP_OK(hipStreamSynchronize(c->s));
+    for (uint32_t b = 0; b < nwg; b++)
+        if (h[b] != b % kDecodeXcds) return false;
     return true;
 }
 
@@ -560,7 +570,7 @@ void setup_persist(qh_ctx* c) {
     int per_cu = 0;
     HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(k_decode), 512, 0));
     const uint32_t nwg = (uint32_t)p.multiProcessorCount;
-    c->persist_ok = per_cu >= 1 && persist_supported(c, nwg);
+    c->persist_ok = per_cu >= 1 && persist_supported(c, nwg) && xcd_placement_ok(c, nwg);
     const char* np = std::getenv("QH_NO_PERSIST");
     c->persist = c->persist_ok && !(np && np[0] == '1');
     if (!c->persist_ok) return;
@@ -594,24 +604,21 @@ void setup_persist(qh_ctx* c) {
     A.onorm = c->onorm;
     A.a = c->acts;
     A.dm = c->dm;
-    A.max_chunks = c->max_chunks;
-    // abort flag | tagged words of each exchange, every region 256-byte aligned
-    const uint64_t qd = (uint64_t)d.heads * 128, kvd = (uint64_t)d.kvheads * 128;
+    // abort flag | tagged words of each exchange; every region (and every
+    // XCD's part of it) starts on a 256-byte boundary, so no cache line is
+    // shared between XCDs
+    const uint64_t X = kDecodeXcds;
     struct Region {
         uint64_t words;
         uint64_t** dst;
     } regions[] = {
-        {(uint64_t)d.hidden + d.experts, &A.tx1},  // x' rows, then the unscaled router logits
-        {d.hidden, &A.tx2},
-        {qd + 2 * kvd, &A.tqkv},
-        {qd, &A.tatt},
-        {(uint64_t)d.heads * c->max_chunks * kPartWords, &A.tpart},
-        {(uint64_t)d.top * d.ff, &A.th},
-        {2ull * nwg, &A.tfin},
+        {X * kDecodeStrideQkv, &A.lqkv}, {X * kDecodeStridePart, &A.lpart}, {X * kDecodeStrideAtt, &A.latt},
+        {X * kDecodeStrideX1, &A.lx1},   {X * kDecodeStrideH, &A.lh},       {X * kDecodeStrideX2, &A.lx2},
+        {X * kDecodeStrideG1, &A.g1},    {X * kDecodeStrideG2, &A.g2},      {2ull * nwg, &A.tfin},
     };
     auto up256 = [](uint64_t b) { return (b + 255) / 256 * 256; };
     size_t total = 256;
-    for (const Region& r : regions) total += up256((r.words + 1) * 8);
+    for (const Region& r : regions) total += up256(r.words * 8);
     c->sync_buf.alloc(total);
     c->sync_bytes = total;
     HIP_OK(hipMemset(c->sync_buf.p, 0, total));
@@ -620,20 +627,27 @@ void setup_persist(qh_ctx* c) {
     q += 256;
     for (const Region& r : regions) {
         *r.dst = reinterpret_cast<uint64_t*>(q);
-        q += up256((r.words + 1) * 8);
+        q += up256(r.words * 8);
     }
     c->flag_base = 0;
+}
+
+// Clears n bytes (a multiple of 4) of device memory with a fill kernel.
+void clear_words(qh_ctx* c, void* p, size_t bytes) {
+    hipLaunchKernelGGL(k_fill_u32, dim3((uint32_t)std::min<size_t>((bytes / 4 + kBlock - 1) / kBlock, 4096)),
+                       dim3(kBlock), 0, c->s, static_cast<uint32_t*>(p), bytes / 4, 0u);
+    HIP_OK(hipGetLastError());
 }
 
 // One cooperative launch of k_decode over layers [l0, l1); vocab: also the
 // final norm, vocab projection, argmax and position advance.
 void launch_decode(qh_ctx* c, uint32_t l0, uint32_t l1, bool vocab) {
     if (!(l0 < l1 && l1 <= c->layers.size())) throw Error("decode launch needs a non-empty layer range");
-    const uint32_t phases = 6 * (l1 - l0) + (vocab ? 1 : 0);
+    const uint32_t phases = 8 * (l1 - l0) + (vocab ? 1 : 0);
     if (c->flag_base > 0xFFFFFFFFu - phases) {
         // tags would wrap: clear every tagged word (no launch is reading them:
         // this stream runs the launches in order) and start again from 0
-        HIP_OK(hipMemsetAsync(c->sync_buf.p, 0, c->sync_bytes, c->s));
+        clear_words(c, c->sync_buf.p, c->sync_bytes);
         c->flag_base = 0;
     }
     DecodeArgs A = c->dargs;
@@ -807,16 +821,20 @@ void reset_model(qh_ctx* c) {
 }
 
 [[noreturn]] void fail_step(qh_ctx* c, uint32_t err) {
+    // a persistent step that gave up leaves its abort flag raised (and
+    // possibly tagged words of the abandoned phases): clear the flag before
+    // anything else, so later steps do not abandon their waits
+    if (err & (kErrSync | kErrPlace)) {
+        if (c->persist_ok) clear_words(c, c->dargs.abort_flag, 4);
+        clear_words(c, c->acts.attn_cnt, pad32h(c->dm.kvheads) * 4);
+    }
     reset_model(c);
+    if (err & kErrPlace) throw Error("persistent step: a workgroup ran on another XCD than expected");
     if (err & kErrToken) throw Error("token outside vocabulary");
     if (err & kErrRouter) throw Error("invalid MoE router");
     if (err & kErrLogits) throw Error("nonfinite model output");
     if (err & kErrContext) throw Error("context limit " + std::to_string(c->context) + " reached");
-    if (err & kErrSync) {
-        if (c->persist_ok) HIP_OK(hipMemset(c->dargs.abort_flag, 0, 4));
-        HIP_OK(hipMemset(c->acts.attn_cnt, 0, pad32h(c->dm.kvheads) * 4));
-        throw Error("device synchronisation timed out");
-    }
+    if (err & kErrSync) throw Error("device synchronisation timed out");
     throw Error("device step failed");
 }
 

@@ -24,6 +24,12 @@ __global__ __launch_bounds__(kBlock) void k_repack(const uint8_t* __restrict__ s
     }
 }
 
+// p[i] = v for i < n: clears device memory inside a stream (or a captured
+// graph) without a memset node.
+__global__ __launch_bounds__(kBlock) void k_fill_u32(uint32_t* __restrict__ p, size_t n, uint32_t v) {
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (size_t)gridDim.x * kBlock) p[i] = v;
+}
+
 // Bit-exact dequantisation of rows [0, rows) (src/quant.rs:81-84).
 __global__ __launch_bounds__(kBlock) void k_dequant(DevMat m, size_t row0, size_t rows, float* __restrict__ out) {
     const size_t total = rows * m.cols;

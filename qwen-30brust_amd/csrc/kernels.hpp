@@ -35,7 +35,8 @@ enum : uint32_t {
     kErrLogits = 2u,   // non-finite output logits (src/model.rs:296-299)
     kErrToken = 4u,    // token outside vocabulary (src/model.rs:222)
     kErrContext = 8u,  // position beyond the allocated context
-    kErrSync = 16u,    // a cross-workgroup wait of the persistent step timed out
+    kErrSync = 16u,    // a cross-workgroup wait of the persistent step timed out (or was abandoned)
+    kErrPlace = 32u,   // a workgroup of the persistent step ran on another XCD than b % 8
 };
 
 struct LayerW {
@@ -96,22 +97,36 @@ struct AttnArgs {
 // [l0, l1) of one token, followed (vocab = 1) by the vocab projection, argmax
 // and position advance.  Workgroups hand values to each other as tagged
 // words: bits 63..32 carry the tag of the phase that wrote the value (base +
-// phase number), bits 31..0 the value; a reader waits for its tag.
-constexpr uint32_t kPartWords = 130;  // words per attention chunk partial: o[128], m, l
+// phase number), bits 31..0 the value; a reader waits for its tag.  The l*
+// buffers hold one region per XCD (used only by that XCD's workgroups, through
+// its L2); the g* buffers are read across XCDs.  Region strides in words.
+constexpr uint32_t kPartWords = 130;        // words per attention chunk partial: o[128], m, l
+constexpr uint32_t kDecodeXcds = 8;         // XCDs of the device (workgroup b on XCD b % 8)
+constexpr uint32_t kDecodeWgPerXcd = 32;    // workgroups per XCD
+constexpr uint32_t kDecodeQkvX = 768;       // q|k|v rows per XCD: 4 query heads + one KV head
+constexpr uint32_t kDecodeStrideQkv = 768;
+constexpr uint32_t kDecodeStridePart = 32 * 4 * kPartWords;  // [chunk][head] partials
+constexpr uint32_t kDecodeStrideAtt = 512;
+constexpr uint32_t kDecodeStrideX1 = 2048 + 128;  // x' and the unscaled router logits
+constexpr uint32_t kDecodeStrideH = 768;
+constexpr uint32_t kDecodeStrideX2 = 2048;
+constexpr uint32_t kDecodeStrideG1 = 2048 + 128;  // o-projection partial and router terms of an XCD
+constexpr uint32_t kDecodeStrideG2 = 2048;        // weighted down rows of an XCD
 struct DecodeArgs {
     const LayerW* layers;  // device array, one per layer
     DevMat emb, out;
     const float* onorm;
     Acts a;
     ModelDims dm;
-    uint32_t max_chunks;   // attention chunks per KV head (<= 32)
     uint32_t* abort_flag;  // set when a wait times out; every wait then returns
-    uint64_t* tx1;         // [hidden + experts] x after attention (x'), then the unscaled router logits
-    uint64_t* tx2;         // [hidden]  x after the MoE block (x'')
-    uint64_t* tqkv;        // [heads*d + 2*kvheads*d] q | k | v projections
-    uint64_t* tatt;        // [heads*d] attention output
-    uint64_t* tpart;       // [heads][max_chunks][d + 2] attention chunk partials (o, m, l)
-    uint64_t* th;          // [top][ff] SwiGLU outputs
+    uint64_t* lqkv;        // [8][768]   q|k|v rows of the XCD
+    uint64_t* lpart;       // [8][32][4][130] attention chunk partials (o, m, l)
+    uint64_t* latt;        // [8][512]   attention output of the XCD's heads
+    uint64_t* lx1;         // [8][2176]  x' and the unscaled router logits
+    uint64_t* lh;          // [8][768]   SwiGLU outputs of the XCD's expert
+    uint64_t* lx2;         // [8][2048]  x''
+    uint64_t* g1;          // [8][2176]  o-projection partials + router terms
+    uint64_t* g2;          // [8][2048]  weighted down partials
     uint64_t* tfin;        // [gridDim.x][2] vocab argmax partials (key, index)
     uint32_t base;         // tag before this launch's first phase
     uint32_t l0, l1, vocab;
