@@ -150,6 +150,8 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-matvec", action="store_true")
+    ap.add_argument("--no-per-phase", action="store_true",
+                    help="skip the per-phase kernels' comparison line (profiler runs of k_decode alone)")
     ap.add_argument("--prefill", type=int, default=2048,
                     help="tokens of the batched-prefill measurement (0: skip)")
     ap.add_argument("--copy-mb", type=int, default=0,
@@ -207,14 +209,17 @@ def main():
     pos_mid = pos_start + args.warmup + args.steps + (args.profile_steps if persistent else 0)
     # the per-phase kernels: timed as a second line, and profiled one kernel
     # class at a time (HIP events between direct launches)
-    model.persistent = False
-    ms_alt = model.bench_decode(alt_warmup, alt_steps) / alt_steps
-    log(f"per-phase kernels: {ms_alt:.3f} ms/token, {1000.0/ms_alt:.1f} tok/s")
-    breakdown = model.profile_step(args.profile_steps)
-    model.persistent = persistent
+    if args.no_per_phase and persistent:
+        ms_alt, breakdown = None, None
+    else:
+        model.persistent = False
+        ms_alt = model.bench_decode(alt_warmup, alt_steps) / alt_steps
+        log(f"per-phase kernels: {ms_alt:.3f} ms/token, {1000.0/ms_alt:.1f} tok/s")
+        breakdown = model.profile_step(args.profile_steps)
+        model.persistent = persistent
     bytes_cls = algorithmic_bytes(model, pos_mid + args.profile_steps / 2)
     classes = {}
-    for k, v in breakdown.items():
+    for k, v in (breakdown or {}).items():
         gbs = bytes_cls[k] / (v * 1e-3) / 1e9 if v > 0 else 0.0
         classes[k] = {"ms_per_token": round(v, 4), "bytes_per_token": int(bytes_cls[k]), "GB_s": round(gbs, 1)}
     if persistent:
@@ -284,8 +289,8 @@ def main():
                              "frac": round(w_active * tok_s / 1e9 / HBM_PEAK_GBS, 4)},
         "step": "persistent k_decode (one launch per token)" if persistent else "per-phase kernels",
         "decode_launch": decode_launch,
-        "per_phase_kernels": {"ms_per_token": round(ms_alt, 4), "tok_s": round(1000.0 / ms_alt, 2),
-                              "breakdown": classes},
+        "per_phase_kernels": None if ms_alt is None else {"ms_per_token": round(ms_alt, 4),
+                                                          "tok_s": round(1000.0 / ms_alt, 2), "breakdown": classes},
         "prefill": prefill,
         "matvec": matvec,
         "cpu_baseline": cpu,

@@ -2,7 +2,8 @@
 command-line driver (qwen-hip) and the synthetic-model generator
 (libqwen_synth.so, host-only g++).
 
-Usage: python qwen-30brust_amd/build.py   (compiles every time it is called)
+Usage: python qwen-30brust_amd/build.py         (compiles every time it is called)
+       python qwen-30brust_amd/build.py trace   (the phase-trace variant, after a build)
 """
 import os
 import subprocess
@@ -16,6 +17,7 @@ BUILD = os.path.join(PKG, "_build")
 ENGINE_SO = os.path.join(PKG, "libqwen_hip.so")
 SYNTH_SO = os.path.join(PKG, "libqwen_synth.so")
 CLI = os.path.join(PKG, "qwen-hip")
+TRACE_SO = os.path.join(PKG, "libqwen_hip_trace.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
@@ -55,6 +57,26 @@ def build_engine():
     return ENGINE_SO
 
 
+def build_trace():
+    """libqwen_hip_trace.so: the engine with the phase-trace build of the
+    persistent step (decode_trace.hip) in place of decode.hip, for
+    phase_trace.py.  Built on request only (`python build.py trace`)."""
+    os.makedirs(BUILD, exist_ok=True)
+    objs = []
+    for src in ENGINE_SOURCES:
+        obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+        if src == "decode.hip":
+            obj = os.path.join(BUILD, "decode_trace.o")
+            _run([HIPCC, *HIP_FLAGS, "-x", "hip", "-c", os.path.join(CSRC, "decode_trace.hip"), "-o", obj])
+        elif not os.path.exists(obj):
+            raise RuntimeError(f"{obj} is missing: build the engine first")
+        objs.append(obj)
+    tmp = TRACE_SO + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, "-lhipblaslt"])
+    os.replace(tmp, TRACE_SO)
+    return TRACE_SO
+
+
 def build_cli():
     """qwen-hip, the command-line driver over the C ABI (links libqwen_hip.so
     from its own directory)."""
@@ -81,6 +103,9 @@ def build():
 
 
 if __name__ == "__main__":
-    for p in build():
-        print(p)
+    if sys.argv[1:] == ["trace"]:
+        print(build_trace())
+    else:
+        for p in build():
+            print(p)
     sys.exit(0)

@@ -8,7 +8,7 @@
 // handed between the 32 workgroups of one XCD go through that XCD's L2
 // (plain stores, loads that skip L1: about 0.4 us per hand-over); values that
 // cross XCDs are written through to memory and read past the caches (about
-// 1.6 us).  The layer is laid out so that only two of its eight hand-overs
+// 1.6 us).  The layer is laid out so that only two of its seven hand-overs
 // cross XCDs:
 //
 //   XCD X owns query heads 4X..4X+3, which share KV head X/2 (Qwen3-30B-A3B:
@@ -21,11 +21,11 @@
 //      router term sum_c router[e][c] ffn_norm[c] x[c] over this XCD's
 //      256 columns for experts 4j..4j+3                        -> L qkv
 //   B  Q/K RMSNorm, RoPE, KV append, GQA attention of the XCD's 4 heads over
-//      key chunk j (online softmax, P.V on MFMA)               -> L partials
-//   M  merge of the chunk partials: head j/8, 16 dims per workgroup -> L attn
-//   C  o-projection partial over this XCD's 512 attention columns for rows
-//      [64j, 64j+64), and the router fold F[e] . a over the same columns
-//                                                              -> G partials
+//      key chunk j (online softmax, P.V on MFMA; at most 16 chunks)
+//                                                              -> L partials
+//   C  merge of the chunk partials (every workgroup); o-projection partial
+//      over this XCD's 512 attention columns for rows [64j, 64j+64), and the
+//      router fold F[e] . a over the same columns              -> G partials
 //   D  x' = x + sum over XCDs of the partials (rows of j), unscaled router
 //      logits u of experts 4j..4j+3                            -> L x', u
 //   E  RMS scale s of x', router logits s u, top-k (every workgroup, bit-exact
@@ -39,7 +39,7 @@
 // by workgroup 0.
 //
 // Hand-over without flags or barriers: every value passed on is a 64-bit
-// word (tag << 32) | bits, with tag = base + 8 (layer - l0) + phase (1..8;
+// word (tag << 32) | bits, with tag = base + 7 (layer - l0) + phase (1..7;
 // the vocab phase uses the next one; base grows by the launch's phase count,
 // so tags never repeat between launches).  A reader polls exactly the words
 // it needs until each carries the tag it expects.  Every wait is bounded: on
@@ -76,14 +76,15 @@ constexpr uint32_t kQkvWg = kQkvX / kNJ;    // 24 per workgroup, 3 per wave
 constexpr uint32_t kRowsWg = 64;            // rows of x per workgroup slice (2048 / 32)
 constexpr uint32_t kExpWg = 4;              // router experts per workgroup slice (128 / 32)
 constexpr uint32_t kDTile = 64;             // keys per attention tile
-constexpr uint32_t kMinKeys = 16;           // fewest keys per attention chunk
+constexpr uint32_t kMinKeys = 64;           // fewest keys per attention chunk (one tile)
+constexpr uint32_t kMaxChunks = 16;         // most attention chunks per XCD
 constexpr uint32_t kTP = 132;               // LDS pitch of the value tile (floats)
 constexpr uint32_t kPP = 68;                // LDS pitch of the per-head scores (floats)
 constexpr uint32_t kDSmem = 10240;          // floats of phase scratch
 constexpr uint32_t kFfWg = 24;              // gate/up rows per workgroup (768 / 32), 3 per wave
 constexpr uint32_t kDownUnits = 3;          // chunks per lane in F (8 rows x 24 chunks per wave)
 constexpr uint32_t kVocabRows = 4;          // vocab rows per wave group
-constexpr uint32_t kGatherPairs = 6;        // word pairs in flight per thread in a gather
+constexpr uint32_t kGatherPairs = 5;        // word pairs in flight per thread in a gather (one round up to 5120 words)
 constexpr int kAuxL = 3;                    // sc0 nt: skip L1, served by the XCD's L2
 constexpr int kAuxG = 17;                   // sc0 sc1: past every cache
 
@@ -106,6 +107,7 @@ struct DecodeLds {
     float red[2 * kDW];
     float ra[kExpWg];         // router term of this XCD's columns for experts 4j..4j+3
     float lg[128];            // router logits
+    float mw[kHX * kMaxChunks];  // merge weight of each (head, chunk)
     alignas(16) long long ck[128];  // composite top-k keys
     float sv[8];
     uint32_t sid[8];
@@ -297,23 +299,24 @@ __device__ __forceinline__ void norm_in_lds(const Ctx& c, float* xs, float4 w, f
     __syncthreads();
 }
 
-// Tag of phase k (1..8) of layer l.
+// Tag of phase k (1..kDecodePhases) of layer l.
 __device__ __forceinline__ uint32_t ptag(const DecodeArgs& A, uint32_t l, uint32_t k) {
-    return A.base + 8 * (l - A.l0) + k;
+    return A.base + kDecodePhases * (l - A.l0) + k;
 }
 
 // Per-XCD and cross-XCD exchange buffers of this workgroup's XCD.
 __device__ __forceinline__ uint64_t* lbuf(uint64_t* base, uint32_t stride, uint32_t X) { return base + (size_t)X * stride; }
 
 // Chunk geometry of the attention: chunk j of T keys, at least kMinKeys keys
-// per chunk, at most 32 chunks.
+// per chunk, at most kMaxChunks chunks (a chunk's time hardly depends on how
+// many of its tile's 64 keys are used, and fewer chunks are cheaper to merge).
 struct AttnChunk {
     uint32_t nch, t0, t1;
     bool active;
 };
 __device__ __forceinline__ AttnChunk attn_chunk(const Ctx& c) {
     AttnChunk k;
-    const uint32_t tc = max((c.T + kNJ - 1) / kNJ, kMinKeys);
+    const uint32_t tc = max((c.T + kMaxChunks - 1) / kMaxChunks, kMinKeys);
     k.nch = (c.T + tc - 1) / tc;
     k.active = c.j < k.nch;
     k.t0 = min(c.T, c.j * tc);
@@ -365,13 +368,16 @@ __device__ __forceinline__ void attn_prefetch(const DecodeArgs& A, const LayerW&
 // (2048 columns = 64 chunks).  The router term of experts 4j..4j+3 over
 // columns [256X, 256X+256) is reduced in the same pass (waves 0-3, one
 // expert each).
-template <uint32_t KQ, uint32_t KV>
+template <uint32_t KQ>
 __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
                                           uint32_t l, AttnPre& P) {
     const Ctx c = fresh(c0);
     const uint32_t g = c.X / 2;
+    // v rows are Q6_K or Q4_K (a Q4_K chunk kept in the ql/qh fields): one
+    // copy of the phase for both layer kinds keeps the step's code small
+    const bool v6 = L.v.kind == Q6_K;
     typename Fmt<KQ>::Raw wq[3];
-    typename Fmt<KV>::Raw wvv[3];
+    typename Fmt<Q6_K>::Raw wvv[3];
 #pragma unroll
     for (uint32_t k = 0; k < 3; k++) {
         const uint32_t r = kQkvWg * c.j + c.wv + kDW * k;  // wave-uniform, < 768
@@ -380,7 +386,14 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
         } else if (r < 640) {
             wq[k] = Fmt<KQ>::load(L.k.w + (size_t)(128 * g + r - 512) * L.k.drb, L.k.geo, c.lane);
         } else {
-            wvv[k] = Fmt<KV>::load(L.v.w + (size_t)(128 * g + r - 640) * L.v.drb, L.v.geo, c.lane);
+            const uint8_t* vrow = L.v.w + (size_t)(128 * g + r - 640) * L.v.drb;
+            if (v6) {
+                wvv[k] = Fmt<Q6_K>::load(vrow, L.v.geo, c.lane);
+            } else {
+                const typename Fmt<Q4_K>::Raw t = Fmt<Q4_K>::load(vrow, L.v.geo, c.lane);
+                wvv[k].ql = t.q;
+                wvv[k].qh = t.h;
+            }
         }
     }
     const float4 nw = gld<float4>(L.attn_norm + 4 * c.tid);
@@ -398,7 +411,7 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
         // x as the embedding kernel (or the host) left it before this launch
         *reinterpret_cast<float4*>(xs + px(4 * c.tid)) = ld_sys4(buf_rsrc(A.a.x, c.H * 4), c.tid * 16);
         __syncthreads();
-    } else if (!gather_l(A, S, lbuf(A.lx2, kDecodeStrideX2, c.X), c.H, ptag(A, l - 1, 8), xs, c.tid)) {
+    } else if (!gather_l(A, S, lbuf(A.lx2, kDecodeStrideX2, c.X), c.H, ptag(A, l - 1, 7), xs, c.tid)) {
         return false;  // x'' of the previous layer (phase R)
     }
     QH_MARK(0, 1);
@@ -424,10 +437,13 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
         float acc;
         if (r < 640) {
             acc = Fmt<KQ>::dot(wq[k], c.lane, xa, xb, sa, sb);
-        } else {
+        } else if (v6) {
             float ya[16], yb[16], ta, tb;
-            x_runs_p<KV>(xs, 0, c.lane, ya, yb, ta, tb);
-            acc = Fmt<KV>::dot(wvv[k], c.lane, ya, yb, ta, tb);
+            x_runs_p<Q6_K>(xs, 0, c.lane, ya, yb, ta, tb);
+            acc = Fmt<Q6_K>::dot(wvv[k], c.lane, ya, yb, ta, tb);
+        } else {
+            static_assert(KQ == Q4_K, "Q4_K v rows reuse the q|k rows' x runs");
+            acc = Fmt<Q4_K>::dot({wvv[k].ql, wvv[k].qh}, c.lane, xa, xb, sa, sb);
         }
         acc = wave_sum(acc);
         if (c.lane == 0) S.hv[c.wv + kDW * k] = acc;
@@ -527,6 +543,7 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
     if (ab) S.abort = 1;
     __syncthreads();
     if (S.abort) return false;
+    QH_MARK(1, 4);
     const float root = sqrtf(128.0f);
     const uint32_t part = tid & 7, kt = tid >> 3, grp = lane >> 4, col = lane & 15;
     float mh = -INFINITY, lh = 0.f;     // softmax state of head wv
@@ -573,6 +590,7 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
         }
         if (tt + kDTile < t1) kv_slice(kr, vr, L.kcache, L.vcache, g, ctx, tt + kDTile, t1, pos, tid);
         __syncthreads();
+        QH_MARK(1, 5);
         if (wv < kHX) {  // wave-uniform: online softmax of head wv
             const float sv = lane < nt ? ps[wv * kPP + lane] : -INFINITY;
             const float M = fmaxf(mh, wave_max(sv));
@@ -584,6 +602,7 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
             if (lane == 0) al[wv] = alpha;
         }
         __syncthreads();
+        QH_MARK(1, 6);
         // O[h][d] = alpha_h O[h][d] + sum_key P[h][key] V[key][d]: M = heads,
         // N = 16 dims per wave, K = 64 keys
 #pragma unroll
@@ -614,47 +633,11 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
     return true;
 }
 
-// ================================================ M: merge of the chunks ==
-// Workgroup j: head j/8, dims 16 (j%8) .. +16.  Wave 0, lane = (half
-// lane/32, chunk lane%32): m, l and dims 8 half .. +8 of the chunk;
-// O = sum_c o_c exp(m_c - M) / sum_c l_c exp(m_c - M) over the chunks in a
-// fixed reduction order.
-__device__ __forceinline__ void phase_merge(const DecodeArgs& A, DecodeLds& S, const Ctx& c0, uint32_t l) {
-    const Ctx c = fresh(c0);
-    if (c.wv != 0) return;
-    const AttnChunk k = attn_chunk(c);
-    const uint32_t hm = c.j >> 3, d0 = 16 * (c.j & 7), cc = c.lane & 31, half = c.lane >> 5;
-    const uint64_t* src = lbuf(A.lpart, kDecodeStridePart, c.X);
-    const __amdgpu_buffer_rsrc_t r = buf_rsrc(src, kDecodeStridePart * 8);
-    const uint32_t pb = (min(cc, k.nch - 1) * kHX + hm) * kPartWords;
-    const uint32_t word[5] = {pb + 128, pb + d0 + 8 * half, pb + d0 + 8 * half + 2, pb + d0 + 8 * half + 4,
-                              pb + d0 + 8 * half + 6};
-    float v[10];
-    bool ab = false;
-    poll_pairs<kAuxL, 5>(A, r, word, cc < k.nch ? 31u : 0u, 31u, ptag(A, l, 2), v, ab);
-    if (ab) {
-        S.abort = 1;
-        return;
-    }
-    const bool on = cc < k.nch;
-    const float m = on ? v[0] : -INFINITY;
-    const float M = wave_max(m);
-    const float e = on ? expf(m - M) : 0.f;
-    const float Ls = seg_sum(on ? v[1] * e : 0.f, 32);
-    float o[8];
-#pragma unroll
-    for (uint32_t i = 0; i < 8; i++) o[i] = seg_sum(on ? v[2 + i] * e : 0.f, 32);
-    const float inv = 1.0f / Ls;
-    if (cc < 8) {
-        float sel = o[0];
-#pragma unroll
-        for (uint32_t i = 1; i < 8; i++) sel = cc == i ? o[i] : sel;
-        put_l(lbuf(A.latt, kDecodeStrideAtt, c.X) + hm * 128 + d0 + 8 * half + cc, sel * inv, ptag(A, l, 3));
-    }
-}
-
-// ======================================================== C: o-projection ==
-// Rows [64j, 64j+64) of the o-projection restricted to this XCD's 512
+// ============================================= C: merge + o-projection ==
+// Every workgroup gathers the XCD's chunk partials and merges them:
+// a = sum_c o_c exp(m_c - M) / sum_c l_c exp(m_c - M) for the 4 heads (the
+// chunk weights by wave 0, lane = (head, chunk), then thread = (head, dim)).
+// Then rows [64j, 64j+64) of the o-projection restricted to this XCD's 512
 // attention columns (chunks 16X..16X+15): wave wv rows 64j + 8wv + rr + 4i
 // (i < 2), lane = (rr lane/16, chunk lane%16).  The router fold
 // F[e] . a over the same columns for experts 4j..4j+3 (two waves each).
@@ -670,10 +653,33 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
     const uint32_t fe = min(kExpWg * c.j + (c.tid >> 7), c.E - 1), fc = 512 * c.X + 4 * (c.tid & 127);
     const float4 f = gld<float4>(L.rfold + (size_t)fe * c.qd + fc);
     QH_MARK(2, 0);
-    float* xs = S.big;
-    if (!gather_l(A, S, lbuf(A.latt, kDecodeStrideAtt, c.X), 512, ptag(A, l, 3), xs, c.tid))
-        return false;  // this XCD's attention output (phase M)
+    float* ps = S.big;             // [nch][4][130] chunk partials (padded layout)
+    float* xs = S.big + 9216;      // [512] merged attention output (padded layout)
+    const uint32_t nch = attn_chunk(c).nch;
+    if (!gather_l(A, S, lbuf(A.lpart, kDecodeStridePart, c.X), nch * kHX * kPartWords, ptag(A, l, 2), ps, c.tid))
+        return false;  // the chunk partials (phase B)
     QH_MARK(2, 1);
+    if (c.wv == 0) {
+        const uint32_t h = c.lane >> 4, ck = c.lane & 15, pb = (ck * kHX + h) * kPartWords;
+        const bool on = ck < nch;
+        const float m = on ? ps[px(pb + 128)] : -INFINITY;
+        float M = fmaxf(m, dpp_f<kDppXor1>(m));
+        M = fmaxf(M, dpp_f<kDppXor2>(M));
+        M = fmaxf(M, dpp_f<kDppHalfMirror>(M));
+        M = fmaxf(M, dpp_f<kDppMirror>(M));  // max over the head's 16 lanes
+        const float e = on ? expf(m - M) : 0.f;
+        const float Ls = seg_sum(on ? ps[px(pb + 129)] * e : 0.f, 16);
+        S.mw[c.lane] = e / Ls;
+    }
+    __syncthreads();
+    {
+        const uint32_t h = c.tid >> 7, d = c.tid & 127;
+        float a = 0.f;
+        for (uint32_t ck = 0; ck < nch; ck++) a = fmaf(ps[px((ck * kHX + h) * kPartWords + d)], S.mw[h * 16 + ck], a);
+        xs[px(c.tid)] = a;
+    }
+    __syncthreads();
+    QH_MARK(2, 2);
     {
         float xa[16], xb[16], sa, sb;
         x_runs_p<KO>(xs, 0, cc, xa, xb, sa, sb);
@@ -694,10 +700,10 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
     }
     __syncthreads();
     uint64_t* dst = lbuf(A.g1, kDecodeStrideG1, c.X);
-    if (c.tid < kRowsWg) put_g(dst + kRowsWg * c.j + c.tid, S.po[c.tid], ptag(A, l, 4));  // one store instruction
+    if (c.tid < kRowsWg) put_g(dst + kRowsWg * c.j + c.tid, S.po[c.tid], ptag(A, l, 3));  // one store instruction
     if (c.tid >= 64 && c.tid < 64 + kExpWg) {
         const uint32_t e = c.tid - 64;
-        put_g(dst + c.H + kExpWg * c.j + e, S.ra[e] + (S.red[2 * e] + S.red[2 * e + 1]), ptag(A, l, 4));
+        put_g(dst + c.H + kExpWg * c.j + e, S.ra[e] + (S.red[2 * e] + S.red[2 * e + 1]), ptag(A, l, 3));
     }
     return true;
 }
@@ -716,13 +722,14 @@ __device__ __forceinline__ bool phase_xr1(const DecodeArgs& A, DecodeLds& S, con
         const uint32_t w = p < kRowsWg / 2 ? kRowsWg * c.j + 2 * p : c.H + kExpWg * c.j + 2 * (p - kRowsWg / 2);
         const uint32_t word[1] = {k * kDecodeStrideG1 + w};
         float v[2];
-        poll_pairs<kAuxG, 1>(A, buf_rsrc(A.g1, kNX * kDecodeStrideG1 * 8), word, 1u, 1u, ptag(A, l, 4), v, ab);
+        poll_pairs<kAuxG, 1>(A, buf_rsrc(A.g1, kNX * kDecodeStrideG1 * 8), word, 1u, 1u, ptag(A, l, 3), v, ab);
         vals[k * 68 + 2 * p] = v[0];
         vals[k * 68 + 2 * p + 1] = v[1];
     }
     if (ab) S.abort = 1;
     __syncthreads();
     if (S.abort) return false;
+    QH_MARK(7, 0);
     uint64_t* dst = lbuf(A.lx1, kDecodeStrideX1, c.X);
     if (c.tid < kRowsWg + kExpWg) {
         float s = vals[c.tid];
@@ -731,9 +738,9 @@ __device__ __forceinline__ bool phase_xr1(const DecodeArgs& A, DecodeLds& S, con
         if (c.tid < kRowsWg) {
             const float x1 = S.xo[c.tid] + s;  // residual (model.rs:246-248)
             S.x1[c.tid] = x1;
-            put_l(dst + kRowsWg * c.j + c.tid, x1, ptag(A, l, 5));
+            put_l(dst + kRowsWg * c.j + c.tid, x1, ptag(A, l, 4));
         } else {
-            put_l(dst + c.H + kExpWg * c.j + (c.tid - kRowsWg), s, ptag(A, l, 5));
+            put_l(dst + c.H + kExpWg * c.j + (c.tid - kRowsWg), s, ptag(A, l, 4));
         }
     }
     return true;
@@ -744,7 +751,7 @@ __device__ __forceinline__ bool phase_xr1(const DecodeArgs& A, DecodeLds& S, con
 // s = 1/sqrt(mean(x'^2) + eps) (ops.rs:3-15) gives logit e = s u_e.  Then
 // the top-k in every workgroup, and this XCD's expert (rank X): gate/up rows
 // 24j + 3wv + k (k < 3), lane = chunk.
-template <uint32_t KG, uint32_t KD>
+template <uint32_t KG>
 __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
                                           uint32_t l) {
     const Ctx c = fresh(c0);
@@ -752,7 +759,7 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
     const float4 fn = gld<float4>(L.ffn_norm + 4 * c.tid);
     QH_MARK(4, 0);
     float* xs = S.big;
-    if (!gather_l(A, S, lbuf(A.lx1, kDecodeStrideX1, c.X), H + E, ptag(A, l, 5), xs, c.tid))
+    if (!gather_l(A, S, lbuf(A.lx1, kDecodeStrideX1, c.X), H + E, ptag(A, l, 4), xs, c.tid))
         return false;  // x' and u (phase D)
     float* x4 = xs + px(4 * c.tid);
     const float4 x1 = *reinterpret_cast<const float4*>(x4);
@@ -776,6 +783,7 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
                                 : LLONG_MIN;
     }
     __syncthreads();
+    QH_MARK(4, 4);
     if (S.bad) {
         if (c.b == 0 && c.tid == 0) atomicOr(&A.a.st->err, kErrRouter);
         return false;  // every workgroup sees the same logits
@@ -784,12 +792,13 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         // thread (i, q) counts the keys of quarter q (32 of them) above expert i's
         const uint32_t i = c.tid >> 2, q = c.tid & 3;
         const long long ki = S.ck[i];
+        // all 16 reads issued before any compare (one LDS round trip)
+        longlong2 w2[16];
+#pragma unroll
+        for (uint32_t k = 0; k < 16; k++) w2[k] = reinterpret_cast<const longlong2*>(S.ck + 32 * q)[k];
         int32_t rank = 0;
 #pragma unroll
-        for (uint32_t jj = 32 * q; jj < 32 * q + 32; jj += 2) {
-            const longlong2 w2 = *reinterpret_cast<const longlong2*>(S.ck + jj);
-            rank += (w2.x > ki) + (w2.y > ki);
-        }
+        for (uint32_t k = 0; k < 16; k++) rank += (w2[k].x > ki) + (w2[k].y > ki);
         rank += dpp_i<kDppXor1>(rank);
         rank += dpp_i<kDppXor2>(rank);
         if (q == 0 && i < E && (uint32_t)rank < top) {
@@ -798,6 +807,7 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         }
     }
     __syncthreads();
+    QH_MARK(4, 5);
     // softmax over the selected logits (ops.rs:29-44), in every wave, lane k =
     // rank k; wave 0 keeps the result in LDS for phase F
     {
@@ -837,7 +847,7 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
     QH_MARK(4, 3);
     __syncthreads();  // S.hv complete; every wave is done with xn, which the next gather overwrites
     if (c.tid < kFfWg)  // one store instruction
-        put_l(lbuf(A.lh, kDecodeStrideH, c.X) + kFfWg * c.j + c.tid, S.hv[c.tid], ptag(A, l, 6));
+        put_l(lbuf(A.lh, kDecodeStrideH, c.X) + kFfWg * c.j + c.tid, S.hv[c.tid], ptag(A, l, 5));
     return true;
 }
 
@@ -857,7 +867,7 @@ __device__ __forceinline__ bool phase_down(const DecodeArgs& A, DecodeLds& S, co
     for (uint32_t i = 0; i < kDownUnits; i++) wd[i] = Fmt<KD>::load(drow, L.down.geo, (c.lane & 7) + 8 * i);
     QH_MARK(5, 0);
     float* xs = S.big;
-    if (!gather_l(A, S, lbuf(A.lh, kDecodeStrideH, c.X), c.ff, ptag(A, l, 6), xs, c.tid))
+    if (!gather_l(A, S, lbuf(A.lh, kDecodeStrideH, c.X), c.ff, ptag(A, l, 5), xs, c.tid))
         return false;  // SwiGLU outputs (phase E)
     QH_MARK(5, 1);
     float acc = 0.f;
@@ -872,7 +882,7 @@ __device__ __forceinline__ bool phase_down(const DecodeArgs& A, DecodeLds& S, co
     if ((c.lane & 7) == 0) S.po[8 * c.wv + (c.lane >> 3)] = S.wts[c.X] * acc;  // w * down (model.rs:281-284)
     __syncthreads();
     if (c.tid < kRowsWg)  // one store instruction
-        put_g(lbuf(A.g2, kDecodeStrideG2, c.X) + kRowsWg * c.j + c.tid, S.po[c.tid], ptag(A, l, 7));
+        put_g(lbuf(A.g2, kDecodeStrideG2, c.X) + kRowsWg * c.j + c.tid, S.po[c.tid], ptag(A, l, 6));
     return true;
 }
 
@@ -887,20 +897,21 @@ __device__ __forceinline__ bool phase_xr2(const DecodeArgs& A, DecodeLds& S, con
         const uint32_t k = c.tid / (kRowsWg / 2), p = c.tid % (kRowsWg / 2);
         const uint32_t word[1] = {k * kDecodeStrideG2 + kRowsWg * c.j + 2 * p};
         float v[2];
-        poll_pairs<kAuxG, 1>(A, buf_rsrc(A.g2, kNX * kDecodeStrideG2 * 8), word, 1u, 1u, ptag(A, l, 7), v, ab);
+        poll_pairs<kAuxG, 1>(A, buf_rsrc(A.g2, kNX * kDecodeStrideG2 * 8), word, 1u, 1u, ptag(A, l, 6), v, ab);
         vals[k * kRowsWg + 2 * p] = v[0];
         vals[k * kRowsWg + 2 * p + 1] = v[1];
     }
     if (ab) S.abort = 1;
     __syncthreads();
     if (S.abort) return false;
+    QH_MARK(7, 1);
     if (c.tid < kRowsWg) {
         float moe = 0.f;
 #pragma unroll
         for (uint32_t k = 0; k < kNX; k++) moe += vals[k * kRowsWg + c.tid];
         const float x2 = S.x1[c.tid] + moe;
         S.xo[c.tid] = x2;
-        put_l(lbuf(A.lx2, kDecodeStrideX2, c.X) + kRowsWg * c.j + c.tid, x2, ptag(A, l, 8));
+        put_l(lbuf(A.lx2, kDecodeStrideX2, c.X) + kRowsWg * c.j + c.tid, x2, ptag(A, l, 7));
         if (last && c.X == 0) A.a.x[kRowsWg * c.j + c.tid] = x2;  // x after the launch, for the host
     }
     // the routing of the layer, for the host
@@ -921,7 +932,7 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
     const Acts& a = A.a;
     const DevMat& mv = A.out;
     const uint32_t V = A.dm.vocab, ngrp = (V + kVocabRows - 1) / kVocabRows, cpr = c.H / 32;
-    const uint32_t tag = A.base + 8 * (A.l1 - A.l0) + 1;
+    const uint32_t tag = A.base + kDecodePhases * (A.l1 - A.l0) + 1;
     using Raw = typename Fmt<KV>::Raw;
     // unconditional loads (row and chunk clamped into the matrix; results of
     // clamped rows are dropped): the compiler then waits for exactly the group
@@ -948,7 +959,7 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
     const float4 on = gld<float4>(A.onorm + 4 * c.tid);
     QH_MARK(6, 0);
     float* xs = S.big;
-    if (!gather_l(A, S, lbuf(A.lx2, kDecodeStrideX2, c.X), c.H, ptag(A, A.l1 - 1, 8), xs, c.tid))
+    if (!gather_l(A, S, lbuf(A.lx2, kDecodeStrideX2, c.X), c.H, ptag(A, A.l1 - 1, 7), xs, c.tid))
         return;  // x after the last layer
     QH_MARK(6, 1);
     norm_in_lds(c, xs, on, A.dm.eps, S.red);
@@ -1114,12 +1125,12 @@ __global__ __launch_bounds__(kDT) void k_decode(DecodeArgs A) {
         const LayerW& L = *(const LayerW*)((const __attribute__((address_space(4))) LayerW*)A.layers + l);
         bool ok = true;
         AttnPre P;
-        QH_DISPATCH_KM(L.v.kind, KV, ok = phase_qkv<Q4_K, KV>(A, S, L, c, l, P));
+        ok = phase_qkv<Q4_K>(A, S, L, c, l, P);
         if (!ok || !phase_attn(A, S, L, c, l, P)) return;
-        phase_merge(A, S, c, l);
         if (!phase_oproj<Q4_K>(A, S, L, c, l)) return;
         if (!phase_xr1(A, S, c, l)) return;
-        QH_DISPATCH_KM(L.down.kind, KD, ok = phase_moe<Q4_K, KD>(A, S, L, c, l) && phase_down<KD>(A, S, L, c, l));
+        ok = phase_moe<Q4_K>(A, S, L, c, l);
+        if (ok) QH_DISPATCH_KM(L.down.kind, KD, ok = phase_down<KD>(A, S, L, c, l));
         if (!ok || !phase_xr2(A, S, c, l, l + 1 == A.l1)) return;
     }
     if (A.vocab) QH_DISPATCH_KM(A.out.kind, KV, phase_vocab<KV>(A, S, c));

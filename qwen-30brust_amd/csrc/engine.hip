@@ -612,7 +612,7 @@ void setup_persist(qh_ctx* c) {
         uint64_t words;
         uint64_t** dst;
     } regions[] = {
-        {X * kDecodeStrideQkv, &A.lqkv}, {X * kDecodeStridePart, &A.lpart}, {X * kDecodeStrideAtt, &A.latt},
+        {X * kDecodeStrideQkv, &A.lqkv}, {X * kDecodeStridePart, &A.lpart},
         {X * kDecodeStrideX1, &A.lx1},   {X * kDecodeStrideH, &A.lh},       {X * kDecodeStrideX2, &A.lx2},
         {X * kDecodeStrideG1, &A.g1},    {X * kDecodeStrideG2, &A.g2},      {2ull * nwg, &A.tfin},
     };
@@ -643,7 +643,7 @@ void clear_words(qh_ctx* c, void* p, size_t bytes) {
 // final norm, vocab projection, argmax and position advance.
 void launch_decode(qh_ctx* c, uint32_t l0, uint32_t l1, bool vocab) {
     if (!(l0 < l1 && l1 <= c->layers.size())) throw Error("decode launch needs a non-empty layer range");
-    const uint32_t phases = 8 * (l1 - l0) + (vocab ? 1 : 0);
+    const uint32_t phases = kDecodePhases * (l1 - l0) + (vocab ? 1 : 0);
     if (c->flag_base > 0xFFFFFFFFu - phases) {
         // tags would wrap: clear every tagged word (no launch is reading them:
         // this stream runs the launches in order) and start again from 0
