@@ -296,6 +296,10 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
+    # release the device before the interpreter (and a profiler's exit
+    # handlers) tear the runtime down
+    del model
+    dev.close()
 
 
 if __name__ == "__main__":

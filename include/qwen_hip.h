@@ -67,6 +67,11 @@ int qh_load_model(qh_ctx *ctx, const void *gguf_image, size_t len, size_t contex
 /* Same, reading the file at `path`. */
 int qh_load_model_file(qh_ctx *ctx, const char *path, size_t context);
 int qh_model_config(const qh_ctx *ctx, qh_config_t *out);
+/* Number of models loaded into this context so far (no counterpart in the
+ * reference, where each Model owns its weights): a caller that keeps a
+ * handle to "the loaded model" compares it with the value seen at load time
+ * to detect that a later load replaced it. */
+int qh_model_generation(const qh_ctx *ctx, uint64_t *out);
 /* == Gguf::tensor (src/gguf.rs:196-200): GGML kind, rank and dims of a
  * loaded tensor (dims[0] = columns); "missing tensor {name}" otherwise. */
 int qh_tensor_info(const qh_ctx *ctx, const char *name, uint32_t *kind, size_t *rank,
@@ -127,16 +132,18 @@ int qh_attention(qh_ctx *ctx, const float *q, const float *k, const float *v, si
 
 /* == Model::forward (src/model.rs:209-216): one causal token step on the
  * device (embedding, every layer, KV append, final norm, vocab projection,
- * finite check).  logits (vocab floats) and argmax may be NULL.  On error the
- * KV cache and position are reset, as the reference rolls back. */
-int qh_forward(qh_ctx *ctx, uint32_t token, float *logits, uint32_t *argmax);
+ * finite check).  logits (room for logits_cap floats; the model's vocab are
+ * written) and argmax may be NULL; logits_cap below the vocabulary is an
+ * error.  On error the KV cache and position are reset, as the reference
+ * rolls back. */
+int qh_forward(qh_ctx *ctx, uint32_t token, float *logits, size_t logits_cap, uint32_t *argmax);
 /* Sequential prefill of `n_prompt` tokens followed by `n_new` greedy tokens,
  * all chained on the device with no per-token host round trip (the
  * src/main.rs:250-282 loop with temperature 0).  out_tokens receives the
- * n_new generated ids; logits_last (vocab floats, nullable) the logits that
- * produced the last generated token. */
+ * n_new generated ids; logits_last (room for logits_cap floats, nullable)
+ * the logits that produced the last generated token. */
 int qh_generate(qh_ctx *ctx, const uint32_t *prompt, size_t n_prompt, size_t n_new,
-                uint32_t *out_tokens, float *logits_last);
+                uint32_t *out_tokens, float *logits_last, size_t logits_cap);
 /* == Sampler (src/sampling.rs:3-65) with its rand 0.8.8 StdRng stream
  * (ChaCha12 seeded by seed_from_u64), host-side state: qh_sampler_create
  * replaces Sampler::new (src/sampling.rs:10-25) with its check ("invalid
@@ -169,13 +176,15 @@ int qh_position(const qh_ctx *ctx, size_t *out);
  * GEMMs and a causal flash-attention pass, in chunks of up to 2048 tokens.
  * Fills the KV cache for those positions, writes the greedy id after the
  * last prompt token to the device token ring (so qh_forward / qh_generate
- * continue from it), advances the position by n.  logits (vocab floats) and
- * argmax (nullable) receive the last prompt token's output.  Numerics: fp16
+ * continue from it), advances the position by n.  logits (room for
+ * logits_cap floats) and argmax (nullable) receive the last prompt token's
+ * output.  Numerics: fp16
  * operands with fp32 accumulation (logits within about 1e-2 relative of the
  * FP32 path); fails for models it does not cover (head_dim != 128, more than
  * 8 query heads per KV head, more than 128 experts, projections other than
  * Q4_K/Q6_K). */
-int qh_prefill(qh_ctx *ctx, const uint32_t *prompt, size_t n, float *logits, uint32_t *argmax);
+int qh_prefill(qh_ctx *ctx, const uint32_t *prompt, size_t n, float *logits, size_t logits_cap,
+               uint32_t *argmax);
 
 /* One decoder layer (the loop body src/model.rs:227-287) applied to x[hidden]
  * in place at position `pos`, with this layer's KV history replaced by
@@ -194,6 +203,23 @@ int qh_persistent(const qh_ctx *ctx, int *out);
 /* Selects the implementation for the loaded model (enable = 0: per-phase
  * kernels).  Enabling fails when the model is not covered. */
 int qh_set_persistent(qh_ctx *ctx, int enable);
+
+/* Diagnostics of the token steps (no counterpart in the reference, whose
+ * KV cache and routing are private to Model): qh_route_log copies the
+ * routed experts recorded for positions [pos0, pos0 + n), ids[n][layers][top]
+ * in rank order, as the last step that processed each position (qh_forward,
+ * qh_generate, qh_prefill, either step implementation) chose them;
+ * qh_read_kv copies layer `layer`'s K and V for those positions in the
+ * reference's time-major layout [t][kvheads][head_dim] (src/ops.rs:84,93). */
+int qh_route_log(qh_ctx *ctx, size_t pos0, size_t n, uint32_t *ids);
+int qh_read_kv(qh_ctx *ctx, size_t layer, size_t pos0, size_t n, float *k, float *v);
+
+/* Fault injection for tests of the failure paths (no counterpart in the
+ * reference): QH_FAULT_ABORT raises the persistent step's abort flag, so the
+ * next step's waits give up at once (every kernel still exits normally) and
+ * the step fails with "device synchronisation timed out" and a reset. */
+#define QH_FAULT_ABORT 1u
+int qh_fault_inject(qh_ctx *ctx, uint32_t kind);
 
 /* Persistent-step timing (no counterpart in the reference): `steps` decode
  * steps continuing from the current position, with HIP events on the

@@ -428,8 +428,10 @@ out:
     return rc;
 }
 
-/* model.rs:217-302 */
-static int forward_inner(or_model *m, uint32_t token, float *logits_out, int threads) {
+/* model.rs:217-302.  vocab = 0 stops after the last layer (a checker's
+ * shortcut for long prompts whose intermediate logits are not compared: no
+ * final norm, vocab projection or finite check; the position still advances). */
+static int forward_inner(or_model *m, uint32_t token, float *logits_out, int threads, int vocab) {
     const or_config *c = &m->c;
     if (!(m->position < m->context)) return or_fail("context limit %zu reached", m->context);
     if (!(token < c->vocab)) return or_fail("token outside vocabulary");
@@ -441,6 +443,11 @@ static int forward_inner(or_model *m, uint32_t token, float *logits_out, int thr
     size_t kvcap = m->context * c->kvheads * c->head_dim;
     for (size_t i = 0; i < c->layers; i++)
         if (layer_body(m, i, x, m->position, &m->cache[i], kvcap, NULL, NULL, threads)) goto out;
+    if (!vocab) {
+        m->position += 1;
+        rc = 0;
+        goto out;
+    }
     if (or_rms(x, m->output_norm, H, c->eps)) goto out;
     const char *out = or_gguf_find(m->g, "output.weight") ? "output.weight" : "token_embd.weight";
     logits = malloc(c->vocab * sizeof(float));
@@ -457,8 +464,8 @@ out:
 }
 
 /* model.rs:209-216: roll back to a clean cache on any error */
-int or_model_forward(or_model *m, uint32_t token, float *logits, int threads) {
-    int rc = forward_inner(m, token, logits, threads);
+static int forward_checked(or_model *m, uint32_t token, float *logits, int threads, int vocab) {
+    int rc = forward_inner(m, token, logits, threads, vocab);
     if (rc) {
         char saved[512];
         snprintf(saved, sizeof saved, "%s", or_last_error());
@@ -466,6 +473,14 @@ int or_model_forward(or_model *m, uint32_t token, float *logits, int threads) {
         or_fail("%s", saved);
     }
     return rc;
+}
+
+int or_model_forward(or_model *m, uint32_t token, float *logits, int threads) {
+    return forward_checked(m, token, logits, threads, 1);
+}
+
+int or_model_step(or_model *m, uint32_t token, int threads) {
+    return forward_checked(m, token, NULL, threads, 0);
 }
 
 int or_layer_forward(or_model *m, size_t layer, float *x, size_t pos, const float *kprev,

@@ -99,6 +99,9 @@ void or_model_reset(or_model *m);                                    /* model.rs
 size_t or_model_position(const or_model *m);
 /* Threads as in or_packed_matvec.  logits may be NULL. */
 int or_model_forward(or_model *m, uint32_t token, float *logits, int threads); /* model.rs:209-302 */
+/* The same step without the final norm and vocab projection (checker shortcut
+ * for long prompts whose intermediate logits are not compared). */
+int or_model_step(or_model *m, uint32_t token, int threads);
 /* Backend::matvec surface: (name, expert) resolved as backend.rs:57-75. */
 int or_model_matvec(or_model *m, const char *name, int64_t expert, const float *x,
                     size_t cols, float *y, size_t rows, int threads);

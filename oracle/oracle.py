@@ -67,6 +67,7 @@ def _load():
         "or_model_reset": (None, [C.c_void_p]),
         "or_model_position": (sz, [C.c_void_p]),
         "or_model_forward": (i32, [C.c_void_p, u32, C.c_void_p, i32]),
+        "or_model_step": (i32, [C.c_void_p, u32, i32]),
         "or_model_matvec": (i32, [C.c_void_p, C.c_char_p, C.c_int64, _f32p, sz, _f32p, sz, i32]),
         "or_layer_forward": (i32, [C.c_void_p, sz, _f32p, sz, C.c_void_p, C.c_void_p,
                                    C.c_void_p, C.c_void_p, i32]),
@@ -319,6 +320,17 @@ class Model:
         _check(lib().or_model_forward(self.h, token, out.ctypes.data,
                                       self.threads if threads is None else threads))
         return out
+
+    def step(self, token, threads=None):
+        """forward() without the final norm and vocab projection: the layers,
+        the KV append and the position advance only (for long prompts whose
+        intermediate logits are not compared)."""
+        _check(lib().or_model_step(self.h, token, self.threads if threads is None else threads))
+
+    def routes(self):
+        """Top-k expert ids of every layer for the last step, [layers][top]."""
+        c = self.config
+        return np.stack([route(self.last_router(l), c["top"])[0] for l in range(c["layers"])])
 
     def matvec(self, name, expert, x, threads=None):
         x = np.ascontiguousarray(x, np.float32)

@@ -16,8 +16,11 @@ gfx950 device every entry raises.
 Import with importlib (the package directory name contains a hyphen):
     qh = importlib.import_module("qwen-30brust_amd")
 """
+import atexit
 import ctypes as C
 import os
+import sys
+import weakref
 
 import numpy as np
 
@@ -80,9 +83,9 @@ _SIGS = {
     "qh_argmax": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.POINTER(C.c_uint32)]),
     "qh_attention": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
                                C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p]),
-    "qh_forward": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.POINTER(C.c_uint32)]),
+    "qh_forward": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.c_size_t, C.POINTER(C.c_uint32)]),
     "qh_generate": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p,
-                              C.c_void_p]),
+                              C.c_void_p, C.c_size_t]),
     "qh_reset": (C.c_int, [C.c_void_p]),
     "qh_position": (C.c_int, [C.c_void_p, C.POINTER(C.c_size_t)]),
     "qh_layer_forward": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p,
@@ -91,7 +94,12 @@ _SIGS = {
     "qh_persistent": (C.c_int, [C.c_void_p, C.POINTER(C.c_int)]),
     "qh_set_persistent": (C.c_int, [C.c_void_p, C.c_int]),
     "qh_profile_decode": (C.c_int, [C.c_void_p, C.c_size_t, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
-    "qh_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.POINTER(C.c_uint32)]),
+    "qh_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t,
+                             C.POINTER(C.c_uint32)]),
+    "qh_model_generation": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint64)]),
+    "qh_fault_inject": (C.c_int, [C.c_void_p, C.c_uint32]),
+    "qh_route_log": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
+    "qh_read_kv": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p]),
     "qh_profile_step": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]),
     "qh_bench_matvec": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint32, C.c_size_t,
                                   C.c_size_t, C.c_size_t, C.c_size_t, C.POINTER(C.c_double)]),
@@ -118,6 +126,10 @@ def lib():
 
 def _ptr(a):
     return a.ctypes.data if a is not None and a.size else None
+
+
+def _cap(a):
+    return 0 if a is None else a.size
 
 
 def _f32(x):
@@ -165,7 +177,9 @@ class Sampler:
             lib().qh_sampler_destroy(self.h)
             self.h = None
 
-    __del__ = close
+    def __del__(self):
+        if not sys.is_finalizing():
+            self.close()
 
     def draw(self):
         """The stream's next rng.gen::<f32>()."""
@@ -182,21 +196,40 @@ class Sampler:
         return out.value
 
 
+_open_devices = weakref.WeakSet()
+
+
+def _close_all():
+    """Destroys every open context while the runtime is still whole: runs
+    from atexit, before the interpreter tears modules down and before the
+    HIP runtime's (or a profiler's) own exit handlers."""
+    for d in list(_open_devices):
+        d.close()
+
+
+atexit.register(_close_all)
+
+
 class Device:
-    """One engine context (one HIP stream) on a gfx950 device."""
+    """One engine context (one HIP stream) on a gfx950 device.  close()
+    releases it (idempotent); open devices are also closed at interpreter
+    exit, before the runtime's own teardown."""
 
     def __init__(self, device=0):
         h = C.c_void_p()
         if lib().qh_create(device, C.byref(h)) != 0:
             raise EngineError(lib().qh_last_error(None).decode())
         self.h = h
+        _open_devices.add(self)
 
     def close(self):
         if getattr(self, "h", None):
             lib().qh_destroy(self.h)
             self.h = None
 
-    __del__ = close
+    def __del__(self):
+        if not sys.is_finalizing():
+            self.close()
 
     def _check(self, rc):
         if rc != 0:
@@ -264,6 +297,45 @@ class Model:
         self.dev._check(lib().qh_model_config(self.dev.h, C.byref(c)))
         self.config = {n: getattr(c, n) for n, _ in _Config._fields_}
         self.context = context
+        self.generation = self._generation()
+
+    def _generation(self):
+        g = C.c_uint64()
+        self.dev._check(lib().qh_model_generation(self.dev.h, C.byref(g)))
+        return g.value
+
+    def _live(self):
+        """Raises when a later load on the same Device replaced this model
+        (the context holds one model at a time)."""
+        if self.dev.h is None:
+            raise EngineError("the device of this model was closed")
+        if self._generation() != self.generation:
+            raise EngineError("this model was replaced by a later load on the same device")
+
+    def route_log(self, pos0, n):
+        """Routed experts [n][layers][top] recorded for positions pos0..pos0+n
+        by the last step that processed them (diagnostics)."""
+        self._live()
+        c = self.config
+        out = np.zeros((max(n, 1), c["layers"], c["top"]), np.uint32)
+        self.dev._check(lib().qh_route_log(self.dev.h, pos0, n, _ptr(out)))
+        return out[:n]
+
+    def read_kv(self, layer, pos0, n):
+        """Layer `layer`'s K and V at positions pos0..pos0+n, time-major
+        [n][kvheads][head_dim] (the reference's layout)."""
+        self._live()
+        c = self.config
+        k = np.zeros((max(n, 1), c["kvheads"], c["head_dim"]), np.float32)
+        v = np.zeros_like(k)
+        self.dev._check(lib().qh_read_kv(self.dev.h, layer, pos0, n, _ptr(k), _ptr(v)))
+        return k[:n], v[:n]
+
+    def inject_fault(self, kind=1):
+        """Fault injection for failure-path tests (qh_fault_inject): kind 1
+        raises the persistent step's abort flag before the next step."""
+        self._live()
+        self.dev._check(lib().qh_fault_inject(self.dev.h, kind))
 
     @property
     def position(self):
@@ -283,13 +355,15 @@ class Model:
         return {"kind": kind.value, "dims": list(dims)[: rank.value]}
 
     def reset(self):
+        self._live()
         self.dev._check(lib().qh_reset(self.dev.h))
 
     def forward(self, token, want_logits=True):
         """== Model::forward: returns the logits (and keeps the argmax)."""
         lg = np.empty(self.config["vocab"], np.float32) if want_logits else None
         am = C.c_uint32()
-        self.dev._check(lib().qh_forward(self.dev.h, token, _ptr(lg), C.byref(am)))
+        self._live()
+        self.dev._check(lib().qh_forward(self.dev.h, token, _ptr(lg), _cap(lg), C.byref(am)))
         self.last_argmax = am.value
         return lg
 
@@ -309,7 +383,8 @@ class Model:
         p = np.ascontiguousarray(prompt, np.uint32)
         out = np.zeros(max(n_new, 1), np.uint32)
         lg = np.empty(self.config["vocab"], np.float32) if want_logits else None
-        self.dev._check(lib().qh_generate(self.dev.h, _ptr(p), p.size, n_new, _ptr(out), _ptr(lg)))
+        self._live()
+        self.dev._check(lib().qh_generate(self.dev.h, _ptr(p), p.size, n_new, _ptr(out), _ptr(lg), _cap(lg)))
         return (out[:n_new], lg) if want_logits else out[:n_new]
 
     def prefill(self, prompt, want_logits=True):
@@ -318,10 +393,12 @@ class Model:
         p = np.ascontiguousarray(prompt, np.uint32)
         lg = np.empty(self.config["vocab"], np.float32) if want_logits else None
         am = C.c_uint32()
-        self.dev._check(lib().qh_prefill(self.dev.h, _ptr(p), p.size, _ptr(lg), C.byref(am)))
+        self._live()
+        self.dev._check(lib().qh_prefill(self.dev.h, _ptr(p), p.size, _ptr(lg), _cap(lg), C.byref(am)))
         return am.value, lg
 
     def layer_forward(self, layer, x, pos, kprev, vprev):
+        self._live()
         x = np.array(x, np.float32)
         top = self.config["top"]
         ids = np.zeros(top, np.uint32)
@@ -354,11 +431,13 @@ class Model:
     def profile_decode(self, steps):
         """Mean GPU ms of (the embedding kernel, the k_decode launch) per token
         of the persistent step, from HIP events around each kernel."""
+        self._live()
         e, d = C.c_double(), C.c_double()
         self.dev._check(lib().qh_profile_decode(self.dev.h, steps, C.byref(e), C.byref(d)))
         return e.value, d.value
 
     def bench_decode(self, warmup, steps):
+        self._live()
         ms = C.c_double()
         self.dev._check(lib().qh_bench_decode(self.dev.h, warmup, steps, C.byref(ms)))
         return ms.value

@@ -219,7 +219,7 @@ int cmd_logits(const Args& a) {
     const auto t0 = std::chrono::steady_clock::now();
     for (uint32_t id : a.tokens) {
         uint32_t am = 0;
-        if (qh_forward(ctx, id, logits.data(), &am) != 0) throw Fail(last_error(ctx));
+        if (qh_forward(ctx, id, logits.data(), logits.size(), &am) != 0) throw Fail(last_error(ctx));
     }
     const double seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
     qh_stats_t st;

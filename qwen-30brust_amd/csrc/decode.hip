@@ -914,11 +914,12 @@ __device__ __forceinline__ bool phase_xr2(const DecodeArgs& A, DecodeLds& S, con
         put_l(lbuf(A.lx2, kDecodeStrideX2, c.X) + kRowsWg * c.j + c.tid, x2, ptag(A, l, 7));
         if (last && c.X == 0) A.a.x[kRowsWg * c.j + c.tid] = x2;  // x after the launch, for the host
     }
-    // the routing of the layer, for the host
+    // the routing of the layer, for the host (and the routing log)
     if (c.b == 0) {
         if (c.tid < c.top) {
             A.a.ids[c.tid] = S.ids[c.tid];
             A.a.wts[c.tid] = S.wts[c.tid];
+            A.a.route_log[((size_t)c.pos * A.dm.layers + l) * c.top + c.tid] = S.ids[c.tid];
         }
         if (c.tid < c.E) A.a.logits_r[c.tid] = S.lg[c.tid];
     }
@@ -1101,6 +1102,12 @@ __global__ __launch_bounds__(kDT) void k_decode(DecodeArgs A) {
     __syncthreads();
     if (c.pos >= dm.ctx || (err0 & kErrToken)) {
         if (c.b == 0 && c.tid == 0 && c.pos >= dm.ctx) atomicOr(&A.a.st->err, kErrContext);
+        return;
+    }
+    if (ld_sys_u(A.abort_flag) != 0) {
+        // a raised abort flag (a wait of an earlier step that gave up, or the
+        // host's fault injection) fails this step before it starts
+        if (c.b == 0 && c.tid == 0) atomicOr(&A.a.st->err, kErrSync);
         return;
     }
     if (xcc_id() != c.X) {

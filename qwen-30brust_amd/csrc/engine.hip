@@ -60,7 +60,8 @@ __global__ void k_pf_attn(const _Float16*, const _Float16*, const _Float16*, uin
                           uint32_t, uint32_t, _Float16*);
 __global__ void k_pf_kvh(const float*, const float*, uint32_t, uint32_t, uint32_t, uint32_t, _Float16*, _Float16*);
 __global__ void k_pf_router(const float*, DevMat, uint32_t, uint32_t, uint32_t, float*);
-__global__ void k_pf_topk(const float*, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t*, float*, DevState*);
+__global__ void k_pf_topk(const float*, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t*, float*, DevState*, uint32_t*,
+                          uint32_t, uint32_t, uint32_t);
 __global__ void k_pf_group(const uint32_t*, uint32_t, uint32_t, uint32_t, uint32_t*, uint32_t*, uint32_t*, uint32_t*,
                            uint32_t*, uint32_t*);
 __global__ void k_pf_combine(float*, const float*, const float*, uint32_t, uint32_t, const float*, float, _Float16*);
@@ -165,6 +166,7 @@ struct qh_ctx {
 
     // model
     bool loaded = false;
+    uint64_t generation = 0;  // models loaded so far (qh_model_generation)
     Config cfg{};
     ModelDims dm{};
     uint64_t packed = 0;
@@ -390,6 +392,7 @@ void alloc_acts(qh_ctx* c) {
         {kMaxGrid * 4, (void**)&a.fin_key},
         {kMaxGrid * 4, (void**)&a.fin_idx},
         {pad32h(c->context + 2) * 4, (void**)&a.tokens},
+        {(uint64_t)c->context * d.layers * d.top * 4, (void**)&a.route_log},
         {256, (void**)&a.st},
     };
     size_t total = 0;
@@ -710,6 +713,7 @@ void load_image(qh_ctx* c, const uint8_t* data, size_t len, size_t context) {
     if (cfg.head_dim > 512) throw Error("head_dim above 512 is not supported by the device kernels");
     if (cfg.top > 1024) throw Error("expert_used_count above 1024 is not supported");
     c->drop_model();
+    c->generation += 1;
     c->cfg = cfg;
     c->context = context;
     c->packed = g.packed_bytes();
@@ -717,6 +721,7 @@ void load_image(qh_ctx* c, const uint8_t* data, size_t len, size_t context) {
     d.hidden = (uint32_t)cfg.hidden; d.heads = (uint32_t)cfg.heads; d.kvheads = (uint32_t)cfg.kvheads;
     d.head_dim = (uint32_t)cfg.head_dim; d.experts = (uint32_t)cfg.experts; d.top = (uint32_t)cfg.top;
     d.ff = (uint32_t)cfg.intermediate; d.vocab = (uint32_t)cfg.vocab; d.ctx = (uint32_t)context;
+    d.layers = (uint32_t)cfg.layers;
     d.eps = cfg.eps;
     // every tensor to HBM once, repacked into the device row layout
     for (auto& kv : g.tensors) {
@@ -754,6 +759,7 @@ void load_image(qh_ctx* c, const uint8_t* data, size_t len, size_t context) {
     for (uint64_t i = 0; i < cfg.layers; i++) {
         std::string p = "blk." + std::to_string(i) + ".";
         LayerW L{};
+        L.index = (uint32_t)i;
         L.q = mat(p + "attn_q.weight");
         L.k = mat(p + "attn_k.weight");
         L.v = mat(p + "attn_v.weight");
@@ -797,6 +803,13 @@ void load_image(qh_ctx* c, const uint8_t* data, size_t len, size_t context) {
 
 void need_model(qh_ctx* c) {
     if (!c->loaded) throw Error("no model loaded");
+}
+
+// A caller's logits buffer must hold the whole vocabulary of the loaded model.
+void need_logits_room(const qh_ctx* c, const float* logits, size_t cap) {
+    if (logits && cap < c->cfg.vocab)
+        throw Error("logits buffer holds " + std::to_string(cap) + " floats, the model has a vocabulary of " +
+                    std::to_string(c->cfg.vocab));
 }
 
 // Writes the device step state from the host mirror.
@@ -1045,7 +1058,7 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
     hipLaunchKernelGGL(k_pf_router, dim3((S + 15) / 16, kPfRouterSplit), dim3(kBlock), 0, c->s, P.Xn32, L.router,
                        S, H, d.experts, P.LR);
     hipLaunchKernelGGL(k_pf_topk, dim3((S + kWaves - 1) / kWaves), dim3(kBlock), 0, c->s, P.LR, kPfRouterSplit, S,
-                       d.experts, d.top, P.ids, P.wts, c->acts.st);
+                       d.experts, d.top, P.ids, P.wts, c->acts.st, c->acts.route_log, d.layers, (uint32_t)l, p0);
     hipLaunchKernelGGL(k_pf_group, dim3(1), dim3(1024), 0, c->s, P.ids, S * d.top, d.top, d.experts, P.goff, P.tok,
                        P.asg, P.te, P.tm, P.ntile);
     const ExpertTiles T{P.goff, P.tok, P.asg, P.te, P.tm, P.ntile};
@@ -1506,10 +1519,11 @@ int qh_attention(qh_ctx* c, const float* q, const float* k, const float* v, size
     });
 }
 
-int qh_forward(qh_ctx* c, uint32_t token, float* logits, uint32_t* argmax) {
+int qh_forward(qh_ctx* c, uint32_t token, float* logits, size_t logits_cap, uint32_t* argmax) {
     return guarded(c, [&] {
         double t0 = now_ms();
         need_model(c);
+        need_logits_room(c, logits, logits_cap);
         if (!(c->pos < c->context)) {
             reset_model(c);
             throw Error("context limit " + std::to_string(c->context) + " reached");
@@ -1533,10 +1547,11 @@ int qh_forward(qh_ctx* c, uint32_t token, float* logits, uint32_t* argmax) {
 }
 
 int qh_generate(qh_ctx* c, const uint32_t* prompt, size_t n_prompt, size_t n_new, uint32_t* out_tokens,
-                float* logits_last) {
+                float* logits_last, size_t logits_cap) {
     return guarded(c, [&] {
         double t0 = now_ms();
         need_model(c);
+        need_logits_room(c, logits_last, logits_cap);
         if (n_prompt == 0) throw Error("empty prompt");
         const size_t steps = n_prompt + (n_new ? n_new - 1 : 0);
         if (c->pos + steps > c->context) throw Error("prompt + max-tokens exceed --ctx");
@@ -1558,10 +1573,11 @@ int qh_generate(qh_ctx* c, const uint32_t* prompt, size_t n_prompt, size_t n_new
     });
 }
 
-int qh_prefill(qh_ctx* c, const uint32_t* prompt, size_t n, float* logits, uint32_t* argmax) {
+int qh_prefill(qh_ctx* c, const uint32_t* prompt, size_t n, float* logits, size_t logits_cap, uint32_t* argmax) {
     return guarded(c, [&] {
         double t0 = now_ms();
         need_model(c);
+        need_logits_room(c, logits, logits_cap);
         if (n == 0) throw Error("empty prompt");
         if (c->pos + n > c->context) throw Error("prompt + max-tokens exceed --ctx");
         for (size_t i = 0; i < n; i++)
@@ -1655,6 +1671,51 @@ int qh_layer_forward(qh_ctx* c, size_t layer, float* x, size_t pos, const float*
         DevState st = get_state(c);
         reset_model(c);
         if (st.err) fail_step(c, st.err);
+    });
+}
+
+int qh_route_log(qh_ctx* c, size_t pos0, size_t n, uint32_t* ids) {
+    return guarded(c, [&] {
+        need_model(c);
+        if (pos0 + n > c->context) throw Error("routing log range beyond the context");
+        const size_t row = (size_t)c->dm.layers * c->dm.top;
+        HIP_OK(hipMemcpyAsync(ids, c->acts.route_log + pos0 * row, n * row * 4, hipMemcpyDeviceToHost, c->s));
+        sync(c);
+    });
+}
+
+int qh_read_kv(qh_ctx* c, size_t layer, size_t pos0, size_t n, float* k, float* v) {
+    return guarded(c, [&] {
+        need_model(c);
+        if (layer >= c->layers.size()) throw Error("layer out of range");
+        if (pos0 + n > c->context) throw Error("KV range beyond the context");
+        const ModelDims& d = c->dm;
+        const LayerW& L = c->layers[layer];
+        // device head-major [kvhead][ctx][d] -> time-major [t][kvhead][d]
+        for (uint32_t h = 0; h < d.kvheads; h++) {
+            const size_t src = ((size_t)h * c->context + pos0) * d.head_dim;
+            HIP_OK(hipMemcpy2DAsync(k + (size_t)h * d.head_dim, (size_t)d.kvheads * d.head_dim * 4, L.kcache + src,
+                                    d.head_dim * 4, d.head_dim * 4, n, hipMemcpyDeviceToHost, c->s));
+            HIP_OK(hipMemcpy2DAsync(v + (size_t)h * d.head_dim, (size_t)d.kvheads * d.head_dim * 4, L.vcache + src,
+                                    d.head_dim * 4, d.head_dim * 4, n, hipMemcpyDeviceToHost, c->s));
+        }
+        sync(c);
+    });
+}
+
+int qh_model_generation(const qh_ctx* c, uint64_t* out) {
+    *out = c->generation;
+    return 0;
+}
+
+int qh_fault_inject(qh_ctx* c, uint32_t kind) {
+    return guarded(c, [&] {
+        need_model(c);
+        if (kind != QH_FAULT_ABORT) throw Error("unknown fault kind " + std::to_string(kind));
+        if (!c->persist) throw Error("the abort fault needs the persistent step");
+        const uint32_t one = 1;
+        HIP_OK(hipMemcpyAsync(c->dargs.abort_flag, &one, 4, hipMemcpyHostToDevice, c->s));
+        sync(c);
     });
 }
 

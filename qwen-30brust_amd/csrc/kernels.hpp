@@ -51,11 +51,13 @@ struct LayerW {
     // ([experts][heads*d] f32), so that router logit e of x' = x + Wo a is
     // s (sum_j router[e][j] ffn_norm[j] x[j] + F[e] . a)
     const float* rfold;
+    uint32_t index;  // layer number (the routing log's row)
 };
 
 struct ModelDims {
     uint32_t hidden, heads, kvheads, head_dim, experts, top, ff, vocab, ctx;
     float eps;
+    uint32_t layers;
 };
 
 // Scratch activations of one step.
@@ -76,6 +78,7 @@ struct Acts {
     uint32_t* fin_key;   // [final blocks] vocab argmax partial keys
     uint32_t* fin_idx;   // [final blocks]
     uint32_t* tokens;    // [ctx+2]
+    uint32_t* route_log; // [ctx][layers][top] routed experts of every layer at every position (diagnostics)
     const float2* rope;  // [ctx][d/2] (cos, sin)
     DevState* st;
 };

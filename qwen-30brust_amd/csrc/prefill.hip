@@ -475,7 +475,9 @@ __global__ __launch_bounds__(kBlock) void k_pf_router(const float* Xn, DevMat R,
 // in rank order (ops.rs:29-44).  E <= 128.  The logits are the sum of the
 // router's nks partial sums, added in split order.
 __global__ __launch_bounds__(kBlock) void k_pf_topk(const float* LR, uint32_t nks, uint32_t S, uint32_t E,
-                                                    uint32_t top, uint32_t* ids, float* wts, DevState* st) {
+                                                    uint32_t top, uint32_t* ids, float* wts, DevState* st,
+                                                    uint32_t* route_log, uint32_t layers, uint32_t layer,
+                                                    uint32_t p0) {
     const uint32_t lane = threadIdx.x & 63, t = blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (t >= S) return;  // wave-uniform
     float v0 = lane < E ? LR[(size_t)t * E + lane] : 0.f, v1 = lane + 64 < E ? LR[(size_t)t * E + lane + 64] : 0.f;
@@ -517,6 +519,7 @@ __global__ __launch_bounds__(kBlock) void k_pf_topk(const float* LR, uint32_t nk
     if (lane < top) {
         ids[(size_t)t * top + lane] = sid;
         wts[(size_t)t * top + lane] = ex / sum;
+        route_log[((size_t)(p0 + t) * layers + layer) * top + lane] = sid;  // routing log (diagnostics)
     }
 }
 

@@ -981,9 +981,11 @@ __global__ __launch_bounds__(kGateupThreads) void k_gateup(LayerW L, Acts a, Mod
     __syncthreads();
     QH_MARK(3, 3);
     if (blockIdx.x == 0) {
+        const uint32_t pos = a.st->pos;
         for (uint32_t i = threadIdx.x; i < top; i += NT) {
             a.ids[i] = sid[i];
             a.wts[i] = sv[i];
+            if (pos < dm.ctx) a.route_log[((size_t)pos * dm.layers + L.index) * top + i] = sid[i];
         }
         if (threadIdx.x < E) a.logits_r[threadIdx.x] = lv;
     }

@@ -1,5 +1,6 @@
 """GPU parity of the device-resident token step against the oracle and the
 reference's own fixture model (tests/model.rs:48-118), through the C ABI."""
+import ctypes as C
 import importlib
 import json
 import os
@@ -237,3 +238,68 @@ def test_persistent_profile_decode(dev, layer30b_q4k):
     m.persistent = False
     with pytest.raises(engine.EngineError):
         m.profile_decode(1)
+
+
+def test_persistent_step_error_paths_and_rollback(dev):
+    """The persistent step's failure paths (src/model.rs:209-224: any error
+    resets the KV cache and the position): the context limit, a token outside
+    the vocabulary, and an abandoned step (the abort flag raised from the
+    host: every wait of the step gives up and the kernels exit normally).
+    Each raises, leaves position 0, and a clean re-run afterwards gives the
+    first run's logits bit for bit."""
+    spec = synth.layer30b(more_bits=False, context=8)
+    img = synth.build_image(spec, threads=8)
+    m = engine.Model(img, spec.context, device=dev)
+    assert m.persistent
+    toks = [5, 17, 3, 250, 9, 0, 77, 128]
+    first = [m.forward(t) for t in toks]
+    assert m.position == 8
+    with pytest.raises(engine.EngineError, match="context limit 8 reached"):
+        m.forward(1)
+    assert m.position == 0
+    for t, ref in zip(toks[:3], first):
+        assert np.array_equal(m.forward(t), ref)
+    with pytest.raises(engine.EngineError, match="token outside vocabulary"):
+        m.forward(spec.vocab)
+    assert m.position == 0
+    m.forward(toks[0])
+    m.inject_fault(1)
+    with pytest.raises(engine.EngineError, match="synchronisation"):
+        m.forward(toks[1])
+    assert m.position == 0
+    for t, ref in zip(toks, first):
+        assert np.array_equal(m.forward(t), ref)
+    with pytest.raises(engine.EngineError, match="exceed"):
+        m.generate(toks, 4)
+    m.reset()
+    ids = m.generate(toks[:4], 4)
+    m.reset()
+    for t in toks[:4]:
+        m.forward(t)
+    step = [m.last_argmax]
+    for _ in range(3):
+        m.forward(step[-1])
+        step.append(m.last_argmax)
+    assert list(ids) == step
+
+
+def test_model_replaced_by_a_later_load_raises(dev):
+    """The context holds one model: a Model whose weights a later load on the
+    same Device replaced refuses to run (it would otherwise run the other
+    model and size its logits from the old vocabulary); the C ABI refuses a
+    logits buffer smaller than the loaded vocabulary."""
+    m1 = engine.Model(FIXTURE, 4, device=dev)
+    m1.forward(1)
+    spec = synth.tiny_k()
+    m2 = engine.Model(synth.build_image(spec, threads=8), spec.context, device=dev)
+    assert m2.config["vocab"] > m1.config["vocab"]
+    with pytest.raises(engine.EngineError, match="replaced by a later load"):
+        m1.forward(1)
+    with pytest.raises(engine.EngineError, match="replaced by a later load"):
+        m1.generate([1, 2], 2)
+    m2.forward(3)
+    buf = np.zeros(10, np.float32)
+    am = C.c_uint32()
+    rc = engine.lib().qh_forward(dev.h, 1, buf.ctypes.data, buf.size, C.byref(am))
+    assert rc != 0
+    assert b"logits buffer holds 10 floats" in engine.lib().qh_last_error(dev.h)

@@ -1,0 +1,213 @@
+"""GPU parity at the configurations' own sizes, through the C ABI.
+
+Config 4 (src/main.rs:250-282, src/model.rs:209-302): the random-init
+48-layer Qwen3-30B-A3B Q4_K_M model, a 512-token uniform random prompt run
+through the exact token step, then 64 greedy tokens chained on the device:
+the ids must equal the oracle's greedy loop, and the persistent step's logits
+at decode steps 1-4 and 60-63 must be within 1e-4 (infinity-norm relative)
+of the oracle's at vocabulary 151,936 (the random-init model's greedy stream
+settles on few ids, so the logits carry most of the check).
+
+Config 5 (the batched prefill replacing src/main.rs:250-256): a 2,048-token
+prompt through qh_prefill, on (a) a 4-layer model at 30B shapes with the full
+vocabulary against the oracle's sequential forward, and (b) the 48-layer
+model against the exact persistent decode path run token by token on the
+same prompt.  fp16 operands cannot meet 1e-4, so the bar is 1e-2 on the last
+prompt token's logits.  The fp16 path's router logits carry about 1e-3
+relative noise, so it picks another expert set where the reference's
+8th/9th router logits nearly tie (about 2 % of (token, layer) pairs for
+random routers); a flip changes that token's later layers, which can then
+flip at wider gaps.  Routing is therefore compared for every (token, layer):
+a token's first disagreement (the "primary" one) must sit on a near-tie of
+the reference side, the flip rates are bounded, and the logits and KV bars
+apply to what no flip reached.
+"""
+import importlib
+import os
+import time
+
+import numpy as np
+import pytest
+
+import oracle
+
+engine = importlib.import_module("qwen-30brust_amd")
+synth = importlib.import_module("qwen-30brust_amd.synth")
+
+pytestmark = pytest.mark.gpu
+THREADS = min(16, os.cpu_count() or 1)
+REL = 1e-4           # decode path vs the FP32 oracle
+PF_TOL = 1e-2        # batched prefill (fp16 operands) vs an FP32 path
+NEAR_TIE = 1e-2      # 8th/9th router logit gap, relative to the largest |logit|, that fp16 noise may flip
+MAX_PAIR_FLIPS = 0.05  # most (token, layer) routing disagreements, as a fraction of the pairs
+MAX_TOKEN_FLIPS_4 = 0.15  # most tokens with a disagreement in any of 4 layers
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+def rel_err(got, ref):
+    return float(np.max(np.abs(got.astype(np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def token_rel_err(got, ref):
+    """Largest over tokens of ||got_t - ref_t||_2 / ||ref_t||_2 (rows = tokens)."""
+    g = got.reshape(got.shape[0], -1).astype(np.float64)
+    r = ref.reshape(ref.shape[0], -1).astype(np.float64)
+    return float(np.max(np.linalg.norm(g - r, axis=1) / np.maximum(np.linalg.norm(r, axis=1), 1e-30)))
+
+
+def first_flip(dis):
+    """Layer of each token's first routing disagreement (-1: none)."""
+    return np.array([int(np.argmax(r)) if r.any() else -1 for r in dis])
+
+
+def router_gap(logits, top):
+    s = np.sort(logits)[::-1]
+    return float(s[top - 1] - s[top]) / float(np.max(np.abs(s)))
+
+
+@pytest.fixture(scope="module")
+def dev():
+    d = engine.Device(0)
+    yield d
+    d.close()
+
+
+@pytest.mark.timeout(1200)
+def test_config4_prompt512_greedy64_and_decode_logits(dev):
+    spec = synth.qwen30b(context=640)
+    t0 = time.time()
+    img = synth.build_image(spec, threads=THREADS)
+    log(f"built the 48-layer image in {time.time() - t0:.1f}s")
+    m = engine.Model(img, spec.context, device=dev)
+    assert m.persistent
+    prompt = np.random.default_rng(512).integers(0, spec.vocab, 512).astype(np.uint32)
+    got = m.generate(prompt, 64)
+    # the persistent step's logits at four decode steps, continuing the same sequence
+    m.reset()
+    first = m.generate(prompt, 1)
+    assert int(first[0]) == int(got[0])
+    dev_logits = {i: m.forward(int(got[i - 1])) for i in range(1, 5)}
+    for i in range(5, 64):
+        lg = m.forward(int(got[i - 1]), want_logits=i >= 60)
+        if i >= 60:
+            dev_logits[i] = lg
+    om = oracle.Model(oracle.Gguf(img), spec.context, threads=THREADS)
+    t0 = time.time()
+    for i, t in enumerate(prompt[:-1]):
+        om.step(int(t))
+        if i % 64 == 63:
+            log(f"oracle prompt token {i + 1}/512 ({time.time() - t0:.0f}s)")
+    ref = om.forward(int(prompt[-1]))
+    ref_ids, margins, errs = [], [], []
+    for i in range(64):
+        s = np.partition(ref, -2)[-2:]
+        margins.append(float(s[1] - s[0]))
+        ref_ids.append(oracle.greedy(ref))
+        if i in dev_logits:
+            errs.append(rel_err(dev_logits[i], ref))
+            log(f"decode step {i}: persistent-step logits rel err {errs[-1]:.2e}")
+        if i + 1 < 64:
+            ref = om.forward(ref_ids[-1])
+        log(f"step {i}: oracle {ref_ids[-1]} device {int(got[i])} top-1/top-2 margin {margins[-1]:.3e}")
+    log(f"smallest margin {min(margins):.3e}; distinct ids {len(set(ref_ids))}; max logits rel err {max(errs):.2e}")
+    assert max(errs) <= REL
+    assert list(got) == ref_ids
+
+
+@pytest.fixture(scope="module")
+def model4():
+    """Config 5 at 4 layers: 30B shapes, full vocabulary 151,936."""
+    spec = synth.qwen30b(layers=4, context=2048 + 8)
+    return spec, synth.build_image(spec, threads=THREADS)
+
+
+@pytest.mark.timeout(900)
+def test_config5_prefill_2048_vs_oracle_4_layers(dev, model4):
+    spec, img = model4
+    n = 2048
+    prompt = np.random.default_rng(2048).integers(0, spec.vocab, n).astype(np.uint32)
+    m = engine.Model(img, spec.context, device=dev)
+    am, lg = m.prefill(prompt)
+    dev_routes = m.route_log(0, n)
+    om = oracle.Model(oracle.Gguf(img), spec.context, threads=THREADS)
+    ref_routes = np.zeros_like(dev_routes)
+    gaps = np.zeros((n, spec.layers))
+    t0 = time.time()
+    for t in range(n):
+        if t + 1 < n:
+            om.step(int(prompt[t]))
+        else:
+            ref = om.forward(int(prompt[t]))
+        ref_routes[t] = om.routes()
+        gaps[t] = [router_gap(om.last_router(l), spec.top) for l in range(spec.layers)]
+        if t % 256 == 255:
+            log(f"oracle token {t + 1}/{n} ({time.time() - t0:.0f}s)")
+    # a disagreement: the two paths chose different expert sets for (token, layer)
+    dis = np.array([[set(dev_routes[t, l]) != set(ref_routes[t, l]) for l in range(spec.layers)] for t in range(n)])
+    ff = first_flip(dis)
+    flipped = np.nonzero(ff >= 0)[0]
+    primary_gaps = gaps[flipped, ff[flipped]]
+    err = rel_err(lg, ref)
+    n_dis = int(dis.sum())
+    log(f"2048-token prefill, 4 layers: last-token logits rel err {err:.2e}; routing disagreements "
+        f"{n_dis} of {dis.size} (token, layer) pairs, in {flipped.size} tokens; largest oracle gap at a "
+        f"token's first disagreement {primary_gaps.max() if flipped.size else 0:.2e}; greedy id device {am} "
+        f"oracle {oracle.greedy(ref)}; last token flipped: {bool(ff[-1] >= 0)}")
+    assert n_dis <= MAX_PAIR_FLIPS * dis.size
+    assert flipped.size <= MAX_TOKEN_FLIPS_4 * n
+    assert flipped.size == 0 or primary_gaps.max() <= NEAR_TIE
+    if ff[-1] < 0:
+        assert err <= PF_TOL
+    s = np.sort(ref)
+    if ff[-1] < 0 and float(s[-1] - s[-2]) > PF_TOL * float(np.max(np.abs(ref))):
+        assert am == oracle.greedy(ref)
+
+
+@pytest.mark.timeout(900)
+def test_config5_prefill_2048_vs_exact_decode_48_layers(dev):
+    spec = synth.qwen30b(context=2048 + 8)
+    img = synth.build_image(spec, threads=THREADS)
+    n = 2048
+    prompt = np.random.default_rng(4096).integers(0, spec.vocab, n).astype(np.uint32)
+    m = engine.Model(img, spec.context, device=dev)
+    assert m.persistent
+    t0 = time.time()
+    am_pf, lg_pf = m.prefill(prompt)
+    log(f"prefill {n} tokens: {time.time() - t0:.2f}s")
+    routes_pf = m.route_log(0, n)
+    kv_pf = [m.read_kv(l, 0, n) for l in range(spec.layers)]
+    m.reset()
+    t0 = time.time()
+    ids, lg_dec = m.generate(prompt, 1, want_logits=True)
+    log(f"exact decode path, {n} tokens one step each: {time.time() - t0:.2f}s")
+    routes_dec = m.route_log(0, n)
+    dis = np.array([[set(routes_pf[t, l]) != set(routes_dec[t, l]) for l in range(spec.layers)] for t in range(n)])
+    ff = first_flip(dis)
+    n_dis = int(dis.sum())
+    per_layer = dis.sum(axis=0)
+    # KV of layer l for the tokens no flip reached before layer l (a flip at
+    # layer l' < l changes that token's input to layer l)
+    kv_err, kv_all = [], []
+    for l in range(spec.layers):
+        k, v = m.read_kv(l, 0, n)
+        clean = (ff < 0) | (ff >= l)
+        kv_err.append(max(token_rel_err(kv_pf[l][0][clean], k[clean]), token_rel_err(kv_pf[l][1][clean], v[clean])))
+        kv_all.append(max(token_rel_err(kv_pf[l][0], k), token_rel_err(kv_pf[l][1], v)))
+    err = rel_err(lg_pf, lg_dec)
+    log(f"2048-token prefill vs exact decode, 48 layers: last-token logits rel err {err:.2e}; "
+        f"greedy id prefill {am_pf} decode {int(ids[0])}; last token flipped at layer {int(ff[-1])}")
+    log(f"routing disagreements {n_dis} of {dis.size} (token, layer) pairs ({n_dis / dis.size:.2%}), "
+        f"in {int((ff >= 0).sum())} of {n} tokens; first flips per layer "
+        f"{np.bincount(ff[ff >= 0], minlength=spec.layers).tolist()}; all per layer {per_layer.tolist()}")
+    log(f"KV per-token rel err (2-norm) per layer, tokens no flip reached: max {max(kv_err):.2e} "
+        f"(layer {int(np.argmax(kv_err))}); all tokens: max {max(kv_all):.2e}")
+    assert n_dis <= MAX_PAIR_FLIPS * dis.size
+    assert max(kv_err) <= PF_TOL
+    if ff[-1] < 0:
+        assert err <= PF_TOL
+        s = np.sort(lg_dec)
+        if float(s[-1] - s[-2]) > PF_TOL * float(np.max(np.abs(lg_dec))):
+            assert am_pf == int(ids[0])
