@@ -129,6 +129,18 @@ int qh_argmax(qh_ctx *ctx, const float *logits, size_t n, uint32_t *out);
  * klen = t*kvheads*d floats. */
 int qh_attention(qh_ctx *ctx, const float *q, const float *k, const float *v, size_t klen,
                  size_t heads, size_t kvheads, size_t d, float *out);
+/* qh_attention on device buffers that allocates nothing (no counterpart in
+ * the reference; for callers that cannot allocate: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  q, k, v
+ * and out are device pointers in qh_attention's layouts; the kernel's chunk
+ * partials and counters live in a fixed 1 MiB device array of the library
+ * (one per GPU), so shapes needing more (heads x chunks x (head_dim + 2)
+ * floats plus kvheads counters) are refused with an error.  stream NULL:
+ * the context's stream, and the call returns when out is written; otherwise
+ * the work is enqueued on that HIP stream and the call returns at once.
+ * Calls that overlap on one GPU share the array and race. */
+int qh_attention_noalloc(qh_ctx *ctx, const float *q, const float *k, const float *v, size_t klen,
+                         size_t heads, size_t kvheads, size_t d, float *out, void *stream);
 
 /* == Model::forward (src/model.rs:209-216): one causal token step on the
  * device (embedding, every layer, KV append, final norm, vocab projection,

@@ -83,6 +83,8 @@ _SIGS = {
     "qh_argmax": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.POINTER(C.c_uint32)]),
     "qh_attention": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
                                C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p]),
+    "qh_attention_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
+                                       C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p]),
     "qh_forward": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.c_size_t, C.POINTER(C.c_uint32)]),
     "qh_generate": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p,
                               C.c_void_p, C.c_size_t]),

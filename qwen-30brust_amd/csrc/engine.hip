@@ -12,6 +12,7 @@
 #include <fcntl.h>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -157,6 +158,34 @@ uint64_t groups_host(uint64_t rows, uint64_t cols, int R) {
 }
 
 }  // namespace
+
+// ------------------------------------------------ no-allocation scratch --
+// Device memory of qh_attention_noalloc: the chunk partials
+// [heads][chunks][d+2] and the last-arrival counters [kvheads] of
+// k_attention_api, at most kNoAllocScratchBytes.  Every GPU the library runs
+// on holds its own copy for the life of the process; host code uses only the
+// per-device address that hipGetSymbolAddress returns (the array's name is a
+// host-side stand-in, not a device address).
+namespace {
+constexpr size_t kNoAllocScratchBytes = 1u << 20;
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_scratch_mu;
+std::array<void*, kNoAllocMaxDevices> g_scratch_ptr{};
+}  // namespace
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+// Resolves this device's copy of `scratch` once per device (called by
+// qh_create with the device current).
+static void noalloc_init(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (device < 0 || device >= kNoAllocMaxDevices) throw Error("device index beyond the scratch table");
+    if (g_scratch_ptr[device]) return;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+        throw Error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_ptr[device] = p;
+}
 
 struct qh_ctx {
     int device = 0;
@@ -1189,6 +1218,7 @@ int qh_create(int device, qh_ctx** out) {
         if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
             throw Error(std::string("device is ") + p.gcnArchName + ", this engine is built for gfx950");
         HIP_OK(hipSetDevice(device));
+        noalloc_init(device);
         auto c = std::make_unique<qh_ctx>();
         c->device = device;
         const char* ng = std::getenv("QH_NO_GRAPH");
@@ -1473,19 +1503,36 @@ int qh_argmax(qh_ctx* c, const float* logits, size_t n, uint32_t* out) {
     });
 }
 
+// Launch geometry of k_attention_api for `heads` query heads over T keys:
+// keys per chunk tc (the LDS budget), chunks nch, dynamic LDS bytes.
+struct AttnGeo {
+    size_t T;
+    uint32_t tc, nch;
+    size_t lds;
+};
+AttnGeo attn_geometry(size_t klen, size_t heads, size_t kvheads, size_t d) {
+    if (!(kvheads > 0 && heads > 0 && d > 0 && heads % kvheads == 0 && klen % (kvheads * d) == 0))
+        throw Error("attention shape mismatch");
+    AttnGeo g{};
+    g.T = klen / (kvheads * d);
+    if (g.T == 0) throw Error("empty KV cache");
+    const uint32_t G = (uint32_t)(heads / kvheads);
+    auto lds = [&](uint32_t tc) { return (size_t)(G * d + tc * (d + 1) + tc * d + G * tc + 2 * G) * 4; };
+    g.tc = 64;
+    while (g.tc > 1 && lds(g.tc) > 60 * 1024) g.tc /= 2;
+    if (lds(g.tc) > 64 * 1024) throw Error("attention shape exceeds the LDS budget");
+    g.nch = (uint32_t)((g.T + g.tc - 1) / g.tc);
+    g.lds = lds(g.tc);
+    return g;
+}
+
 int qh_attention(qh_ctx* c, const float* q, const float* k, const float* v, size_t klen, size_t heads,
                  size_t kvheads, size_t d, float* out) {
     return guarded(c, [&] {
-        if (!(kvheads > 0 && heads > 0 && d > 0 && heads % kvheads == 0 && klen % (kvheads * d) == 0))
-            throw Error("attention shape mismatch");
-        const size_t T = klen / (kvheads * d);
-        if (T == 0) throw Error("empty KV cache");
-        const uint32_t G = (uint32_t)(heads / kvheads);
-        auto lds = [&](uint32_t tc) { return (size_t)(G * d + tc * (d + 1) + tc * d + G * tc + 2 * G) * 4; };
-        uint32_t tc = 64;
-        while (tc > 1 && lds(tc) > 60 * 1024) tc /= 2;
-        if (lds(tc) > 64 * 1024) throw Error("attention shape exceeds the LDS budget");
-        const uint32_t nch = (uint32_t)((T + tc - 1) / tc);
+        const AttnGeo geo = attn_geometry(klen, heads, kvheads, d);
+        const size_t T = geo.T;
+        const uint32_t tc = geo.tc, nch = geo.nch;
+        auto lds = [&](uint32_t) { return geo.lds; };
         const float* qd = upload_x(c, c->sa, q, heads * d);
         c->sb.reserve(klen * 8 + 256);
         HIP_OK(hipMemcpyAsync(c->sb.p, k, klen * 4, hipMemcpyHostToDevice, c->s));
@@ -1516,6 +1563,44 @@ int qh_attention(qh_ctx* c, const float* q, const float* k, const float* v, size
         HIP_OK(hipGetLastError());
         HIP_OK(hipMemcpyAsync(out, dout, heads * d * 4, hipMemcpyDeviceToHost, c->s));
         sync(c);
+    });
+}
+
+int qh_attention_noalloc(qh_ctx* c, const float* q, const float* k, const float* v, size_t klen, size_t heads,
+                         size_t kvheads, size_t d, float* out, void* stream) {
+    return guarded(c, [&] {
+        const AttnGeo geo = attn_geometry(klen, heads, kvheads, d);
+        const size_t part_bytes = (heads * geo.nch * (d + 2) * 4 + 255) / 256 * 256;
+        const size_t need = part_bytes + kvheads * 4;
+        if (need > kNoAllocScratchBytes)
+            throw Error("attention over " + std::to_string(geo.T) + " keys needs " + std::to_string(need) +
+                        " bytes of scratch; the no-allocation entry point holds " +
+                        std::to_string(kNoAllocScratchBytes));
+        uint8_t* base = static_cast<uint8_t*>(g_scratch_ptr[c->device]);
+        if (!base) throw Error("no-allocation scratch is not set up on this device");
+        uint32_t* cnt = reinterpret_cast<uint32_t*>(base + part_bytes);
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->s;
+        // the counters start at zero (a fill kernel, no memset node)
+        hipLaunchKernelGGL(k_fill_u32, dim3(1), dim3(kBlock), 0, s, cnt, kvheads, 0u);
+        AttnArgs a{};
+        a.q = q;
+        a.k = k;
+        a.v = v;
+        a.sh = d;
+        a.st = kvheads * d;
+        a.heads = (uint32_t)heads;
+        a.kvheads = (uint32_t)kvheads;
+        a.d = (uint32_t)d;
+        a.tc = geo.tc;
+        a.max_chunks = geo.nch;
+        a.part = reinterpret_cast<float*>(base);
+        a.counter = cnt;
+        a.out = out;
+        a.err = nullptr;
+        hipLaunchKernelGGL(k_attention_api, dim3((uint32_t)kvheads, geo.nch), dim3(kBlock), geo.lds, s, a,
+                           (uint32_t)geo.T);
+        HIP_OK(hipGetLastError());
+        if (!stream) HIP_OK(hipStreamSynchronize(s));
     });
 }
 
