@@ -113,6 +113,15 @@ int qh_stats(const qh_ctx *ctx, qh_stats_t *out);
 int qh_packed_matvec(qh_ctx *ctx, const void *data, size_t len, uint32_t kind, size_t rows,
                      size_t cols, const float *x, float *y);
 
+/* The per-expert down projections of one MoE layer (the loop of
+ * src/model.rs:274-284) as one streaming launch: y[b] = W_b x[b] for b < nvec
+ * (1-8), data = the nvec matrices of rows x cols packed GGUF rows back to
+ * back, x = nvec x cols floats, y = nvec x rows floats.  Block-quantised
+ * formats only (kinds 2, 8, 12, 13, 14), rows of up to 8,192 columns and at
+ * most 12,288 x floats in all; other shapes are refused with an error. */
+int qh_packed_matvec_batch(qh_ctx *ctx, const void *data, size_t len, uint32_t kind, size_t rows,
+                           size_t cols, size_t nvec, const float *x, float *y);
+
 /* == quant::decode (src/quant.rs:81-84) on the device, for `rows` packed
  * rows: out[rows*cols].  Bit-exact with the reference decoder. */
 int qh_dequant(qh_ctx *ctx, const void *data, size_t len, uint32_t kind, size_t rows, size_t cols,
@@ -257,12 +266,24 @@ int qh_bench_decode(qh_ctx *ctx, size_t warmup, size_t steps, double *ms_total);
 #define QH_NUM_KERNEL_CLASSES 7
 int qh_profile_step(qh_ctx *ctx, size_t steps, double *ms_by_class, size_t nclass);
 
-/* Benchmark surface for single matvecs with device-resident inputs: uploads
- * `copies` copies of the packed matrix (so successive launches stream
- * distinct HBM and do not hit the 256 MB MALL), then times `iters` launches
- * rotating over the copies.  ms_per_launch receives the mean launch time. */
+/* Timing of one benchmarked matvec shape. */
+typedef struct qh_matvec_timing {
+    double mean_ms;   /* back-to-back launches rotating over the copies: elapsed / iters */
+    double median_ms; /* median over iters launches, each between its own pair of events */
+    double empty_ms;  /* back-to-back launches of an empty kernel: the launch floor */
+} qh_matvec_timing_t;
+
+/* Benchmark surface for matvecs with device-resident inputs (no reference
+ * counterpart).  data holds nvec (1-8) matrices of rows x cols packed GGUF
+ * rows back to back, x their nvec input vectors (nvec x cols floats): nvec = 1
+ * is Backend::matvec's launch, nvec > 1 the streaming kernel's batched form
+ * (one launch for the routed experts' down projections of a MoE layer).
+ * `copies` copies of the matrices are uploaded so that successive launches
+ * stream distinct HBM rather than the 256 MB MALL; `iters` launches rotate
+ * over them.  Fails if an output is not finite. */
 int qh_bench_matvec(qh_ctx *ctx, const void *data, size_t len, uint32_t kind, size_t rows,
-                    size_t cols, size_t copies, size_t iters, double *ms_per_launch);
+                    size_t cols, size_t nvec, const float *x, size_t copies, size_t iters,
+                    qh_matvec_timing_t *out);
 
 #ifdef __cplusplus
 }

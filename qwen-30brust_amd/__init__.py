@@ -74,6 +74,8 @@ _SIGS = {
     "qh_matvec": (C.c_int, [C.c_void_p, C.c_char_p, C.c_int64, C.c_void_p, C.c_size_t,
                             C.c_void_p, C.c_size_t]),
     "qh_stats": (C.c_int, [C.c_void_p, C.POINTER(_Stats)]),
+    "qh_packed_matvec_batch": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint32, C.c_size_t,
+                                         C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p]),
     "qh_packed_matvec": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint32, C.c_size_t,
                                    C.c_size_t, C.c_void_p, C.c_void_p]),
     "qh_dequant": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint32, C.c_size_t,
@@ -104,7 +106,8 @@ _SIGS = {
     "qh_read_kv": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p]),
     "qh_profile_step": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]),
     "qh_bench_matvec": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint32, C.c_size_t,
-                                  C.c_size_t, C.c_size_t, C.c_size_t, C.POINTER(C.c_double)]),
+                                  C.c_size_t, C.c_size_t, C.c_void_p, C.c_size_t, C.c_size_t,
+                                  C.c_void_p]),
 }
 
 _lib = None
@@ -246,6 +249,16 @@ class Device:
         self._check(lib().qh_packed_matvec(self.h, _ptr(d), d.size, kind, rows, cols, _ptr(x), _ptr(y)))
         return y[:rows]
 
+    def packed_matvec_batch(self, data, kind, rows, cols, x, nvec):
+        """The routed experts' down projections of one layer in one launch:
+        y[b] = W_b x[b] (rows of nvec matrices back to back in data)."""
+        d = np.ascontiguousarray(data, np.uint8)
+        x = _f32(x)
+        y = np.empty(max(nvec * rows, 1), np.float32)
+        self._check(lib().qh_packed_matvec_batch(self.h, _ptr(d), d.size, kind, rows, cols, nvec, _ptr(x),
+                                                 _ptr(y)))
+        return y[:nvec * rows].reshape(nvec, rows)
+
     def dequant(self, data, kind, rows, cols):
         """== quant::decode (src/quant.rs:81-84) for `rows` packed rows."""
         d = np.ascontiguousarray(np.frombuffer(data, np.uint8) if isinstance(data, (bytes, bytearray)) else data, np.uint8)
@@ -277,11 +290,17 @@ class Device:
         self._check(lib().qh_attention(self.h, _ptr(q), _ptr(k), _ptr(v), k.size, heads, kvheads, d, _ptr(out)))
         return out
 
-    def bench_matvec(self, data, kind, rows, cols, copies, iters):
+    def bench_matvec(self, data, kind, rows, cols, x, copies, iters, nvec=1):
+        """Times nvec matvecs of rows x cols (one launch) on device-resident
+        copies: {"mean_ms", "median_ms", "empty_ms"} per launch."""
         d = np.ascontiguousarray(data, np.uint8)
-        ms = C.c_double()
-        self._check(lib().qh_bench_matvec(self.h, _ptr(d), d.size, kind, rows, cols, copies, iters, C.byref(ms)))
-        return ms.value
+        xv = np.ascontiguousarray(x, np.float32)
+        if xv.size != nvec * cols:
+            raise EngineError("x must hold nvec * cols floats")
+        t = (C.c_double * 3)()
+        self._check(lib().qh_bench_matvec(self.h, _ptr(d), d.size, kind, rows, cols, nvec, _ptr(xv),
+                                          copies, iters, C.cast(t, C.c_void_p)))
+        return {"mean_ms": t[0], "median_ms": t[1], "empty_ms": t[2]}
 
 
 class Model:

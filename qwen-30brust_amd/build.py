@@ -27,7 +27,7 @@ HIP_FLAGS = [
     "-Wall", "-Wno-unused-result", "-Wno-unknown-pragmas",
     "-I", os.path.join(ROOT, "include"),
 ]
-ENGINE_SOURCES = ["kernels.hip", "step.hip", "decode.hip", "prefill.hip", "sample.hip", "engine.hip", "gguf.cpp"]
+ENGINE_SOURCES = ["kernels.hip", "matvec.hip", "step.hip", "decode.hip", "prefill.hip", "sample.hip", "engine.hip", "gguf.cpp"]
 
 
 def _run(cmd):

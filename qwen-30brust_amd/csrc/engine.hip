@@ -49,6 +49,9 @@ __global__ void k_finish(Acts, ModelDims, uint32_t);
 __global__ void k_embed(DevMat, Acts, ModelDims);
 __global__ void k_decode(DecodeArgs);
 __global__ void k_xcd_map(uint32_t*);
+// Streaming quantised matvec (matvec.hip).
+bool launch_mv_stream(const DevMat&, const uint8_t* const*, uint32_t, const float*, float*, uint32_t, hipStream_t);
+void launch_empty(hipStream_t);
 // Batched prefill (prefill.hip).
 template <uint32_t K> __global__ void k_gemm_gateup(const _Float16*, uint32_t, ExpertTiles, DevMat, DevMat, _Float16*);
 template <uint32_t K> __global__ void k_gemm_down(const _Float16*, ExpertTiles, DevMat, float*);
@@ -189,6 +192,7 @@ static void noalloc_init(int device) {
 
 struct qh_ctx {
     int device = 0;
+    uint32_t num_cu = 0;  // compute units of the device
     hipStream_t s = nullptr;
     std::string err;
     qh_stats_t stats{};
@@ -345,6 +349,12 @@ void upload_rows(qh_ctx* c, const uint8_t* src, uint8_t* dst, uint32_t kind, uin
 }
 
 void launch_matvec(qh_ctx* c, const DevMat& m, const float* x, float* y, int R = 4) {
+    // block-quantised rows of up to 8,192 columns: the streaming kernel
+    const uint8_t* mats[1] = {m.w};
+    if (launch_mv_stream(m, mats, 1, x, y, c->num_cu, c->s)) {
+        HIP_OK(hipGetLastError());
+        return;
+    }
     const uint32_t np = pad32h(m.cols);
     const bool lds = np * 4 <= 65536;
     const size_t smem = lds ? np * 4 : 0;
@@ -1221,6 +1231,7 @@ int qh_create(int device, qh_ctx** out) {
         noalloc_init(device);
         auto c = std::make_unique<qh_ctx>();
         c->device = device;
+        c->num_cu = (uint32_t)p.multiProcessorCount;
         const char* ng = std::getenv("QH_NO_GRAPH");
         c->use_graph = !(ng && ng[0] == '1');
         HIP_OK(hipStreamCreateWithFlags(&c->s, hipStreamNonBlocking));
@@ -1439,6 +1450,33 @@ int qh_packed_matvec(qh_ctx* c, const void* data, size_t len, uint32_t kind, siz
         HIP_OK(hipMemcpyAsync(y, c->sc.p, rows * 4, hipMemcpyDeviceToHost, c->s));
         sync(c);
         c->stats.matvecs += 1;
+        c->stats.matvec_ms += now_ms() - t0;
+    });
+}
+
+int qh_packed_matvec_batch(qh_ctx* c, const void* data, size_t len, uint32_t kind, size_t rows, size_t cols,
+                           size_t nvec, const float* x, float* y) {
+    return guarded(c, [&] {
+        double t0 = now_ms();
+        size_t rb = row_bytes_checked(kind, cols);
+        if (!(nvec >= 1 && nvec <= 8 && rows > 0 && nvec * rows * rb == len)) throw Error("GPU matvec shape mismatch");
+        if (rows > 0xffffffffull) throw Error("matrix too tall");
+        HIP_OK(hipSetDevice(c->device));
+        const size_t drb = dev_row_bytes(kind, cols);
+        c->sd.reserve(nvec * rows * drb + 64);
+        upload_rows(c, static_cast<const uint8_t*>(data), c->sd.as<uint8_t>(), kind, cols, nvec * rows);
+        const DevMat m = make_mat(c->sd.as<uint8_t>(), kind, rows, cols, 0);
+        const uint8_t* mats[8];
+        for (size_t b = 0; b < nvec; b++) mats[b] = c->sd.as<uint8_t>() + b * rows * drb;
+        const float* xd = upload_x(c, c->sb, x, nvec * cols);
+        c->sc.reserve(nvec * rows * 4);
+        if (!launch_mv_stream(m, mats, (uint32_t)nvec, xd, c->sc.as<float>(), c->num_cu, c->s))
+            throw Error("batched matvec shape not covered (block-quantised rows of <= 8192 columns, "
+                        "<= 12288 x floats)");
+        HIP_OK(hipGetLastError());
+        HIP_OK(hipMemcpyAsync(y, c->sc.p, nvec * rows * 4, hipMemcpyDeviceToHost, c->s));
+        sync(c);
+        c->stats.matvecs += nvec;
         c->stats.matvec_ms += now_ms() - t0;
     });
 }
@@ -1922,39 +1960,74 @@ int qh_profile_step(qh_ctx* c, size_t steps, double* ms_by_class, size_t nclass)
     });
 }
 
-int qh_bench_matvec(qh_ctx* c, const void* data, size_t len, uint32_t kind, size_t rows, size_t cols,
-                    size_t copies, size_t iters, double* ms_per_launch) {
+int qh_bench_matvec(qh_ctx* c, const void* data, size_t len, uint32_t kind, size_t rows, size_t cols, size_t nvec,
+                    const float* x, size_t copies, size_t iters, qh_matvec_timing_t* out) {
     return guarded(c, [&] {
         size_t rb = row_bytes_checked(kind, cols);
-        if (!(rows > 0 && rows * rb == len)) throw Error("GPU matvec shape mismatch");
+        if (!(nvec >= 1 && nvec <= 8 && rows > 0 && nvec * rows * rb == len)) throw Error("GPU matvec shape mismatch");
+        if (rows > 0xffffffffull) throw Error("matrix too tall");
         if (copies == 0 || iters == 0) throw Error("copies and iters must be positive");
-        const size_t drb = dev_row_bytes(kind, cols), one = rows * drb;
+        HIP_OK(hipSetDevice(c->device));
+        const size_t drb = dev_row_bytes(kind, cols), one = nvec * rows * drb;
         DevBuf w;
         w.alloc(one * copies + 64);
-        upload_rows(c, static_cast<const uint8_t*>(data), w.as<uint8_t>(), kind, cols, rows);
+        upload_rows(c, static_cast<const uint8_t*>(data), w.as<uint8_t>(), kind, cols, nvec * rows);
         for (size_t i = 1; i < copies; i++)
             HIP_OK(hipMemcpyAsync(w.as<uint8_t>() + i * one, w.p, one, hipMemcpyDeviceToDevice, c->s));
         DevBuf xb, yb;
-        xb.alloc(pad32h(cols) * 4);
-        HIP_OK(hipMemsetAsync(xb.p, 0, pad32h(cols) * 4, c->s));
-        yb.alloc(rows * 4);
+        xb.alloc(pad32h(nvec * cols) * 4);
+        HIP_OK(hipMemsetAsync(xb.p, 0, pad32h(nvec * cols) * 4, c->s));
+        HIP_OK(hipMemcpyAsync(xb.p, x, nvec * cols * 4, hipMemcpyHostToDevice, c->s));
+        yb.alloc(nvec * rows * 4);
         const int R = pick_r(rows, cols);
-        for (size_t i = 0; i < std::min<size_t>(copies, 8); i++)
-            launch_matvec(c, make_mat(w.as<uint8_t>() + i * one, kind, rows, cols, 0), xb.as<float>(), yb.as<float>(), R);
-        hipEvent_t e0, e1;
-        HIP_OK(hipEventCreate(&e0));
-        HIP_OK(hipEventCreate(&e1));
-        HIP_OK(hipEventRecord(e0, c->s));
-        for (size_t i = 0; i < iters; i++)
-            launch_matvec(c, make_mat(w.as<uint8_t>() + (i % copies) * one, kind, rows, cols, 0), xb.as<float>(),
-                          yb.as<float>(), R);
-        HIP_OK(hipEventRecord(e1, c->s));
-        HIP_OK(hipEventSynchronize(e1));
+        auto launch = [&](size_t i) {
+            const uint8_t* base = w.as<uint8_t>() + (i % copies) * one;
+            const DevMat m = make_mat(base, kind, rows, cols, 0);
+            if (nvec == 1) {
+                launch_matvec(c, m, xb.as<float>(), yb.as<float>(), R);
+                return;
+            }
+            const uint8_t* mats[8];
+            for (size_t b = 0; b < nvec; b++) mats[b] = base + b * rows * drb;
+            if (!launch_mv_stream(m, mats, (uint32_t)nvec, xb.as<float>(), yb.as<float>(), c->num_cu, c->s))
+                throw Error("batched matvec shape not covered by the streaming kernel");
+            HIP_OK(hipGetLastError());
+        };
+        for (size_t i = 0; i < std::min<size_t>(copies, 8); i++) launch(i);
+        std::vector<hipEvent_t> ev(2 * iters + 2, nullptr);
+        for (auto& e : ev) HIP_OK(hipEventCreate(&e));
         float ms = 0;
-        HIP_OK(hipEventElapsedTime(&ms, e0, e1));
-        (void)hipEventDestroy(e0);
-        (void)hipEventDestroy(e1);
-        *ms_per_launch = ms / (double)iters;
+        // back-to-back launches
+        HIP_OK(hipEventRecord(ev[0], c->s));
+        for (size_t i = 0; i < iters; i++) launch(i);
+        HIP_OK(hipEventRecord(ev[1], c->s));
+        HIP_OK(hipEventSynchronize(ev[1]));
+        HIP_OK(hipEventElapsedTime(&ms, ev[0], ev[1]));
+        out->mean_ms = ms / (double)iters;
+        // the empty kernel, back to back: the launch floor
+        HIP_OK(hipEventRecord(ev[0], c->s));
+        for (size_t i = 0; i < iters; i++) launch_empty(c->s);
+        HIP_OK(hipEventRecord(ev[1], c->s));
+        HIP_OK(hipEventSynchronize(ev[1]));
+        HIP_OK(hipEventElapsedTime(&ms, ev[0], ev[1]));
+        out->empty_ms = ms / (double)iters;
+        // each launch between its own pair of events
+        for (size_t i = 0; i < iters; i++) {
+            HIP_OK(hipEventRecord(ev[2 + 2 * i], c->s));
+            launch(i);
+            HIP_OK(hipEventRecord(ev[3 + 2 * i], c->s));
+        }
+        HIP_OK(hipEventSynchronize(ev[1 + 2 * iters]));
+        std::vector<float> t(iters);
+        for (size_t i = 0; i < iters; i++) HIP_OK(hipEventElapsedTime(&t[i], ev[2 + 2 * i], ev[3 + 2 * i]));
+        for (auto& e : ev) (void)hipEventDestroy(e);
+        std::sort(t.begin(), t.end());
+        out->median_ms = iters % 2 ? t[iters / 2] : 0.5 * ((double)t[iters / 2 - 1] + t[iters / 2]);
+        std::vector<float> y(nvec * rows);
+        HIP_OK(hipMemcpyAsync(y.data(), yb.p, y.size() * 4, hipMemcpyDeviceToHost, c->s));
+        sync(c);
+        for (float v : y)
+            if (!std::isfinite(v)) throw Error("benchmark matvec produced a non-finite value");
     });
 }
 

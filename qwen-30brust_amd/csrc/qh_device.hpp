@@ -159,7 +159,10 @@ template <> struct Fmt<Q5_K> {
 // -------------------------------------------------------------------- Q6_K --
 template <> struct Fmt<Q6_K> {
     // ql, qh of the chunk; the 8 scale bytes of its half-block (selected in
-    // dot(), so that load() only issues loads); d
+    // dot(), so that load() only issues loads); the aligned 32-bit word
+    // holding d (a 16-bit load would give the value a 16-bit type, whose
+    // widening the compiler then places right after the load, where it waits
+    // for it)
     struct Raw { uint4 ql, qh; uint2 s8; uint32_t d; };
     static __device__ __forceinline__ uint32_t xoff_a(uint32_t c) {
         uint32_t j = c & 7;
@@ -171,7 +174,7 @@ template <> struct Fmt<Q6_K> {
         return {ld16(row + g.off_a + b * 128 + j * 16),
                 ld16(row + g.off_b + b * 64 + (j >> 2) * 32 + (j & 1) * 16),
                 gld<uint2>(row + g.off_c + b * 16 + (j >> 2) * 8),
-                ld_u16(row + g.off_d + b * 2)};
+                gld<uint32_t>(row + g.off_d + (b >> 1) * 4)};
     }
     static __device__ __forceinline__ float dot(const Raw& r, uint32_t c, const float* xa,
                                                 const float* xb, float sa, float sb) {
@@ -183,7 +186,8 @@ template <> struct Fmt<Q6_K> {
         float sca = (float)(int8_t)(rsc & 0xffu), scb = (float)(int8_t)(rsc >> 8);
         // opaque: the conversion stays here, after the caller's waits; hoisted
         // next to the load it made the loading code wait for the load
-        float d = h2f(opaque(r.d));
+        const uint32_t dw = opaque(r.d);
+        float d = h2f(((c >> 3) & 1) ? dw >> 16 : dw);
         uint32_t l[4] = {r.ql.x, r.ql.y, r.ql.z, r.ql.w};
         uint32_t h[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
         float pa = 0.f, pb = 0.f;
@@ -204,9 +208,10 @@ template <> struct Fmt<Q4_0> {
     static __device__ __forceinline__ uint32_t xoff_a(uint32_t c) { return c * 32; }
     static __device__ __forceinline__ uint32_t xoff_b(uint32_t c) { return c * 32 + 16; }
     static __device__ __forceinline__ Raw load(const uint8_t* row, const RowGeo& g, uint32_t c) {
-        return {ld16(row + g.off_a + c * 16), ld_u16(row + g.off_b + c * 2)};
+        // d in the aligned 32-bit word holding it (the row is padded past it)
+        return {ld16(row + g.off_a + c * 16), gld<uint32_t>(row + g.off_b + (c >> 1) * 4)};
     }
-    static __device__ __forceinline__ float dot(const Raw& r, uint32_t, const float* xa,
+    static __device__ __forceinline__ float dot(const Raw& r, uint32_t c, const float* xa,
                                                 const float* xb, float sa, float sb) {
         uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
         float p = 0.f;
@@ -215,7 +220,7 @@ template <> struct Fmt<Q4_0> {
             p = dot4u8(w[k] & 0x0f0f0f0fu, xa + 4 * k, p);
             p = dot4u8((w[k] >> 4) & 0x0f0f0f0fu, xb + 4 * k, p);
         }
-        return h2f(r.d) * (p - 8.f * (sa + sb));
+        return h2f((c & 1) ? r.d >> 16 : r.d) * (p - 8.f * (sa + sb));
     }
 };
 
@@ -226,9 +231,9 @@ template <> struct Fmt<Q8_0> {
     static __device__ __forceinline__ uint32_t xoff_b(uint32_t c) { return c * 32 + 16; }
     static __device__ __forceinline__ Raw load(const uint8_t* row, const RowGeo& g, uint32_t c) {
         return {ld16(row + g.off_a + c * 32), ld16(row + g.off_a + c * 32 + 16),
-                ld_u16(row + g.off_b + c * 2)};
+                gld<uint32_t>(row + g.off_b + (c >> 1) * 4)};
     }
-    static __device__ __forceinline__ float dot(const Raw& r, uint32_t, const float* xa,
+    static __device__ __forceinline__ float dot(const Raw& r, uint32_t c, const float* xa,
                                                 const float* xb, float sa, float sb) {
         // bytes ^ 0x80 = q + 128 (unsigned); subtract 128 * sum(x) afterwards
         uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
@@ -237,7 +242,7 @@ template <> struct Fmt<Q8_0> {
         for (int k = 0; k < 4; k++) p = dot4u8(w[k] ^ 0x80808080u, xa + 4 * k, p);
 #pragma unroll
         for (int k = 0; k < 4; k++) p = dot4u8(w[4 + k] ^ 0x80808080u, xb + 4 * k, p);
-        return h2f(r.d) * (p - 128.f * (sa + sb));
+        return h2f((c & 1) ? r.d >> 16 : r.d) * (p - 128.f * (sa + sb));
     }
 };
 

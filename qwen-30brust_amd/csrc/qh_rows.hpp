@@ -38,6 +38,33 @@ __device__ __forceinline__ void x_runs(const float* xs, uint32_t c, float* xa, f
     }
 }
 
+// LDS layout of the gathered activation vectors: element i at px(i) =
+// i + 4 (i / 64).  The lanes of one read take the 16-float runs of
+// neighbouring chunks of a Q4_K/Q6_K row, 16-64 floats apart; unpadded, four
+// of every eight lanes of a 16-byte read met in the same banks.  A run never
+// crosses a 64-float block, so it stays contiguous.
+__device__ __forceinline__ uint32_t px(uint32_t i) { return i + ((i >> 6) << 2); }
+
+// x_runs (the two 16-float runs of chunk c and their sums) of the vector
+// that starts at element `base` of a padded LDS vector.
+template <uint32_t KIND>
+__device__ __forceinline__ void x_runs_p(const float* xs, uint32_t base, uint32_t c, float* xa, float* xb, float& sa,
+                                         float& sb) {
+    const uint32_t fa = base + Fmt<KIND>::xoff_a(c), fb = base + Fmt<KIND>::xoff_b(c);
+    const float4* pa = reinterpret_cast<const float4*>(xs + px(fa));
+    const float4* pb = reinterpret_cast<const float4*>(xs + px(fb));
+    sa = 0.f;
+    sb = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float4 a = pa[k], b = pb[k];
+        xa[4 * k] = a.x; xa[4 * k + 1] = a.y; xa[4 * k + 2] = a.z; xa[4 * k + 3] = a.w;
+        xb[4 * k] = b.x; xb[4 * k + 1] = b.y; xb[4 * k + 2] = b.z; xb[4 * k + 3] = b.w;
+        sa += (a.x + a.y) + (a.z + a.w);
+        sb += (b.x + b.y) + (b.z + b.w);
+    }
+}
+
 // Chunk load with a column bound: F32/F16 rows may end inside a chunk; the
 // missing weights read as zero.  Quantized formats always hold whole blocks.
 template <uint32_t KIND>

@@ -123,6 +123,70 @@ def test_matvec_30b_shapes(dev, name, kind, rows, cols):
     assert rel_err(y, ref) <= REL
 
 
+QUANT_KINDS = [2, 8, 12, 13, 14]
+
+
+@pytest.mark.parametrize("kind", QUANT_KINDS)
+@pytest.mark.parametrize("rows,cols", [(1, 256), (3, 3072), (40, 4096), (9, 8192), (17, 160), (33, 8448)])
+def test_packed_matvec_lane_layouts(dev, kind, rows, cols):
+    """Row lengths that select every (chunks per lane, lanes per row) layout
+    of the streaming kernel (3,072 columns: 3 chunks on 32 lanes; 8,192: 4 on
+    64; 160: 3 on 2) and, past 8,192 columns, the general kernel."""
+    blk, _ = LAYOUT[kind]
+    if cols % blk:
+        pytest.skip("shape not representable in this format")
+    rng = np.random.default_rng(rows * 13 + cols + kind)
+    data = random_blocks(kind, rows, cols, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    y = dev.packed_matvec(data, kind, rows, cols, x)
+    ref = oracle.packed_matvec(data, kind, rows, cols, x, threads=8)
+    assert rel_err(y, ref) <= REL
+
+
+@pytest.mark.parametrize("kind", QUANT_KINDS)
+@pytest.mark.parametrize("nvec,rows,cols", [(1, 37, 512), (3, 130, 2048), (8, 64, 768), (2, 7, 4096)])
+def test_packed_matvec_batch_vs_oracle(dev, kind, nvec, rows, cols):
+    """The batched launch (one matrix and one x per vector) against the
+    oracle's matvec of each matrix."""
+    blk, _ = LAYOUT[kind]
+    if cols % blk:
+        pytest.skip("shape not representable in this format")
+    rng = np.random.default_rng(nvec * 101 + rows + cols + kind)
+    data = random_blocks(kind, nvec * rows, cols, rng)
+    x = rng.standard_normal(nvec * cols).astype(np.float32)
+    y = dev.packed_matvec_batch(data, kind, rows, cols, x, nvec)
+    per = data.size // nvec
+    for b in range(nvec):
+        ref = oracle.packed_matvec(data[b * per:(b + 1) * per], kind, rows, cols, x[b * cols:(b + 1) * cols],
+                                   threads=8)
+        assert rel_err(y[b], ref) <= REL, b
+
+
+def test_packed_matvec_batch_30b_down(dev):
+    """The 8 routed experts' down projections of a 30B-A3B layer (768 -> 2048
+    Q6_K each) in one launch, against the oracle per expert."""
+    rows, cols, nvec = 2048, 768, 8
+    w = synth.normal(5, nvec * rows * cols, 0.0, 0.02).reshape(nvec * rows, cols)
+    data = synth.quantize(14, w)
+    x = synth.normal(18, nvec * cols)
+    y = dev.packed_matvec_batch(data, 14, rows, cols, x, nvec)
+    per = data.size // nvec
+    for b in range(nvec):
+        ref = oracle.packed_matvec(data[b * per:(b + 1) * per], 14, rows, cols, x[b * cols:(b + 1) * cols],
+                                   threads=8)
+        assert rel_err(y[b], ref) <= REL, b
+
+
+def test_packed_matvec_batch_refusals(dev):
+    x = np.zeros(2 * 256, np.float32)
+    with pytest.raises(engine.EngineError, match="not covered"):
+        dev.packed_matvec_batch(np.zeros(2 * 256 * 4, np.uint8), 0, 1, 256, x, 2)  # F32 rows
+    with pytest.raises(engine.EngineError, match="shape mismatch"):
+        dev.packed_matvec_batch(np.zeros(9 * 144, np.uint8), 12, 1, 256, np.zeros(9 * 256), 9)
+    with pytest.raises(engine.EngineError, match="not covered"):  # 2 x 8,192 x floats
+        dev.packed_matvec_batch(np.zeros(2 * 32 * 144, np.uint8), 12, 1, 8192, np.zeros(2 * 8192), 2)
+
+
 def test_large_grid(dev):  # tests/core.rs:186-209: 70,001 rows x 2 cols F32
     rows = 70001
     x = np.array([1.5, -0.5], np.float32)
