@@ -87,6 +87,13 @@ def matvec_cases(engine, synth, dev):
              ("vocab 2048->151936 Q6_K", 14, 151936, 2048, 1), ("expert_down 768->2048 Q6_K", 14, 2048, 768, 1),
              ("expert_down x8 768->2048 Q6_K (one launch)", 14, 2048, 768, 8)]
     out = []
+    # the device's practical read ceiling: a plain stream over as many bytes as the vocab matrix
+    rd = dev.bench_read(255868416, 2, 200)
+    ceil_gbs = 255868416 / (rd["median_ms"] * 1e-3) / 1e9
+    out.append({"case": "read-only stream 255,868,416 B (ceiling)", "bytes": 255868416,
+                "us_median": round(rd["median_ms"] * 1e3, 3), "GB_s": round(ceil_gbs, 1),
+                "frac_of_peak": round(ceil_gbs / HBM_PEAK_GBS, 4)})
+    log(f"read-only stream: median {rd['median_ms']*1e3:.2f} us ({ceil_gbs:.0f} GB/s)")
     for i, (name, kind, rows, cols, nvec) in enumerate(cases):
         w = synth.normal(100 + i, nvec * rows * cols, 0.0, 0.02).reshape(nvec * rows, cols)
         data = synth.quantize(kind, w)
@@ -99,6 +106,7 @@ def matvec_cases(engine, synth, dev):
                     "us_mean_back_to_back": round(t["mean_ms"] * 1e3, 3),
                     "us_empty_kernel_floor": round(t["empty_ms"] * 1e3, 3),
                     "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+                    "frac_of_read_ceiling": round(gbs / ceil_gbs, 4),
                     "GB_s_back_to_back": round(nbytes / (t["mean_ms"] * 1e-3) / 1e9, 1)})
         log(f"matvec {name}: median {t['median_ms']*1e3:.2f} us ({gbs:.0f} GB/s), back-to-back "
             f"{t['mean_ms']*1e3:.2f} us, empty kernel {t['empty_ms']*1e3:.2f} us")

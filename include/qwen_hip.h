@@ -285,6 +285,12 @@ int qh_bench_matvec(qh_ctx *ctx, const void *data, size_t len, uint32_t kind, si
                     size_t cols, size_t nvec, const float *x, size_t copies, size_t iters,
                     qh_matvec_timing_t *out);
 
+/* Read-only stream ceiling (no reference counterpart): `bytes` of device
+ * memory, `copies` copies rotated over, each 16-byte word loaded once per
+ * launch by a plain streaming kernel; mean and median launch times as for
+ * qh_bench_matvec (empty_ms is 0).  The matvec bandwidths are read against it. */
+int qh_bench_read(qh_ctx *ctx, size_t bytes, size_t copies, size_t iters, qh_matvec_timing_t *out);
+
 #ifdef __cplusplus
 }
 #endif

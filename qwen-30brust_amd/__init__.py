@@ -105,6 +105,7 @@ _SIGS = {
     "qh_route_log": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
     "qh_read_kv": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p]),
     "qh_profile_step": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]),
+    "qh_bench_read": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p]),
     "qh_bench_matvec": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint32, C.c_size_t,
                                   C.c_size_t, C.c_size_t, C.c_void_p, C.c_size_t, C.c_size_t,
                                   C.c_void_p]),
@@ -289,6 +290,12 @@ class Device:
         out = np.empty(heads * d, np.float32)
         self._check(lib().qh_attention(self.h, _ptr(q), _ptr(k), _ptr(v), k.size, heads, kvheads, d, _ptr(out)))
         return out
+
+    def bench_read(self, nbytes, copies, iters):
+        """Times a read-only stream over nbytes: {"mean_ms", "median_ms"}."""
+        t = (C.c_double * 3)()
+        self._check(lib().qh_bench_read(self.h, nbytes, copies, iters, C.cast(t, C.c_void_p)))
+        return {"mean_ms": t[0], "median_ms": t[1]}
 
     def bench_matvec(self, data, kind, rows, cols, x, copies, iters, nvec=1):
         """Times nvec matvecs of rows x cols (one launch) on device-resident

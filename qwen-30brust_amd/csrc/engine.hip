@@ -52,6 +52,7 @@ __global__ void k_xcd_map(uint32_t*);
 // Streaming quantised matvec (matvec.hip).
 bool launch_mv_stream(const DevMat&, const uint8_t* const*, uint32_t, const float*, float*, uint32_t, hipStream_t);
 void launch_empty(hipStream_t);
+void launch_read_stream(const void*, size_t, uint32_t*, uint32_t, hipStream_t);
 // Batched prefill (prefill.hip).
 template <uint32_t K> __global__ void k_gemm_gateup(const _Float16*, uint32_t, ExpertTiles, DevMat, DevMat, _Float16*);
 template <uint32_t K> __global__ void k_gemm_down(const _Float16*, ExpertTiles, DevMat, float*);
@@ -1957,6 +1958,46 @@ int qh_profile_step(qh_ctx* c, size_t steps, double* ms_by_class, size_t nclass)
         if (st.err) fail_step(c, st.err);
         c->pos += steps;
         for (size_t j = 0; j < QH_NUM_KERNEL_CLASSES; j++) ms_by_class[j] = acc[j] / (double)steps;
+    });
+}
+
+int qh_bench_read(qh_ctx* c, size_t bytes, size_t copies, size_t iters, qh_matvec_timing_t* out) {
+    return guarded(c, [&] {
+        if (bytes < 16 || copies == 0 || iters == 0) throw Error("bytes, copies and iters must be positive");
+        HIP_OK(hipSetDevice(c->device));
+        const size_t one = bytes / 16 * 16;
+        DevBuf w, o;
+        w.alloc(one * copies);
+        o.alloc(64);
+        HIP_OK(hipMemsetAsync(w.p, 0x5a, one * copies, c->s));
+        const uint32_t grid = 4 * std::max(c->num_cu, 1u);
+        auto launch = [&](size_t i) {
+            launch_read_stream(w.as<uint8_t>() + (i % copies) * one, one, o.as<uint32_t>(), grid, c->s);
+            HIP_OK(hipGetLastError());
+        };
+        for (size_t i = 0; i < std::min<size_t>(copies, 4); i++) launch(i);
+        std::vector<hipEvent_t> ev(2 * iters + 2, nullptr);
+        for (auto& e : ev) HIP_OK(hipEventCreate(&e));
+        float ms = 0;
+        HIP_OK(hipEventRecord(ev[0], c->s));
+        for (size_t i = 0; i < iters; i++) launch(i);
+        HIP_OK(hipEventRecord(ev[1], c->s));
+        HIP_OK(hipEventSynchronize(ev[1]));
+        HIP_OK(hipEventElapsedTime(&ms, ev[0], ev[1]));
+        out->mean_ms = ms / (double)iters;
+        out->empty_ms = 0;
+        for (size_t i = 0; i < iters; i++) {
+            HIP_OK(hipEventRecord(ev[2 + 2 * i], c->s));
+            launch(i);
+            HIP_OK(hipEventRecord(ev[3 + 2 * i], c->s));
+        }
+        HIP_OK(hipEventSynchronize(ev[1 + 2 * iters]));
+        std::vector<float> t(iters);
+        for (size_t i = 0; i < iters; i++) HIP_OK(hipEventElapsedTime(&t[i], ev[2 + 2 * i], ev[3 + 2 * i]));
+        for (auto& e : ev) (void)hipEventDestroy(e);
+        std::sort(t.begin(), t.end());
+        out->median_ms = iters % 2 ? t[iters / 2] : 0.5 * ((double)t[iters / 2 - 1] + t[iters / 2]);
+        sync(c);
     });
 }
 

@@ -33,6 +33,7 @@ struct MvArgs {
     uint32_t per;                   // row groups per workgroup
     uint32_t xpitch;                // LDS elements between vectors (a multiple of 64, before padding)
     uint32_t single;                // every wave has at most one group
+    uint32_t xsum_off;              // LDS float offset of the chunk run sums (even)
 };
 
 // x elements staged per thread (float4 loads, issued before the weights):
@@ -41,11 +42,62 @@ struct MvArgs {
 template <int NT>
 constexpr int mv_xv() { return NT == kMvT ? (int)(kMvMaxXFloats / 4 + kMvT - 1) / kMvT : 8; }
 
+// Chunk loads of a row through a buffer resource: the row's byte offset is
+// one 32-bit add per lane, the field offsets (RowGeo) go in the scalar offset.
+__device__ __forceinline__ uint4 bld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+__device__ __forceinline__ uint2 bld8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+    return make_uint2((uint32_t)v[0], (uint32_t)v[1]);
+}
+__device__ __forceinline__ uint32_t bld4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
+
+// The same bytes as Fmt<KIND>::load (qh_device.hpp), for the row at byte
+// offset ro of the buffer.
+template <uint32_t KIND>
+__device__ __forceinline__ typename Fmt<KIND>::Raw bload(__amdgpu_buffer_rsrc_t r, uint32_t ro, const RowGeo& g,
+                                                         uint32_t c) {
+    const uint32_t b = c >> 3, j = c & 7;
+    if constexpr (KIND == Q4_K) {
+        return {bld16(r, ro + b * 128 + j * 16, g.off_b), bld16(r, ro + b * 16, g.off_a)};
+    } else if constexpr (KIND == Q5_K) {
+        return {bld16(r, ro + b * 128 + j * 16, g.off_c), bld16(r, ro + b * 16, g.off_a),
+                bld16(r, ro + b * 32 + (j & 1) * 16, g.off_b)};
+    } else if constexpr (KIND == Q6_K) {
+        return {bld16(r, ro + b * 128 + j * 16, g.off_a), bld16(r, ro + b * 64 + (j >> 2) * 32 + (j & 1) * 16, g.off_b),
+                bld8(r, ro + b * 16 + (j >> 2) * 8, g.off_c), bld4(r, ro + (b >> 1) * 4, g.off_d)};
+    } else if constexpr (KIND == Q4_0) {
+        return {bld16(r, ro + c * 16, g.off_a), bld4(r, ro + (c >> 1) * 4, g.off_b)};
+    } else {
+        static_assert(KIND == Q8_0, "block-quantised formats only");
+        return {bld16(r, ro + c * 32, g.off_a), bld16(r, ro + c * 32 + 16, g.off_a), bld4(r, ro + (c >> 1) * 4, g.off_b)};
+    }
+}
+
+// The two 16-float runs of chunk c of the padded LDS vector that starts at
+// element `base` (their sums come precomputed).
+template <uint32_t KIND>
+__device__ __forceinline__ void x_runs_only(const float* xs, uint32_t base, uint32_t c, float* xa, float* xb) {
+    const float4* pa = reinterpret_cast<const float4*>(xs + px(base + Fmt<KIND>::xoff_a(c)));
+    const float4* pb = reinterpret_cast<const float4*>(xs + px(base + Fmt<KIND>::xoff_b(c)));
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float4 u = pa[k], v = pb[k];
+        xa[4 * k] = u.x; xa[4 * k + 1] = u.y; xa[4 * k + 2] = u.z; xa[4 * k + 3] = u.w;
+        xb[4 * k] = v.x; xb[4 * k + 1] = v.y; xb[4 * k + 2] = v.z; xb[4 * k + 3] = v.w;
+    }
+}
+
 template <uint32_t KIND, int C, int R, int NT>
 __global__ __launch_bounds__(NT) void k_mv_stream(MvArgs a) {
     constexpr int NW = NT / 64, XV = mv_xv<NT>();
     extern __shared__ float4 smem4[];
     float* xs = reinterpret_cast<float*>(smem4);
+    float2* xsum = reinterpret_cast<float2*>(xs + a.xsum_off);  // [nb][cpr]
     using Raw = typename Fmt<KIND>::Raw;
     const DevMat& m = a.m;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
@@ -56,18 +108,19 @@ __global__ __launch_bounds__(NT) void k_mv_stream(MvArgs a) {
     const uint32_t g0 = min(blockIdx.x * a.per, ngrp), g1 = min(g0 + a.per, ngrp);
     if (g0 >= g1) return;  // the whole workgroup
 
+    const uint32_t mbytes = m.rows * m.drb;  // < 2^32 (checked by the host)
     auto load_group = [&](Raw (&t)[R][C], uint32_t g) {
         const uint32_t b = g / a.gpb, rg = g - b * a.gpb;
         // a select chain, so that the argument array stays in scalar registers
         const uint8_t* base = a.mat[0];
 #pragma unroll
         for (uint32_t j = 1; j < kMvMaxVec; j++) base = b == j ? a.mat[j] : base;
+        const __amdgpu_buffer_rsrc_t rs = buf_rsrc(base, mbytes);
 #pragma unroll
         for (int k = 0; k < R; k++) {
-            const uint32_t r = min(rg * rpg + sub + k * S, m.rows - 1);
-            const uint8_t* row = base + (size_t)r * m.drb;
+            const uint32_t ro = min(rg * rpg + sub + k * S, m.rows - 1) * m.drb;
 #pragma unroll
-            for (int i = 0; i < C; i++) t[k][i] = Fmt<KIND>::load(row, m.geo, min(cl + i * L, cpr - 1));
+            for (int i = 0; i < C; i++) t[k][i] = bload<KIND>(rs, ro, m.geo, min(cl + i * L, cpr - 1));
         }
     };
     auto reduce_store = [&](const Raw (&t)[R][C], uint32_t g) {
@@ -79,8 +132,10 @@ __global__ __launch_bounds__(NT) void k_mv_stream(MvArgs a) {
         for (int i = 0; i < C; i++) {
             const uint32_t ch = cl + i * L;
             if (ch < cpr) {
-                float xa[16], xb[16], sa, sb;
-                x_runs_p<KIND>(xs, b * a.xpitch, ch, xa, xb, sa, sb);
+                float xa[16], xb[16];
+                x_runs_only<KIND>(xs, b * a.xpitch, ch, xa, xb);
+                const float2 s2 = xsum[b * cpr + ch];
+                const float sa = s2.x, sb = s2.y;
 #pragma unroll
                 for (int k = 0; k < R; k++) acc[k] += Fmt<KIND>::dot(t[k][i], ch, xa, xb, sa, sb);
             }
@@ -115,7 +170,15 @@ __global__ __launch_bounds__(NT) void k_mv_stream(MvArgs a) {
         }
     }
     __syncthreads();
-    if (gi >= g1) return;  // wave-uniform, after the barrier
+    // the sums of every chunk's two runs (the K-quant offsets' factors)
+    for (uint32_t i = tid; i < a.nb * cpr; i += NT) {
+        const uint32_t b = i / cpr, c = i - b * cpr;
+        float xa[16], xb[16], sa, sb;
+        x_runs_p<KIND>(xs, b * a.xpitch, c, xa, xb, sa, sb);
+        xsum[i] = make_float2(sa, sb);
+    }
+    __syncthreads();
+    if (gi >= g1) return;  // wave-uniform, after the barriers
     if (a.single) {        // one group per wave: nothing to prefetch
         reduce_store(ta, gi);
         return;
@@ -200,7 +263,7 @@ void launch_one(MvArgs a, uint64_t ngrp, uint32_t num_cu, size_t smem, hipStream
     // residency at the largest x this kernel stages (asked once per kernel)
     static const int per_cu = [] {
         int n = 0;
-        const size_t most = (size_t)(kMvMaxXFloats + 4 * (kMvMaxXFloats / 64)) * 4;
+        const size_t most = (size_t)(kMvMaxXFloats + 4 * (kMvMaxXFloats / 64) + 2 * kMvMaxXFloats / 32) * 4;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_mv_stream<K, C, R, kMvT>, kMvT, most) != hipSuccess)
             n = 1;
         return std::max(n, 1);
@@ -237,6 +300,7 @@ bool launch_mv_stream(const DevMat& m, const uint8_t* const* mats, uint32_t nb, 
     if (!quant || nb == 0 || nb > kMvMaxVec || m.rows == 0 || m.cols % 32 != 0) return false;
     const uint32_t cpr = m.cols / 32, xpitch = (m.cols + 63) / 64 * 64;
     if (cpr > 256 || (uint64_t)nb * xpitch > kMvMaxXFloats) return false;
+    if ((uint64_t)m.rows * m.drb + 64 >= (1ull << 32)) return false;  // 32-bit buffer offsets
     const MvShape s = mv_shape(cpr, m.rows, nb, 2 * std::max(num_cu, 1u) * kMvW);
     if (s.C == 0) return false;
     MvArgs a{};
@@ -251,7 +315,8 @@ bool launch_mv_stream(const DevMat& m, const uint8_t* const* mats, uint32_t nb, 
     a.xpitch = xpitch;
     const uint64_t ngrp = (uint64_t)nb * a.gpb;
     const uint32_t nx = nb * xpitch;
-    const size_t smem = (size_t)(nx + 4 * (nx / 64)) * 4;
+    a.xsum_off = nx + 4 * (nx / 64);
+    const size_t smem = (size_t)(a.xsum_off + 2 * nb * cpr) * 4;
     switch (m.kind) {
     case Q4_0: return launch_kind<Q4_0>(s, a, ngrp, num_cu, smem, st);
     case Q8_0: return launch_kind<Q8_0>(s, a, ngrp, num_cu, smem, st);
@@ -259,6 +324,31 @@ bool launch_mv_stream(const DevMat& m, const uint8_t* const* mats, uint32_t nb, 
     case Q5_K: return launch_kind<Q5_K>(s, a, ngrp, num_cu, smem, st);
     default: return launch_kind<Q6_K>(s, a, ngrp, num_cu, smem, st);
     }
+}
+
+// Read-only stream: every 16-byte word of p[0, n16) loaded once (eight loads
+// in flight per thread), folded by xor (a word is stored only if the fold hits
+// one fixed value, so the loads cannot be dropped).  Its
+// rate is the device's practical read ceiling beside the matvec timings.
+__global__ __launch_bounds__(kMvT) void k_read_stream(const uint4* __restrict__ p, size_t n16, uint32_t* out) {
+    const size_t stride = (size_t)gridDim.x * kMvT;
+    uint32_t acc = 0;
+    size_t i = (size_t)blockIdx.x * kMvT + threadIdx.x;
+    for (; i + 7 * stride < n16; i += 8 * stride) {
+        uint4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = gld<uint4>(p + i + k * stride);
+#pragma unroll
+        for (int k = 0; k < 8; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    }
+    for (; i < n16; i += stride) {
+        const uint4 v = gld<uint4>(p + i);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9e3779b9u) out[0] = acc;  // keeps the loads; almost never stores
+}
+void launch_read_stream(const void* p, size_t bytes, uint32_t* out, uint32_t grid, hipStream_t st) {
+    hipLaunchKernelGGL(k_read_stream, dim3(grid), dim3(kMvT), 0, st, static_cast<const uint4*>(p), bytes / 16, out);
 }
 
 // An empty kernel: the launch floor beside the small matvec timings.
