@@ -113,33 +113,44 @@ def matvec_cases(engine, synth, dev):
     return out
 
 
-def measured_traffic(kernel_class):
+def measured_traffic(kernel_class, position):
     """HBM bytes per launch of a step kernel class (reads + writes), from the
     committed rocprofv3 PMC summary (FETCH_SIZE / WRITE_SIZE passes scaled by
-    a copy of known size); None when the summary is absent."""
+    a copy of known size).  For the persistent step the summary holds a
+    least-squares line over every launch of the profiled run (the KV history
+    grows with the position), evaluated here at the position timed; None when
+    the summary is absent."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic_decode_30b.json")
     try:
         with open(path) as f:
             d = json.load(f)["per_launch"][kernel_class]
-        return int(d["read_bytes"] + d["write_bytes"])
-    except (OSError, KeyError, ValueError):
+        tot = 0.0
+        for k in ("read_bytes", "write_bytes"):
+            v = d[k]
+            tot += v["intercept"] + v["slope"] * position if isinstance(v, dict) else v
+        return int(tot)
+    except (OSError, KeyError, ValueError, TypeError):
         return None
 
 
-def cpu_baseline(img, spec, threads_nt):
+def cpu_baseline(img, spec, threads_nt, pos):
     """The oracle (C restatement of the reference CPU backend) on this host:
     faithful single-thread per-element decode, as backend.rs:41-48.  Sample:
-    layers 0-15 and the vocab projection of one decode token at position 0,
-    scaled to the 48-layer token.  Also the row-threaded oracle (same bits)."""
+    layers 0-15 and the vocab projection of one decode token at position
+    `pos` (the position the GPU step is timed at) over a seeded N(0,1) KV
+    history of `pos` positions, scaled to the 48-layer token.  Also the
+    row-threaded oracle (same bits) on one full token at position 0."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     g = oracle.Gguf(img)
     m = oracle.Model(g, 8, threads=0)
     x = g.row("token_embd.weight", 3)
+    kvd = spec.kvheads * spec.head_dim
+    hist = np.random.default_rng(7).standard_normal((2, pos * kvd)).astype(np.float32)
     n_sample = 16
     t0 = time.time()
     for layer in range(n_sample):
-        x, _, _ = m.layer_forward(layer, x, 0, None, None, threads=0)
+        x, _, _ = m.layer_forward(layer, x, pos, hist[0], hist[1], threads=0)
     t_layers = time.time() - t0
     t0 = time.time()
     m.matvec("output.weight", None, x, threads=0)
@@ -152,8 +163,9 @@ def cpu_baseline(img, spec, threads_nt):
     t_nt = time.time() - t0
     log(f"cpu oracle {threads_nt} threads: {t_nt:.2f} s/token")
     return {"value": round(1.0 / per_token, 5), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": f"faithful single-thread oracle, one decode token at position 0: layers 0-{n_sample-1} "
-                      f"({t_layers:.1f} s) + vocab projection ({t_vocab:.1f} s), layers scaled to {spec.layers}",
+            "sample": f"faithful single-thread oracle, one decode token at position {pos} over a seeded KV history: "
+                      f"layers 0-{n_sample-1} ({t_layers:.1f} s) + vocab projection ({t_vocab:.1f} s), layers "
+                      f"scaled to {spec.layers}",
             "threaded": {"value": round(1.0 / t_nt, 4), "unit": "tok/s", "cores": threads_nt,
                          "sample": "row-threaded oracle (bit-identical), one full decode token at position 0"}}
 
@@ -278,7 +290,7 @@ def main():
 
     w_active = sum(bytes_cls[k] for k in ("qkv", "oproj", "gateup", "down", "vocab"))
     matvec = [] if args.no_matvec else matvec_cases(engine, synth, dev)
-    cpu = None if args.no_cpu else cpu_baseline(img, spec, threads)
+    cpu = None if args.no_cpu else cpu_baseline(img, spec, threads, int(pos_dec) if persistent else int(pos_mid))
 
     result = {
         "metric": "decode tok/s, 30B-A3B Q4_K_M batch 1; matvec HBM GB/s as % of peak",
@@ -300,7 +312,8 @@ def main():
                    "positions": [pos_start, pos_start + args.warmup + args.steps]},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(dom), "algorithmic_bytes_per_launch": int(per_launch_bytes),
+                     "traffic": measured_traffic(dom, pos_dec if persistent else pos_mid),
+                     "algorithmic_bytes_per_launch": int(per_launch_bytes),
                      "launch_us": round(per_launch_ms * 1e3, 2)},
         "weights_roofline": {"active_weight_bytes_per_token": int(w_active),
                              "GB_s": round(w_active * tok_s / 1e9, 1),
