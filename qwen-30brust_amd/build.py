@@ -51,7 +51,7 @@ def build_engine():
     with ThreadPoolExecutor(max_workers=len(ENGINE_SOURCES)) as ex:
         objs = list(ex.map(compile_one, ENGINE_SOURCES))
     tmp = ENGINE_SO + ".tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, "-lhipblaslt"])
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, ENGINE_SO)
     build_cli()
     return ENGINE_SO
@@ -72,7 +72,7 @@ def build_trace():
             raise RuntimeError(f"{obj} is missing: build the engine first")
         objs.append(obj)
     tmp = TRACE_SO + ".tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, "-lhipblaslt"])
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, TRACE_SO)
     return TRACE_SO
 

@@ -1,7 +1,6 @@
 // Host side of the decode engine: model upload, the captured token-step
 // graph, and the C ABI declared in include/qwen_hip.h.
 #include <hip/hip_runtime.h>
-#include <hipblaslt/hipblaslt.h>
 
 #include <algorithm>
 #include <array>
@@ -56,9 +55,9 @@ void launch_read_stream(const void*, size_t, uint32_t*, uint32_t, hipStream_t);
 // Batched prefill (prefill.hip).
 template <uint32_t K> __global__ void k_gemm_gateup(const _Float16*, uint32_t, ExpertTiles, DevMat, DevMat, _Float16*);
 template <uint32_t K> __global__ void k_gemm_down(const _Float16*, ExpertTiles, DevMat, float*);
-template <uint32_t K> __global__ void k_dequant16(DevMat, uint32_t, uint32_t, _Float16*);
+__global__ void k_gemm_dense(const _Float16*, uint32_t, DenseSegs, float*, uint32_t, size_t);
 __global__ void k_pf_embed(DevMat, const uint32_t*, uint32_t, uint32_t, float*, DevState*);
-__global__ void k_pf_norm(const float*, const float*, uint32_t, float, _Float16*, float*);
+__global__ void k_pf_norm(float*, const float*, uint32_t, float, _Float16*, float*, const float*, size_t);
 __global__ void k_pf_qkrope(const float*, const float*, const float*, const float2*, uint32_t, uint32_t, uint32_t,
                             uint32_t, uint32_t, float, _Float16*, float*, float*, _Float16*, _Float16*, uint32_t);
 __global__ void k_pf_attn(const _Float16*, const _Float16*, const _Float16*, uint32_t, uint32_t, uint32_t, uint32_t,
@@ -246,22 +245,7 @@ struct qh_ctx {
         uint32_t *ids = nullptr, *goff = nullptr, *tok = nullptr, *asg = nullptr, *te = nullptr, *tm = nullptr,
                  *ntile = nullptr;
         uint32_t max_tiles = 0;
-        // fp16 copies of every layer's q|k|v ([qd + 2 kvd][H]) and o ([H][qd])
-        // weights, made on the first prefill and kept with the model
-        DevBuf w16;
-        std::vector<const _Float16*> wqkv16, wo16;
     } pf;
-
-    // library GEMMs of the prefill's dense projections (hipBLASLt): one plan
-    // (descriptors + chosen algorithm) per (N, K, tokens, accumulate) shape
-    struct GemmPlan {
-        hipblasLtMatmulDesc_t desc = nullptr;
-        hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
-        hipblasLtMatmulAlgo_t algo{};
-    };
-    hipblasLtHandle_t blt = nullptr;
-    DevBuf blt_ws;
-    std::map<std::array<uint32_t, 4>, GemmPlan> plans;
 
     // scratch for the API surfaces
     DevBuf sa, sb, sc, sd;
@@ -274,13 +258,6 @@ struct qh_ctx {
 
     ~qh_ctx() {
         drop_model();
-        for (auto& kv : plans) {
-            (void)hipblasLtMatrixLayoutDestroy(kv.second.la);
-            (void)hipblasLtMatrixLayoutDestroy(kv.second.lb);
-            (void)hipblasLtMatrixLayoutDestroy(kv.second.lc);
-            (void)hipblasLtMatmulDescDestroy(kv.second.desc);
-        }
-        if (blt) (void)hipblasLtDestroy(blt);
         if (s) (void)hipStreamDestroy(s);
     }
 
@@ -295,9 +272,6 @@ struct qh_ctx {
         acts_buf.release();
         pf.buf.release();
         pf.cap = 0;
-        pf.w16.release();
-        pf.wqkv16.clear();
-        pf.wo16.clear();
         layers_dev.release();
         sync_buf.release();
         rfold.release();
@@ -932,7 +906,7 @@ void prefill_alloc(qh_ctx* c, uint32_t cap) {
     } regs[] = {
         {cap * H * 4, (void**)&P.X},           {cap * H * 4, (void**)&P.Xn32},
         {cap * (qd + 2 * kvd) * 4, (void**)&P.QKV}, {(uint64_t)cap * d.experts * 4 * kPfRouterSplit, (void**)&P.LR},
-        {n_asg * 4, (void**)&P.wts},           {n_asg * H * 4, (void**)&P.Y},
+        {n_asg * 4, (void**)&P.wts},           {std::max<uint64_t>(n_asg, 2ull * cap) * H * 4, (void**)&P.Y},
         {cap * H * 2, (void**)&P.Xn16},        {(uint64_t)d.heads * cap * 128 * 2, (void**)&P.Q16},
         {cap * qd * 2, (void**)&P.O16},        {n_asg * d.ff * 2, (void**)&P.Hs},
         {n_asg * 4, (void**)&P.ids},           {(uint64_t)(d.experts + 1) * 4, (void**)&P.goff},
@@ -960,117 +934,27 @@ template <class F> void dispatch_km(uint32_t kind, F f) {
     else f(std::integral_constant<uint32_t, Q6_K>{});
 }
 
-#define BLT_OK(x)                                                                              \
-    do {                                                                                       \
-        const hipblasStatus_t st_ = (x);                                                       \
-        if (st_ != HIPBLAS_STATUS_SUCCESS) throw Error(std::string(#x) + " failed: status " + std::to_string((int)st_)); \
-    } while (0)
-
-// C[S][N] (= or +=) X16[S][K] W16[N][K]^T on the matrix cores: fp16 operands,
-// f32 accumulation and output (hipBLASLt, column-major C^T = W X^T).
-void pf_dense(qh_ctx* c, const _Float16* W16, uint32_t N, uint32_t K, const _Float16* X16, uint32_t S, float* C,
-              bool accumulate) {
-    if (!c->blt) {
-        BLT_OK(hipblasLtCreate(&c->blt));
-        c->blt_ws.alloc(32u << 20);
+// C[t][cofs_i + n] = X16[t] . W_i[n] for t < S and each matrix i of `mats`
+// (one launch; with `splits` > 1 the columns are split in equal parts, part z
+// written to C + z * split_stride): the MFMA GEMM on the quantised rows
+// (Q4_K / Q6_K dequantised into the tiles).
+void pf_dense(qh_ctx* c, std::initializer_list<std::pair<const DevMat*, uint32_t>> mats, const _Float16* X16,
+              uint32_t S, float* C, uint32_t ldc, uint32_t splits = 1, size_t split_stride = 0) {
+    DenseSegs G{};
+    uint32_t tiles = 0;
+    for (const auto& m : mats) {
+        const DevMat& W = *m.first;
+        if (W.kind != Q4_K && W.kind != Q6_K) throw Error("prefill projection is not Q4_K or Q6_K");
+        if ((W.cols / splits) % 256 || W.cols % splits) throw Error("prefill projection width does not split");
+        G.W[G.n] = W;
+        tiles += (W.rows + 127) / 128;
+        G.tile_end[G.n] = tiles;
+        G.cofs[G.n] = m.second;
+        G.n++;
     }
-    const std::array<uint32_t, 4> key{N, K, S, accumulate ? 1u : 0u};
-    auto it = c->plans.find(key);
-    if (it == c->plans.end()) {
-        qh_ctx::GemmPlan g;
-        BLT_OK(hipblasLtMatmulDescCreate(&g.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F));
-        const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-        BLT_OK(hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta));
-        BLT_OK(hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb));
-        BLT_OK(hipblasLtMatrixLayoutCreate(&g.la, HIP_R_16F, K, N, K));
-        BLT_OK(hipblasLtMatrixLayoutCreate(&g.lb, HIP_R_16F, K, S, K));
-        BLT_OK(hipblasLtMatrixLayoutCreate(&g.lc, HIP_R_32F, N, S, N));
-        hipblasLtMatmulPreference_t pref;
-        BLT_OK(hipblasLtMatmulPreferenceCreate(&pref));
-        const uint64_t wsz = c->blt_ws.n;
-        BLT_OK(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz, sizeof wsz));
-        // the library's first candidates, each timed once on this shape (into a
-        // scratch output: an accumulating projection must not see the trials)
-        constexpr int kCand = 8;
-        hipblasLtMatmulHeuristicResult_t res[kCand] = {};
-        int n = 0;
-        const hipblasStatus_t st =
-            hipblasLtMatmulAlgoGetHeuristic(c->blt, g.desc, g.la, g.lb, g.lc, g.lc, pref, kCand, res, &n);
-        (void)hipblasLtMatmulPreferenceDestroy(pref);
-        if (st != HIPBLAS_STATUS_SUCCESS || n < 1) throw Error("no hipBLASLt algorithm for a prefill projection");
-        int best = 0;
-        if (n > 1) {
-            DevBuf trial;
-            trial.alloc((size_t)N * S * 4);
-            HIP_OK(hipMemsetAsync(trial.p, 0, (size_t)N * S * 4, c->s));
-            hipEvent_t e0, e1;
-            HIP_OK(hipEventCreate(&e0));
-            HIP_OK(hipEventCreate(&e1));
-            const float one = 1.f, zero = 0.f;
-            const float* beta_t = accumulate ? &one : &zero;
-            float best_ms = 0.f;
-            bool found = false;
-            for (int i = 0; i < n; i++) {
-                if (res[i].state != HIPBLAS_STATUS_SUCCESS) continue;
-                auto run = [&] {
-                    return hipblasLtMatmul(c->blt, g.desc, &one, W16, g.la, X16, g.lb, beta_t, trial.p, g.lc, trial.p,
-                                           g.lc, &res[i].algo, c->blt_ws.p, c->blt_ws.n, c->s);
-                };
-                if (run() != HIPBLAS_STATUS_SUCCESS) continue;  // warm-up; a failing candidate is skipped
-                HIP_OK(hipEventRecord(e0, c->s));
-                for (int r = 0; r < 3; r++) (void)run();
-                HIP_OK(hipEventRecord(e1, c->s));
-                HIP_OK(hipEventSynchronize(e1));
-                float ms = 0.f;
-                HIP_OK(hipEventElapsedTime(&ms, e0, e1));
-                if (!found || ms < best_ms) {
-                    best = i;
-                    best_ms = ms;
-                    found = true;
-                }
-            }
-            (void)hipEventDestroy(e0);
-            (void)hipEventDestroy(e1);
-            HIP_OK(hipStreamSynchronize(c->s));  // trials done before the scratch output is freed
-        }
-        g.algo = res[best].algo;
-        it = c->plans.emplace(key, g).first;
-    }
-    const qh_ctx::GemmPlan& g = it->second;
-    const float alpha = 1.f, beta = accumulate ? 1.f : 0.f;
-    BLT_OK(hipblasLtMatmul(c->blt, g.desc, &alpha, W16, g.la, X16, g.lb, &beta, C, g.lc, C, g.lc, &g.algo,
-                           c->blt_ws.p, c->blt_ws.n, c->s));
-}
-
-// fp16 copy of a Q4_K / Q6_K matrix into rows [r0, r0 + m.rows) of dst
-void pf_dequant16(qh_ctx* c, const DevMat& m, uint32_t r0, _Float16* dst) {
-    const uint32_t units = m.rows * (m.cols / 32);
-    dispatch_km(m.kind, [&](auto K) {
-        hipLaunchKernelGGL(k_dequant16<decltype(K)::value>, dim3((units + kBlock - 1) / kBlock), dim3(kBlock), 0, c->s,
-                           m, m.rows, r0, dst);
-    });
-}
-
-// fp16 copies of the dense attention weights of every layer (the same
-// dequantisation as the expert tiles), made once: 2 bytes per weight, 1.8 GB
-// for the 30B model, instead of four copy launches per layer and prefill.
-void prefill_weights(qh_ctx* c) {
-    auto& P = c->pf;
-    if (!P.wqkv16.empty()) return;
-    const ModelDims& d = c->dm;
-    const uint64_t H = d.hidden, qd = (uint64_t)d.heads * 128, kvd = (uint64_t)d.kvheads * 128;
-    const uint64_t nqkv = (qd + 2 * kvd) * H, no = H * qd, per = (nqkv + no + 127) / 128 * 128;
-    P.w16.alloc(per * 2 * c->layers.size());
-    for (size_t l = 0; l < c->layers.size(); l++) {
-        const LayerW& L = c->layers[l];
-        _Float16* q = P.w16.as<_Float16>() + per * l;
-        pf_dequant16(c, L.q, 0, q);
-        pf_dequant16(c, L.k, (uint32_t)qd, q);
-        pf_dequant16(c, L.v, (uint32_t)(qd + kvd), q);
-        pf_dequant16(c, L.o, 0, q + nqkv);
-        P.wqkv16.push_back(q);
-        P.wo16.push_back(q + nqkv);
-    }
+    for (uint32_t i = G.n; i < 3; i++) G.tile_end[i] = tiles;
+    hipLaunchKernelGGL(k_gemm_dense, dim3(tiles, (S + 127) / 128, splits), dim3(256), 0, c->s, X16, S, G, C, ldc,
+                       split_stride);
 }
 
 // One decoder layer (src/model.rs:227-287) for chunk tokens [0, S) at
@@ -1082,9 +966,9 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
     const uint32_t H = d.hidden, qd = d.heads * 128, kvd = d.kvheads * 128, row = qd + 2 * kvd;
     if (l == 0)  // later layers: written by the previous layer's combine
         hipLaunchKernelGGL(k_pf_norm, dim3(S), dim3(kBlock), 0, c->s, P.X, L.attn_norm, H, d.eps, P.Xn16,
-                           (float*)nullptr);
-    // q | k | v as one library GEMM over the fp16 copy of the three matrices
-    pf_dense(c, P.wqkv16[l], row, H, P.Xn16, S, P.QKV, false);
+                           (float*)nullptr, (const float*)nullptr, (size_t)0);
+    // q | k | v: one launch over the three quantised matrices, QKV[t] = [q | k | v]
+    pf_dense(c, {{&L.q, 0u}, {&L.k, qd}, {&L.v, qd + kvd}}, P.Xn16, S, P.QKV, row);
     const uint32_t vp = (d.ctx + 63) / 64 * 64;  // row pitch of the transposed V copy
     if (p0 > 0)  // fp16 copies of this layer's earlier positions
         hipLaunchKernelGGL(k_pf_kvh, dim3(p0), dim3(kBlock), 0, c->s, L.kcache, L.vcache, 0u, d.kvheads, d.ctx, vp,
@@ -1093,8 +977,12 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
                        d.heads, d.kvheads, d.ctx, d.eps, P.Q16, L.kcache, L.vcache, P.Kh, P.Vth, vp);
     hipLaunchKernelGGL(k_pf_attn, dim3((S + 31) / 32, 2 * d.kvheads), dim3(256), 0, c->s, P.Q16, P.Kh, P.Vth, p0, S,
                        d.heads / d.kvheads, d.ctx, vp, qd, P.O16);
-    pf_dense(c, P.wo16[l], H, qd, P.O16, S, P.X, true);  // residual add (model.rs:246-248)
-    hipLaunchKernelGGL(k_pf_norm, dim3(S), dim3(kBlock), 0, c->s, P.X, L.ffn_norm, H, d.eps, P.Xn16, P.Xn32);
+    // o in two column halves (twice the workgroups) into Y's space; the norm
+    // adds both to the residual (model.rs:246-248) before normalising
+    const size_t ostride = (size_t)S * H;
+    pf_dense(c, {{&L.o, 0u}}, P.O16, S, P.Y, H, 2, ostride);
+    hipLaunchKernelGGL(k_pf_norm, dim3(S), dim3(kBlock), 0, c->s, P.X, L.ffn_norm, H, d.eps, P.Xn16, P.Xn32,
+                       (const float*)P.Y, ostride);
     hipLaunchKernelGGL(k_pf_router, dim3((S + 15) / 16, kPfRouterSplit), dim3(kBlock), 0, c->s, P.Xn32, L.router,
                        S, H, d.experts, P.LR);
     hipLaunchKernelGGL(k_pf_topk, dim3((S + kWaves - 1) / kWaves), dim3(kBlock), 0, c->s, P.LR, kPfRouterSplit, S,
@@ -1712,7 +1600,6 @@ int qh_prefill(qh_ctx* c, const uint32_t* prompt, size_t n, float* logits, size_
         if (const char* e = std::getenv("QH_PREFILL_CHUNK")) chunk = std::max<long>(1, std::atol(e));
         const uint32_t cap = (uint32_t)std::min<size_t>({n, chunk, kPrefillChunk, c->context});
         prefill_alloc(c, cap);
-        prefill_weights(c);
         auto& P = c->pf;
         const ModelDims& d = c->dm;
         const uint32_t p_start = (uint32_t)c->pos;

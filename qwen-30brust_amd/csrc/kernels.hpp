@@ -163,4 +163,14 @@ struct ExpertTiles {
     const uint32_t* ntile;  // [1] tiles in use
 };
 
+// Matrices of one dense-projection GEMM launch of the batched prefill
+// (prefill.hip: k_gemm_dense): column tiles [tile_end[i-1], tile_end[i]) of
+// the grid belong to W[i], whose output columns start at cofs[i].
+struct DenseSegs {
+    DevMat W[3];
+    uint32_t tile_end[3];  // cumulative 128-row tiles
+    uint32_t cofs[3];      // output column of row 0
+    uint32_t n;
+};
+
 }  // namespace qh

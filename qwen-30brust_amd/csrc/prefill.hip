@@ -136,7 +136,8 @@ __device__ __forceinline__ void st_p16(_Float16* dst, const uint32_t (&v)[8]) {
 }
 
 // ---------------------------------------------------------------- GEMM --
-// acc[nb][mt][nt] += A[m0 .. m0+128) x W_nb[n0 .. n0+128)^T over K columns.
+// acc[nb][mt][nt] += A[m0 .. m0+128) x W_nb[n0 .. n0+128)^T over columns
+// [kbeg, kbeg + K) (kbeg a multiple of 256).
 // arow: pointer to the fp16 row of tile row r (any valid row when r is past
 // the tile's rows: those outputs are not stored).  wrow[nb]: this thread's
 // weight row (row n0 + tid/2 of matrix nb; likewise any valid row past the
@@ -146,13 +147,14 @@ __device__ __forceinline__ void st_p16(_Float16* dst, const uint32_t (&v)[8]) {
 // loads are unconditional, so each wait covers exactly one stage.
 template <uint32_t KIND, int NB, int STAGES = 1>
 __device__ __forceinline__ void gemm_tile(const _Float16* arow, const uint8_t* const (&wrow)[NB], const RowGeo& g,
-                                          uint32_t K, f4v (&acc)[NB][4][4], _Float16* As, _Float16* Ws) {
+                                          uint32_t K, f4v (&acc)[NB][4][4], _Float16* As, _Float16* Ws,
+                                          uint32_t kbeg = 0) {
     const uint32_t tid = threadIdx.x, r = tid >> 1, h = tid & 1, lane = tid & 63, w = tid >> 6;
     const uint32_t wm = w & 1, wn = w >> 1;
     uint4 av[STAGES][4];
     WSlice<KIND> ws[STAGES][NB];
     auto gload = [&](int st, uint32_t k0) {
-        k0 = min(k0, K - kGK);  // past the end: a harmless reload of the last slice
+        k0 = kbeg + min(k0, K - kGK);  // past the end: a harmless reload of the last slice
         const uint32_t b = k0 >> 8, s = (k0 >> 6) & 3;
 #pragma unroll
         for (int i = 0; i < 4; i++) av[st][i] = gld<uint4>(arow + k0 + 32 * h + 8 * i);
@@ -160,7 +162,7 @@ __device__ __forceinline__ void gemm_tile(const _Float16* arow, const uint8_t* c
         for (int nb = 0; nb < NB; nb++) ws[st][nb].load(wrow[nb], g, b, s, h);
     };
     auto lstore = [&](int st, uint32_t k0) {
-        const uint32_t s = (k0 >> 6) & 3;
+        const uint32_t s = ((kbeg + k0) >> 6) & 3;
 #pragma unroll
         for (int i = 0; i < 4; i++) *reinterpret_cast<uint4*>(As + r * kGL + 32 * h + 8 * i) = av[st][i];
 #pragma unroll
@@ -291,6 +293,53 @@ __global__ __launch_bounds__(kGT) void k_gemm_down(const _Float16* Hs, ExpertTil
             }
 }
 
+// Dense projections (the per-token q/k/v and o matvecs of model.rs:230-232,
+// 245 over a chunk), up to three matrices of either format in one launch so
+// that the small k and v projections share the machine with q:
+// C[m][cofs_i + n] = X16[m] . W_i[n] (columns [kbeg, kbeg + K) of W_i, K =
+// cols / gridDim.z, split z of the columns writing to C + z * split_stride),
+// for m < S, n < W_i.rows.  Column tiles [t_i, t_{i+1}) of gridDim.x belong
+// to matrix i.  Tiles as the expert GEMMs, two register stages of loads ahead
+// of the LDS tile.
+template <uint32_t KIND>
+__device__ __forceinline__ void dense_body(const _Float16* X16, uint32_t S, const DevMat& W, uint32_t n0,
+                                           uint32_t kbeg, uint32_t K, float* C, uint32_t ldc, uint32_t cofs,
+                                           _Float16* smem) {
+    const uint32_t m0 = blockIdx.y * kGM, r = threadIdx.x >> 1, N = W.rows, ld = W.cols;
+    const _Float16* arow = X16 + (size_t)min(m0 + r, S - 1) * ld;
+    const uint8_t* const wrow[1] = {W.w + (size_t)min(n0 + r, N - 1) * W.drb};
+    f4v acc[1][4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) acc[0][mt][nt] = f4v{0.f, 0.f, 0.f, 0.f};
+    gemm_tile<KIND, 1, 2>(arow, wrow, W.geo, K, acc, smem, smem + kGM * kGL, kbeg);
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t m = m0 + acc_row(mt, i), n = n0 + acc_col(nt);
+                if (m < S && n < N) C[(size_t)m * ldc + cofs + n] = acc[0][mt][nt][i];
+            }
+}
+
+__global__ __launch_bounds__(kGT, 2) void k_gemm_dense(const _Float16* X16, uint32_t S, DenseSegs G, float* C,
+                                                    uint32_t ldc, size_t split_stride) {
+    __shared__ __align__(16) _Float16 smem[2 * kGM * kGL];
+    const uint32_t t = blockIdx.x;
+    const uint32_t i = t < G.tile_end[0] ? 0 : t < G.tile_end[1] ? 1 : 2;  // workgroup-uniform
+    const uint32_t t0 = i == 0 ? 0 : G.tile_end[i - 1];
+    const DevMat& W = G.W[i];
+    const uint32_t K = W.cols / gridDim.z, kbeg = blockIdx.z * K;
+    float* Cz = C + blockIdx.z * split_stride;
+    if (W.kind == Q4_K)
+        dense_body<Q4_K>(X16, S, W, (t - t0) * kGN, kbeg, K, Cz, ldc, G.cofs[i], smem);
+    else
+        dense_body<Q6_K>(X16, S, W, (t - t0) * kGN, kbeg, K, Cz, ldc, G.cofs[i], smem);
+}
+
 // ------------------------------------------------------ element kernels --
 // X[t] = embedding row of tokens[t] (model.rs:225), bit-exact decode.
 __global__ __launch_bounds__(kBlock) void k_pf_embed(DevMat emb, const uint32_t* tokens, uint32_t H, uint32_t vocab,
@@ -305,11 +354,24 @@ __global__ __launch_bounds__(kBlock) void k_pf_embed(DevMat emb, const uint32_t*
 }
 
 // RMSNorm (ops.rs:3-15) of row t: fp16 copy (GEMM input), optional fp32 copy.
-__global__ __launch_bounds__(kBlock) void k_pf_norm(const float* X, const float* w, uint32_t H, float eps,
-                                                    _Float16* Y16, float* Y32) {
+// With P: first X[t] += P[0][t] + P[1][t] (the two column halves of the
+// o-projection: the residual add of model.rs:246-248, in that order).
+__global__ __launch_bounds__(kBlock) void k_pf_norm(float* X, const float* w, uint32_t H, float eps,
+                                                    _Float16* Y16, float* Y32, const float* P, size_t pstride) {
     __shared__ float red[kWaves];
     const size_t t = blockIdx.x;
-    const float* x = X + t * H;
+    float* x = X + t * H;
+    if (P) {
+        const float* p0 = P + t * H;
+        const float* p1 = p0 + pstride;
+        for (uint32_t i4 = threadIdx.x; 4 * i4 < H; i4 += kBlock) {
+            const float4 v = reinterpret_cast<const float4*>(x)[i4], a = reinterpret_cast<const float4*>(p0)[i4],
+                         b = reinterpret_cast<const float4*>(p1)[i4];
+            reinterpret_cast<float4*>(x)[i4] =
+                make_float4(v.x + (a.x + b.x), v.y + (a.y + b.y), v.z + (a.z + b.z), v.w + (a.w + b.w));
+        }
+        // each thread reads back only the elements it wrote
+    }
     // 4 consecutive elements per thread (H % 64 == 0), the sum of squares in
     // the same element order as k_pf_combine's
     float ss = 0.f;
@@ -858,29 +920,10 @@ __global__ __launch_bounds__(kBlock) void k_pf_kvh(const float* kcache, const fl
     }
 }
 
-// fp16 copy of rows [0, rows) of a Q4_K / Q6_K matrix into dst rows
-// [r0, r0 + rows) (row pitch = cols), for the dense projections that run as
-// library GEMMs.  One thread per (row, super-block, 64-column slice, half):
-// the same dequantisation as the fused GEMM tiles (WSlice).
-template <uint32_t KIND>
-__global__ __launch_bounds__(kBlock) void k_dequant16(DevMat W, uint32_t rows, uint32_t r0, _Float16* dst) {
-    const uint32_t per_row = W.cols / 32;  // (super-block, slice, half) units
-    const uint32_t i = blockIdx.x * kBlock + threadIdx.x;
-    if (i >= rows * per_row) return;
-    const uint32_t r = i / per_row, u = i % per_row, b = u >> 3, sl = (u >> 1) & 3, h = u & 1;
-    WSlice<KIND> w;
-    w.load(W.w + (size_t)r * W.drb, W.geo, b, sl, h);
-    uint32_t lo[8], hi[8];
-    w.dequant(sl, h, lo, hi);
-    _Float16* o = dst + (size_t)(r0 + r) * W.cols + 256 * b + 64 * sl + 16 * h;
-    st_p16(o, lo);
-    st_p16(o + 32, hi);
-}
-
 #define QH_INSTANTIATE_PREFILL_GEMM(K)                                                                          \
     template __global__ void k_gemm_gateup<K>(const _Float16*, uint32_t, ExpertTiles, DevMat, DevMat, _Float16*);     \
     template __global__ void k_gemm_down<K>(const _Float16*, ExpertTiles, DevMat, float*);                          \
-    template __global__ void k_dequant16<K>(DevMat, uint32_t, uint32_t, _Float16*);
+
 QH_INSTANTIATE_PREFILL_GEMM(Q4_K)
 QH_INSTANTIATE_PREFILL_GEMM(Q6_K)
 
