@@ -179,9 +179,9 @@ int qh_sampler_draw(qh_sampler *sampler, float *out);
 int qh_set_valid_tokens(qh_ctx *ctx, const uint8_t *valid, size_t n);
 /* == Sampler::sample (src/sampling.rs:26-63) on the logits of the last token
  * step, on the device: greedy at temperature 0, else top-k, temperature,
- * top-p and one draw from the stream (consumed only on success).  Errors:
- * "invalid logits"; more than 4096 ids with nonzero probability when top_k is
- * 0 or above 4096 (a limit of the device sampler). */
+ * top-p and one draw from the stream (consumed only on success), over any
+ * number of candidates (up to 4096 sorted in one workgroup's LDS, more in
+ * HBM).  Errors: "invalid logits"; more than 1,048,576 logits. */
 int qh_sample(qh_ctx *ctx, qh_sampler *sampler, uint32_t *out);
 /* The same on n caller logits with an optional mask (valid may be NULL). */
 int qh_sample_logits(qh_ctx *ctx, qh_sampler *sampler, const float *logits, const uint8_t *valid,

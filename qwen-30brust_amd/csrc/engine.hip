@@ -253,7 +253,7 @@ struct qh_ctx {
 
     // sampler: the padding-vocab mask of the loaded model, host-logits upload
     // buffers and the result words
-    DevBuf valid, samp_logits, samp_valid, samp_out;
+    DevBuf valid, samp_logits, samp_valid, samp_out, samp_big;
     size_t valid_n = 0;
 
     ~qh_ctx() {
@@ -1076,8 +1076,8 @@ namespace {
 uint32_t run_sample(qh_ctx* c, qh_sampler* sp, const float* dlogits, const uint8_t* dvalid, size_t n) {
     if (n == 0) throw Error("invalid logits");
     if (n > (1u << 20)) throw Error("the device sampler takes at most 1048576 logits");
-    c->samp_out.reserve(16);
-    c->pin.reserve(16);
+    c->samp_out.reserve(32);
+    c->pin.reserve(32);
     SampleArgs a{};
     a.logits = dlogits;
     a.valid = dvalid;
@@ -1086,17 +1086,42 @@ uint32_t run_sample(qh_ctx* c, qh_sampler* sp, const float* dlogits, const uint8
     a.temperature = sp->temperature;
     a.top_p = sp->top_p;
     a.draw = sp->rng.peek_f32();
+    a.mode = kSampleModeSample;
     a.out = c->samp_out.as<uint32_t>();
     HIP_OK(hipSetDevice(c->device));
-    launch_sample(a, c->s);
-    HIP_OK(hipGetLastError());
-    HIP_OK(hipMemcpyAsync(c->pin.p, a.out, 16, hipMemcpyDeviceToHost, c->s));
-    HIP_OK(hipStreamSynchronize(c->s));
     const uint32_t* r = static_cast<const uint32_t*>(c->pin.p);
+    auto read_out = [&] {
+        HIP_OK(hipGetLastError());
+        HIP_OK(hipMemcpyAsync(c->pin.p, a.out, 32, hipMemcpyDeviceToHost, c->s));
+        HIP_OK(hipStreamSynchronize(c->s));
+    };
+    launch_sample(a, c->s);
+    read_out();
     if (r[1] == kSampleBadLogits) throw Error("invalid logits");
-    if (r[1] == kSampleSupport)
-        throw Error("sampling support of " + std::to_string(r[3]) + " tokens exceeds the device sampler's " +
-                    std::to_string(kSampleMax) + "; set top_k <= " + std::to_string(kSampleMax));
+    if (r[1] == kSampleSupport) {
+        // more candidates than one workgroup sorts in LDS: collect the P ids at
+        // or above the key of rank P - 1 into HBM, sort them there, fold
+        const uint32_t P = r[3];
+        const unsigned long long theta = ((unsigned long long)r[5] << 32) | r[4];
+        const uint32_t K = (a.top_k > 0 && a.top_k < a.n) ? a.top_k : a.n;
+        uint32_t np = 4096;
+        while (np < P) np <<= 1;
+        c->samp_big.reserve((size_t)np * 8 + (size_t)P * 4 + 64);
+        auto* cand = c->samp_big.as<unsigned long long>();
+        float* prob = reinterpret_cast<float*>(cand + np);
+        uint32_t* cnt = reinterpret_cast<uint32_t*>(prob + P);
+        hipLaunchKernelGGL(k_fill_u32, dim3(1), dim3(kBlock), 0, c->s, cnt, (size_t)1, 0u);
+        launch_sample_collect(a, theta, P, np, cand, cnt, c->s);
+        launch_sample_sort(cand, np, c->s);
+        launch_sample_fold(a, cand, prob, P, K, c->s);
+        read_out();
+        if (r[1] == kSampleRank) {  // ids.last() is the id of rank m - 1, past the candidates
+            a.mode = kSampleModeRank;
+            a.rank = r[2] - 1;
+            launch_sample(a, c->s);
+            read_out();
+        }
+    }
     if (r[1] != 0) throw Error("device sampler failed");
     if (sp->temperature != 0.f) sp->rng.word++;
     return r[0];

@@ -135,21 +135,36 @@ struct DecodeArgs {
 };
 
 // Device sampler (sample.hip): src/sampling.rs:26-63 over n logits in HBM.
-constexpr uint32_t kSampleMax = 4096;  // largest candidate list it sorts
+// Up to kSampleMax candidates are sorted in LDS by one workgroup; more go
+// through a global buffer (collected, bitonic-sorted by grid-wide steps,
+// folded by one workgroup).
+constexpr uint32_t kSampleMax = 4096;  // largest candidate list sorted in LDS
 enum : uint32_t {
     kSampleBadLogits = 1u,  // empty or non-finite logits ("invalid logits")
-    kSampleSupport = 2u,    // more than kSampleMax ids with nonzero probability
+    kSampleSupport = 2u,    // more than kSampleMax candidates: out[3] = P, out[4..5] = key of rank P - 1
     kSampleInternal = 3u,   // the candidate selection did not yield the expected count
+    kSampleRank = 4u,       // the pick is the id of rank out[2] - 1, beyond the candidates
 };
+enum : uint32_t { kSampleModeSample = 0u, kSampleModeRank = 1u };
 struct SampleArgs {
     const float* logits;   // [n]
     const uint8_t* valid;  // [n] 0 = masked to f32::MIN, or null
     uint32_t n, top_k;     // top_k 0 = no truncation
     float temperature, top_p;
     float draw;            // rand's gen::<f32>() for this call (unused at temperature 0)
-    uint32_t* out;         // [4] id, status, kept count, candidate count
+    uint32_t mode;         // kSampleModeRank: out[0] = the id of rank `rank` of the sort
+    uint32_t rank;
+    uint32_t* out;         // [8] id, status, kept count, candidate count, key of rank P - 1 (2 words)
 };
 void launch_sample(const SampleArgs& a, hipStream_t s);
+// The candidates beyond kSampleMax: cand[0, np) = the P composite keys >=
+// theta (in any order), then 0 (np a power of two >= P); cnt a zeroed
+// counter.  Then sorted descending and folded (sampling.rs:43-62) into out.
+void launch_sample_collect(const SampleArgs& a, unsigned long long theta, uint32_t P, uint32_t np,
+                           unsigned long long* cand, uint32_t* cnt, hipStream_t s);
+void launch_sample_sort(unsigned long long* cand, uint32_t np, hipStream_t s);
+void launch_sample_fold(const SampleArgs& a, const unsigned long long* cand, float* prob, uint32_t P, uint32_t K,
+                        hipStream_t s);
 
 // Expert work list of the batched-prefill grouped GEMMs (prefill.hip): tile
 // y covers rows [tm, tm + 128) of expert te; the rows of expert e are

@@ -20,6 +20,7 @@
 // stream and is passed in.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cfloat>
 #include <cstdint>
 
@@ -150,6 +151,14 @@ __global__ __launch_bounds__(kST) void k_sample(SampleArgs a) {
         S.flag = 0;
     }
     __syncthreads();
+    if (a.mode == kSampleModeRank) {  // the id of rank a.rank (the last kept id past the candidates)
+        const unsigned long long k = select_rank(S, lg, a.valid, n, a.rank);
+        if (tid == 0) {
+            a.out[0] = ck_index(k);
+            a.out[1] = 0;
+        }
+        return;
+    }
     // 1. finiteness and the first id
     unsigned long long best = 0;
     bool bad = false;
@@ -185,11 +194,15 @@ __global__ __launch_bounds__(kST) void k_sample(SampleArgs a) {
         for (uint32_t i = tid; i < n; i += kST) cnt += expf((masked(lg, a.valid, i) - mx) / T) > 0.f;
         atomicAdd(&S.count, cnt);
         __syncthreads();
-        P = S.count;
+        P = min(S.count, K);
         if (P > kSampleMax) {
+            // the global path: the key of rank P - 1 bounds the candidates
+            const unsigned long long theta = select_rank(S, lg, a.valid, n, P - 1);
             if (tid == 0) {
                 a.out[1] = kSampleSupport;
                 a.out[3] = P;
+                a.out[4] = (uint32_t)theta;
+                a.out[5] = (uint32_t)(theta >> 32);
             }
             return;
         }
@@ -273,8 +286,175 @@ __global__ __launch_bounds__(kST) void k_sample(SampleArgs a) {
     }
 }
 
+// ------------------------------------------------- more than kSampleMax --
+// cand[slot] = composite key of every id at or above theta (exactly P of
+// them); cand[P, np) = 0, below every finite key.
+__global__ __launch_bounds__(kBlock) void k_sample_collect(SampleArgs a, unsigned long long theta, uint32_t P,
+                                                           uint32_t np, unsigned long long* cand, uint32_t* cnt) {
+    const uint32_t stride = gridDim.x * kBlock;
+    for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < a.n; i += stride) {
+        const unsigned long long k = ckey(masked(a.logits, a.valid, i), i);
+        if (k >= theta) {
+            const uint32_t slot = atomicAdd(cnt, 1u);
+            if (slot < P) cand[slot] = k;
+        }
+    }
+    for (uint32_t i = P + blockIdx.x * kBlock + threadIdx.x; i < np; i += stride) cand[i] = 0;
+}
+
+// One compare-exchange step (k, j) of a descending bitonic sort of cand[0, np).
+__global__ __launch_bounds__(kBlock) void k_bitonic_step(unsigned long long* cand, uint32_t np, uint32_t k,
+                                                         uint32_t j) {
+    const uint32_t t = blockIdx.x * kBlock + threadIdx.x;  // pair index < np / 2
+    if (t >= np / 2) return;
+    const uint32_t i = 2 * t - (t & (j - 1)), l = i + j;  // i has bit j clear
+    const unsigned long long x = cand[i], y = cand[l];
+    const bool down = (i & k) == 0;
+    if (down ? x < y : x > y) {
+        cand[i] = y;
+        cand[l] = x;
+    }
+}
+
+// The steps with j < 2048 of stage k for every 4096-key block, in LDS.
+__global__ __launch_bounds__(kST) void k_bitonic_local(unsigned long long* cand, uint32_t k, uint32_t j0) {
+    __shared__ unsigned long long s[4096];
+    const uint32_t base = blockIdx.x * 4096;
+    for (uint32_t i = threadIdx.x; i < 4096; i += kST) s[i] = cand[base + i];
+    __syncthreads();
+    for (uint32_t j = j0; j > 0; j >>= 1) {
+        for (uint32_t t = threadIdx.x; t < 2048; t += kST) {
+            const uint32_t i = 2 * t - (t & (j - 1)), l = i + j;
+            const unsigned long long x = s[i], y = s[l];
+            const bool down = ((base + i) & k) == 0;
+            if (down ? x < y : x > y) {
+                s[i] = y;
+                s[l] = x;
+            }
+        }
+        __syncthreads();
+    }
+    for (uint32_t i = threadIdx.x; i < 4096; i += kST) cand[base + i] = s[i];
+}
+
+// The probabilities of the P sorted candidates (sampling.rs:43-46), then one
+// lane runs the sequential folds of sampling.rs:47-62 in the reference's
+// order, 4096 values at a time staged in LDS.
+__global__ __launch_bounds__(kST) void k_sample_fold(SampleArgs a, const unsigned long long* cand, float* prob,
+                                                     uint32_t P, uint32_t K) {
+    __shared__ float sp[4096];
+    __shared__ uint32_t m_sh;
+    const uint32_t tid = threadIdx.x;
+    const float T = a.temperature, mx = masked(a.logits, a.valid, ck_index(cand[0]));
+    for (uint32_t i = tid; i < P; i += kST) {
+#pragma clang fp contract(off)
+        prob[i] = expf((masked(a.logits, a.valid, ck_index(cand[i])) - mx) / T);
+    }
+    __syncthreads();
+    // total (sampling.rs:47)
+    float total = -0.0f;
+    for (uint32_t c0 = 0; c0 < P; c0 += 4096) {
+        const uint32_t nc = min(4096u, P - c0);
+        for (uint32_t i = tid; i < nc; i += kST) sp[i] = prob[c0 + i];
+        __syncthreads();
+        if (tid == 0) {
+#pragma clang fp contract(off)
+            for (uint32_t i = 0; i < nc; i++) total += sp[i];
+        }
+        __syncthreads();
+    }
+    // the top-p cut (sampling.rs:48-56); m = K when it is never reached
+    float cumulative = 0.f;
+    if (tid == 0) m_sh = K;
+    bool done = false;  // thread 0's state
+    for (uint32_t c0 = 0; c0 < P; c0 += 4096) {
+        const uint32_t nc = min(4096u, P - c0);
+        for (uint32_t i = tid; i < nc; i += kST) sp[i] = prob[c0 + i];
+        __syncthreads();
+        if (tid == 0 && !done) {
+#pragma clang fp contract(off)
+            for (uint32_t i = 0; i < nc; i++) {
+                cumulative += sp[i] / total;
+                if (cumulative >= a.top_p) {
+                    m_sh = c0 + i + 1;
+                    done = true;
+                    break;
+                }
+            }
+        }
+        __syncthreads();
+        if (m_sh != K) break;  // every thread reads the same word after the barrier
+    }
+    const uint32_t m = m_sh, mp = min(m, P);
+    // kept mass, the draw scaled by it, the walk (sampling.rs:57-62)
+    float kept = -0.0f;
+    for (uint32_t c0 = 0; c0 < mp; c0 += 4096) {
+        const uint32_t nc = min(4096u, mp - c0);
+        for (uint32_t i = tid; i < nc; i += kST) sp[i] = prob[c0 + i];
+        __syncthreads();
+        if (tid == 0) {
+#pragma clang fp contract(off)
+            for (uint32_t i = 0; i < nc; i++) kept += sp[i];
+        }
+        __syncthreads();
+    }
+    float draw = a.draw * kept;  // thread 0's value
+    uint32_t pick = 0xffffffffu;
+    for (uint32_t c0 = 0; c0 < mp; c0 += 4096) {
+        const uint32_t nc = min(4096u, mp - c0);
+        for (uint32_t i = tid; i < nc; i += kST) sp[i] = prob[c0 + i];
+        __syncthreads();
+        if (tid == 0 && pick == 0xffffffffu) {
+#pragma clang fp contract(off)
+            for (uint32_t i = 0; i < nc; i++) {
+                if (draw < sp[i]) {
+                    pick = ck_index(cand[c0 + i]);
+                    break;
+                }
+                draw -= sp[i];
+            }
+            m_sh = pick;
+        }
+        __syncthreads();
+        if (m_sh != 0xffffffffu) break;
+    }
+    if (tid == 0) {
+        uint32_t status = 0;
+        if (pick == 0xffffffffu) {  // ids.last()
+            if (m <= P) pick = ck_index(cand[m - 1]);
+            else status = kSampleRank;  // rank m - 1 lies past the candidates (their probabilities are 0)
+        }
+        a.out[0] = pick;
+        a.out[1] = status;
+        a.out[2] = m;
+        a.out[3] = P;
+    }
+}
+
 }  // namespace
 
 void launch_sample(const SampleArgs& a, hipStream_t s) { k_sample<<<1, kST, 0, s>>>(a); }
+
+void launch_sample_collect(const SampleArgs& a, unsigned long long theta, uint32_t P, uint32_t np,
+                           unsigned long long* cand, uint32_t* cnt, hipStream_t s) {
+    const uint32_t grid = std::min<uint32_t>((std::max(a.n, np) + kBlock - 1) / kBlock, 1024);
+    k_sample_collect<<<grid, kBlock, 0, s>>>(a, theta, P, np, cand, cnt);
+}
+
+// Descending bitonic sort of cand[0, np), np a power of two >= 4096: steps
+// with j >= 2048 one launch each over the grid, the rest of a stage in LDS.
+void launch_sample_sort(unsigned long long* cand, uint32_t np, hipStream_t s) {
+    const uint32_t pairs_grid = (np / 2 + kBlock - 1) / kBlock;
+    for (uint32_t k = 2; k <= np; k <<= 1) {
+        uint32_t j = k >> 1;
+        for (; j >= 2048; j >>= 1) k_bitonic_step<<<pairs_grid, kBlock, 0, s>>>(cand, np, k, j);
+        k_bitonic_local<<<np / 4096, kST, 0, s>>>(cand, k, j);
+    }
+}
+
+void launch_sample_fold(const SampleArgs& a, const unsigned long long* cand, float* prob, uint32_t P, uint32_t K,
+                        hipStream_t s) {
+    k_sample_fold<<<1, kST, 0, s>>>(a, cand, prob, P, K);
+}
 
 }  // namespace qh

@@ -40,6 +40,13 @@ CASES = [  # (vocab, scale, temperature, top_k, top_p)
     (4000, 1.0, 1.0, 0, 0.5),      # no top-k, every id a candidate
     (257, 0.5, 2.0, 300, 1.0),     # top_k above the vocabulary
     (3, 1.0, 1.0, 0, 1.0),
+    # more than 4096 candidates: sorted in HBM (sampling.rs:36-63 over the full support)
+    (151936, 1.0, 1.0, 0, 1.0),    # every id has nonzero probability
+    (151936, 1.0, 1.0, 0, 0.9),
+    (151936, 5.0, 1.0, 0, 1.0),    # part of the vocabulary underflows to probability 0
+    (151936, 3.0, 1.0, 10000, 1.0),
+    (151936, 0.5, 2.0, 50000, 0.99),
+    (9000, 1.0, 1.0, 0, 1.0),
 ]
 
 
@@ -78,10 +85,11 @@ def test_sampler_errors_leave_the_stream(dev):
         s.sample(dev, bad)
     with pytest.raises(engine.EngineError, match="invalid logits"):
         s.sample(dev, np.array([1.0, np.inf], np.float32))
-    # a support above 4096 ids is refused (device limit), without a draw
+    with pytest.raises(engine.EngineError, match="at most 1048576 logits"):
+        s.sample(dev, np.zeros((1 << 20) + 1, np.float32))
+    # a flat support of 10,000 ids (the HBM path) draws like the reference
     flat = np.zeros(10000, np.float32)
-    with pytest.raises(engine.EngineError, match="exceeds the device sampler"):
-        s.sample(dev, flat)
+    assert [s.sample(dev, flat) for _ in range(5)] == [ref.sample(flat) for _ in range(5)]
     lg = np.array([1.0, 2.0, 3.0], np.float32)
     assert [s.sample(dev, lg) for _ in range(10)] == [ref.sample(lg) for _ in range(10)]
 
