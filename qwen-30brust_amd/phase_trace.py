@@ -6,8 +6,9 @@ libqwen_hip_trace.so (`python qwen-30brust_amd/build.py trace`).
     python qwen-30brust_amd/phase_trace.py [--layers 48] [--prompt 512] [--tokens 8]
 
 Prints, for each mark, the min / median / max over workgroups of the time
-since the first workgroup reached the layer (microseconds), and the median
-over the traced tokens of each phase's span.
+since the first workgroup reached the layer (microseconds), the median over
+the traced tokens; with --split, separately for the attention workgroups
+(key chunk j < chunks, workgroup b = 8 j + XCD) and the others.
 """
 import argparse
 import ctypes as C
@@ -59,6 +60,7 @@ def main():
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--tokens", type=int, default=8)
+    ap.add_argument("--split", action="store_true", help="attention workgroups and the others apart")
     args = ap.parse_args()
     engine = importlib.import_module("qwen-30brust_amd")
     synth = importlib.import_module("qwen-30brust_amd.synth")
@@ -74,28 +76,37 @@ def main():
     m.generate(prompt, 2)
     lib = C.CDLL(build.TRACE_SO)
     buf = np.zeros((8, 512, 8), np.uint64)
-    rows = {mk: [] for mk, _ in MARKS}
+    classes = ("all", "attention", "other") if args.split else ("all",)
+    rows = {(mk, cl): [] for mk, _ in MARKS for cl in classes}
     for _ in range(args.tokens):
+        T = m.position + 1
+        tc = max((T + 15) // 16, 64)
+        nch = (T + tc - 1) // tc  # key chunks per XCD (decode.hip: attn_chunk)
+        wg = np.arange(512)
+        member = {"all": wg >= 0, "attention": wg // 8 < nch, "other": wg // 8 >= nch}
         assert lib.qh_dtrace_clear() == 0
         m.forward(7, want_logits=False)
         assert lib.qh_dtrace_dump(buf.ctypes.data_as(C.c_void_p)) == 0
         t = buf.astype(np.int64)
         base = t[0, :, 0][t[0, :, 0] > 0].min()
         for (k, p), _ in MARKS:
-            col = t[k, :, p]
-            col = col[col > 0]
-            if col.size:
-                r = (col - base) * 0.01  # 100 MHz ticks -> us
-                rows[(k, p)].append((np.min(r), np.median(r), np.max(r), col.size))
+            for cl in classes:
+                col = t[k, :, p][member[cl]]
+                col = col[col > 0]
+                if col.size:
+                    r = (col - base) * 0.01  # 100 MHz ticks -> us
+                    rows[((k, p), cl)].append((np.min(r), np.median(r), np.max(r), col.size))
     print(f"persistent step, {args.layers} layers, positions {args.prompt + 1}..{m.position - 1}: "
           f"last layer of the token, us since the first workgroup reached it "
           f"(min / median / max over workgroups; median over {args.tokens} tokens)")
     for (k, p), name in MARKS:
-        r = rows[(k, p)]
-        if not r:
-            continue
-        a = np.median(np.array([x[:3] for x in r]), axis=0)
-        print(f"  {name:42s} {a[0]:7.2f} {a[1]:7.2f} {a[2]:7.2f}   (workgroups {r[0][3]})")
+        for cl in classes:
+            r = rows[((k, p), cl)]
+            if not r:
+                continue
+            a = np.median(np.array([x[:3] for x in r]), axis=0)
+            tag = "" if cl == "all" else f" [{cl}]"
+            print(f"  {name + tag:54s} {a[0]:7.2f} {a[1]:7.2f} {a[2]:7.2f}   (workgroups {r[0][3]})")
 
 
 if __name__ == "__main__":
