@@ -201,9 +201,10 @@ int qh_position(const qh_ctx *ctx, size_t *out);
  * logits_cap floats) and argmax (nullable) receive the last prompt token's
  * output.  Numerics: fp16
  * operands with fp32 accumulation (logits within about 1e-2 relative of the
- * FP32 path); fails for models it does not cover (head_dim != 128, more than
- * 8 query heads per KV head, more than 128 experts, projections other than
- * Q4_K/Q6_K). */
+ * FP32 path).  Models the batched path does not cover (head_dim != 128, more
+ * than 8 query heads per KV head, more than 128 experts, projections other
+ * than Q4_K/Q6_K) run the prompt through the exact token step instead, one
+ * per token on the device (the same bits as n qh_forward calls). */
 int qh_prefill(qh_ctx *ctx, const uint32_t *prompt, size_t n, float *logits, size_t logits_cap,
                uint32_t *argmax);
 

@@ -417,7 +417,8 @@ class Model:
 
     def prefill(self, prompt, want_logits=True):
         """Batched prefill of `prompt` from the current position (fp16 matrix
-        cores); returns (greedy id, logits of the last prompt token)."""
+        cores; models outside its coverage run the exact token step per
+        prompt token); returns (greedy id, logits of the last prompt token)."""
         p = np.ascontiguousarray(prompt, np.uint32)
         lg = np.empty(self.config["vocab"], np.float32) if want_logits else None
         am = C.c_uint32()

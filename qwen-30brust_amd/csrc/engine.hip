@@ -1619,8 +1619,23 @@ int qh_prefill(qh_ctx* c, const uint32_t* prompt, size_t n, float* logits, size_
         if (c->pos + n > c->context) throw Error("prompt + max-tokens exceed --ctx");
         for (size_t i = 0; i < n; i++)
             if (prompt[i] >= c->cfg.vocab) throw Error("token outside vocabulary");
-        const std::string gap = prefill_gap(c);
-        if (!gap.empty()) throw Error("batched prefill does not cover this model: " + gap);
+        if (!prefill_gap(c).empty()) {
+            // outside the batched path's coverage (formats, head_dim, ...):
+            // the prompt runs through the exact token step, one per token, on
+            // the device, as the reference's prompt loop does (src/main.rs:250-256)
+            HIP_OK(hipMemcpyAsync(c->acts.tokens + c->pos, prompt, n * 4, hipMemcpyHostToDevice, c->s));
+            put_state(c, (uint32_t)c->pos, (uint32_t)(c->pos + n));
+            for (size_t i = 0; i < n; i++) launch_step(c);
+            DevState st = get_state(c);
+            if (st.err) fail_step(c, st.err);
+            if (logits) HIP_OK(hipMemcpyAsync(logits, c->acts.logits, c->cfg.vocab * 4, hipMemcpyDeviceToHost, c->s));
+            sync(c);
+            if (argmax) *argmax = st.argmax;
+            c->pos += n;
+            c->stats.matvecs += matvecs_per_token(c) * n;
+            c->stats.matvec_ms += now_ms() - t0;
+            return;
+        }
         size_t chunk = kPrefillChunk;
         if (const char* e = std::getenv("QH_PREFILL_CHUNK")) chunk = std::max<long>(1, std::atol(e));
         const uint32_t cap = (uint32_t)std::min<size_t>({n, chunk, kPrefillChunk, c->context});

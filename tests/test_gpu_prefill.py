@@ -131,10 +131,21 @@ def test_prefill_continues_a_sequence(dev, model2):
     check_top1(am, ref)
 
 
-def test_prefill_rejects_uncovered_model(dev):
-    """head_dim 16 (the reference's F32 fixture shape) is outside the batched
-    path: the call fails, it does not fall back."""
+def test_prefill_uncovered_model_runs_the_exact_step(dev):
+    """head_dim 16 with F32 weights (the reference's fixture model) is outside
+    the batched path: the prompt then runs through the exact token step on the
+    device, so the logits, the greedy id, the position and the decode that
+    follows equal a stepwise forward bit for bit."""
     from helpers import GOLDEN
-    m = engine.Model(os.path.join(GOLDEN, "tiny-qwen3moe.gguf"), 4, device=dev)
-    with pytest.raises(engine.EngineError, match="batched prefill does not cover"):
-        m.prefill(np.array([1, 5], np.uint32))
+    path = os.path.join(GOLDEN, "tiny-qwen3moe.gguf")
+    m = engine.Model(path, 8, device=dev)
+    prompt = np.array([1, 5, 2, 9], np.uint32)
+    am, lg = m.prefill(prompt)
+    assert m.position == 4
+    assert am == int(np.argmax(lg))
+    nxt = m.forward(am)
+    ref = engine.Model(path, 8, device=dev)
+    for t in prompt:
+        ref_lg = ref.forward(int(t))
+    assert np.array_equal(lg, ref_lg)
+    assert np.array_equal(nxt, ref.forward(int(np.argmax(ref_lg))))
