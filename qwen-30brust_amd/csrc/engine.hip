@@ -953,7 +953,7 @@ void pf_dense(qh_ctx* c, std::initializer_list<std::pair<const DevMat*, uint32_t
         G.n++;
     }
     for (uint32_t i = G.n; i < 3; i++) G.tile_end[i] = tiles;
-    hipLaunchKernelGGL(k_gemm_dense, dim3(tiles, (S + 127) / 128, splits), dim3(256), 0, c->s, X16, S, G, C, ldc,
+    hipLaunchKernelGGL(k_gemm_dense, dim3(8 * ((S + 1023) / 1024) * tiles, 1, splits), dim3(256), 0, c->s, X16, S, G, C, ldc,
                        split_stride);
 }
 
@@ -992,11 +992,11 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
     const ExpertTiles T{P.goff, P.tok, P.asg, P.te, P.tm, P.ntile};
     const uint32_t tiles = (S * d.top + 127) / 128 + d.experts;
     dispatch_km(L.gate.kind, [&](auto K) {
-        hipLaunchKernelGGL(k_gemm_gateup<decltype(K)::value>, dim3((d.ff + 127) / 128, tiles), dim3(256), 0, c->s,
+        hipLaunchKernelGGL(k_gemm_gateup<decltype(K)::value>, dim3(8 * ((tiles + 7) / 8) * ((d.ff + 127) / 128)), dim3(256), 0, c->s,
                            P.Xn16, H, T, L.gate, L.up, P.Hs);
     });
     dispatch_km(L.down.kind, [&](auto K) {
-        hipLaunchKernelGGL(k_gemm_down<decltype(K)::value>, dim3((H + 127) / 128, tiles), dim3(256), 0, c->s, P.Hs, T,
+        hipLaunchKernelGGL(k_gemm_down<decltype(K)::value>, dim3(8 * ((tiles + 7) / 8) * ((H + 127) / 128)), dim3(256), 0, c->s, P.Hs, T,
                            L.down, P.Y);
     });
     // + the next layer's attention RMSNorm (fp16 operand of its q|k|v GEMM)

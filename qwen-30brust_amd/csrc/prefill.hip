@@ -212,6 +212,18 @@ __device__ __forceinline__ void gemm_tile(const _Float16* arow, const uint8_t* c
     }
 }
 
+// XCD-aware tile order.  Workgroup b runs on XCD b % 8 (each XCD has its own
+// L2).  The grid is 1-D: XCD x takes the row tiles t = x, x + 8, ... and, for
+// each in turn, all nn column tiles, so that one row tile's activations (read
+// by every column tile) stay in that XCD's L2 while its column tiles run.
+// Returns (row tile, column tile) of this workgroup; the grid holds
+// 8 * ceil(row tiles / 8) * nn workgroups.
+__device__ __forceinline__ void xcd_tile(uint32_t nn, uint32_t& t, uint32_t& n) {
+    const uint32_t b = blockIdx.x, x = b & 7, i = b >> 3;
+    t = x + 8 * (i / nn);
+    n = i % nn;
+}
+
 // Output element of acc[.][mt][nt][i] for this lane: tile row / column.
 __device__ __forceinline__ uint32_t acc_row(uint32_t mt, uint32_t i) {
     const uint32_t lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) & 1;
@@ -228,10 +240,12 @@ template <uint32_t KIND>
 __global__ __launch_bounds__(kGT, 2) void k_gemm_gateup(const _Float16* Xn, uint32_t H, ExpertTiles G, DevMat Wg, DevMat Wu,
                                                      _Float16* Hs) {
     __shared__ __align__(16) _Float16 smem[3 * kGM * kGL];
-    if (blockIdx.y >= *G.ntile) return;
-    const uint32_t e = G.te[blockIdx.y], mt0 = G.tm[blockIdx.y];
+    uint32_t ty, tx;
+    xcd_tile((Wg.rows + kGN - 1) / kGN, ty, tx);
+    if (ty >= *G.ntile) return;
+    const uint32_t e = G.te[ty], mt0 = G.tm[ty];
     const uint32_t base = G.goff[e], rows = G.goff[e + 1] - base;
-    const uint32_t n0 = blockIdx.x * kGN, r = threadIdx.x >> 1, ff = Wg.rows;
+    const uint32_t n0 = tx * kGN, r = threadIdx.x >> 1, ff = Wg.rows;
     const _Float16* arow = Xn + (size_t)(mt0 + r < rows ? G.tok[base + mt0 + r] : 0u) * H;
     const uint32_t wr = min(n0 + r, ff - 1);
     const uint8_t* const wrow[2] = {Wg.w + e * Wg.expert_stride + (size_t)wr * Wg.drb,
@@ -263,10 +277,12 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_gateup(const _Float16* Xn, uint
 template <uint32_t KIND>
 __global__ __launch_bounds__(kGT) void k_gemm_down(const _Float16* Hs, ExpertTiles G, DevMat Wd, float* Y) {
     __shared__ __align__(16) _Float16 smem[2 * kGM * kGL];
-    if (blockIdx.y >= *G.ntile) return;
-    const uint32_t e = G.te[blockIdx.y], mt0 = G.tm[blockIdx.y];
+    uint32_t ty, tx;
+    xcd_tile((Wd.rows + kGN - 1) / kGN, ty, tx);
+    if (ty >= *G.ntile) return;
+    const uint32_t e = G.te[ty], mt0 = G.tm[ty];
     const uint32_t base = G.goff[e], rows = G.goff[e + 1] - base;
-    const uint32_t n0 = blockIdx.x * kGN, r = threadIdx.x >> 1, ff = Wd.cols, N = Wd.rows;
+    const uint32_t n0 = tx * kGN, r = threadIdx.x >> 1, ff = Wd.cols, N = Wd.rows;
     const _Float16* arow = Hs + (size_t)(base + min(mt0 + r, rows - 1)) * ff;
     const uint8_t* const wrow[1] = {Wd.w + e * Wd.expert_stride + (size_t)min(n0 + r, N - 1) * Wd.drb};
     // output rows of this lane's accumulators: their assignment indices,
@@ -302,10 +318,10 @@ __global__ __launch_bounds__(kGT) void k_gemm_down(const _Float16* Hs, ExpertTil
 // to matrix i.  Tiles as the expert GEMMs, two register stages of loads ahead
 // of the LDS tile.
 template <uint32_t KIND>
-__device__ __forceinline__ void dense_body(const _Float16* X16, uint32_t S, const DevMat& W, uint32_t n0,
-                                           uint32_t kbeg, uint32_t K, float* C, uint32_t ldc, uint32_t cofs,
-                                           _Float16* smem) {
-    const uint32_t m0 = blockIdx.y * kGM, r = threadIdx.x >> 1, N = W.rows, ld = W.cols;
+__device__ __forceinline__ void dense_body(const _Float16* X16, uint32_t S, const DevMat& W, uint32_t m0,
+                                           uint32_t n0, uint32_t kbeg, uint32_t K, float* C, uint32_t ldc,
+                                           uint32_t cofs, _Float16* smem) {
+    const uint32_t r = threadIdx.x >> 1, N = W.rows, ld = W.cols;
     const _Float16* arow = X16 + (size_t)min(m0 + r, S - 1) * ld;
     const uint8_t* const wrow[1] = {W.w + (size_t)min(n0 + r, N - 1) * W.drb};
     f4v acc[1][4][4];
@@ -328,16 +344,18 @@ __device__ __forceinline__ void dense_body(const _Float16* X16, uint32_t S, cons
 __global__ __launch_bounds__(kGT, 2) void k_gemm_dense(const _Float16* X16, uint32_t S, DenseSegs G, float* C,
                                                     uint32_t ldc, size_t split_stride) {
     __shared__ __align__(16) _Float16 smem[2 * kGM * kGL];
-    const uint32_t t = blockIdx.x;
+    uint32_t mt, t;
+    xcd_tile(G.tile_end[2], mt, t);  // row tile (tokens), column tile
+    if (mt * kGM >= S) return;
     const uint32_t i = t < G.tile_end[0] ? 0 : t < G.tile_end[1] ? 1 : 2;  // workgroup-uniform
     const uint32_t t0 = i == 0 ? 0 : G.tile_end[i - 1];
     const DevMat& W = G.W[i];
     const uint32_t K = W.cols / gridDim.z, kbeg = blockIdx.z * K;
     float* Cz = C + blockIdx.z * split_stride;
     if (W.kind == Q4_K)
-        dense_body<Q4_K>(X16, S, W, (t - t0) * kGN, kbeg, K, Cz, ldc, G.cofs[i], smem);
+        dense_body<Q4_K>(X16, S, W, mt * kGM, (t - t0) * kGN, kbeg, K, Cz, ldc, G.cofs[i], smem);
     else
-        dense_body<Q6_K>(X16, S, W, (t - t0) * kGN, kbeg, K, Cz, ldc, G.cofs[i], smem);
+        dense_body<Q6_K>(X16, S, W, mt * kGM, (t - t0) * kGN, kbeg, K, Cz, ldc, G.cofs[i], smem);
 }
 
 // ------------------------------------------------------ element kernels --
