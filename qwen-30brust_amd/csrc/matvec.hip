@@ -293,11 +293,13 @@ bool launch_kind(const MvShape& s, const MvArgs& a, uint64_t ngrp, uint32_t num_
 // y[b][r] = sum_c W_b[r][c] x[b][c] for b < nb, W_b at mats[b] with the
 // shape and format of m.  Returns false (nothing launched) for shapes this
 // kernel does not cover: formats that are not block-quantised, rows longer
-// than 256 chunks, more than kMvMaxVec vectors or more x than LDS holds.
+// than 256 chunks, more than kMvMaxVec vectors, more x than LDS holds, x not
+// 16-byte aligned, or a matrix past 32-bit byte offsets.
 bool launch_mv_stream(const DevMat& m, const uint8_t* const* mats, uint32_t nb, const float* x, float* y,
                       uint32_t num_cu, hipStream_t st) {
     const bool quant = m.kind == Q4_0 || m.kind == Q8_0 || m.kind == Q4_K || m.kind == Q5_K || m.kind == Q6_K;
     if (!quant || nb == 0 || nb > kMvMaxVec || m.rows == 0 || m.cols % 32 != 0) return false;
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return false;  // x is staged with 16-byte loads
     const uint32_t cpr = m.cols / 32, xpitch = (m.cols + 63) / 64 * 64;
     if (cpr > 256 || (uint64_t)nb * xpitch > kMvMaxXFloats) return false;
     if ((uint64_t)m.rows * m.drb + 64 >= (1ull << 32)) return false;  // 32-bit buffer offsets
