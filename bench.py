@@ -235,7 +235,8 @@ def main():
         # the k_decode launch alone, timed with HIP events on its stream
         ms_embed, ms_decode = model.profile_decode(args.profile_steps)
         decode_launch = {"ms_embed": round(ms_embed, 4), "ms_decode": round(ms_decode, 4)}
-        log(f"persistent step: k_embed {ms_embed*1e3:.1f} us, k_decode {ms_decode*1e3:.1f} us per token")
+        log(f"persistent step: k_decode {ms_decode*1e3:.1f} us per token (embedding row included; "
+            f"empty interval before it {ms_embed*1e3:.1f} us)")
     pos_mid = pos_start + args.warmup + args.steps + (args.profile_steps if persistent else 0)
     # the per-phase kernels: timed as a second line, and profiled one kernel
     # class at a time (HIP events between direct launches)

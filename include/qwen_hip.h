@@ -245,9 +245,11 @@ int qh_fault_inject(qh_ctx *ctx, uint32_t kind);
 
 /* Persistent-step timing (no counterpart in the reference): `steps` decode
  * steps continuing from the current position, with HIP events on the
- * context's stream around each kernel of the step; ms_embed / ms_decode
- * receive the mean milliseconds of the embedding kernel and of the one
- * k_decode launch per token.  Fails unless the persistent step is selected. */
+ * context's stream around the step's one k_decode launch; ms_decode receives
+ * its mean milliseconds per token.  ms_embed receives the time between the
+ * step's first event and that launch (the embedding row is computed inside
+ * k_decode, so it is an empty interval).  Fails unless the persistent step is
+ * selected. */
 int qh_profile_decode(qh_ctx *ctx, size_t steps, double *ms_embed, double *ms_decode);
 
 /* Benchmark surface: `warmup` untimed then `steps` timed greedy decode steps

@@ -1,6 +1,6 @@
-// Persistent token step (src/model.rs:227-302 and the greedy sampler,
+// Persistent token step (src/model.rs:222-302 and the greedy sampler,
 // src/sampling.rs:26-35) as ONE launch of one 512-thread workgroup per CU,
-// preceded by k_embed (the embedding row of tokens[pos], model.rs:225).
+// the embedding row of tokens[pos] (model.rs:225) included.
 //
 // Placement.  MI355X has 8 XCDs of 32 CUs, each XCD with its own L2, and the
 // dispatcher places workgroup b on XCD b % 8 (checked at set-up and again by
@@ -124,6 +124,7 @@ struct DecodeLds {
 struct Ctx {
     uint32_t b, nwg, X, j, tid, wv, lane, gw;
     uint32_t pos, T, H, E, top, ff, qd, ctx;
+    uint32_t tok;  // tokens[pos]
 };
 
 // A copy of the launch constants whose per-lane fields are opaque to the
@@ -381,8 +382,20 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
     float* xs = S.big;
     QH_MARK(0, 0);
     if (l == A.l0) {
-        // x as the embedding kernel (or the host) left it before this launch
-        *reinterpret_cast<float4*>(xs + px(4 * c.tid)) = ld_sys4(buf_rsrc(A.a.x, c.H * 4), c.tid * 16);
+        if (A.embed) {
+            // the embedding row of tokens[pos] (model.rs:225), bit-exact
+            // decode, four elements per thread
+            const uint8_t* row = A.emb.w + (size_t)c.tok * A.emb.drb;
+            float4 e;
+            e.x = dequant_value(row, A.emb.kind, A.emb.geo, 4 * c.tid);
+            e.y = dequant_value(row, A.emb.kind, A.emb.geo, 4 * c.tid + 1);
+            e.z = dequant_value(row, A.emb.kind, A.emb.geo, 4 * c.tid + 2);
+            e.w = dequant_value(row, A.emb.kind, A.emb.geo, 4 * c.tid + 3);
+            *reinterpret_cast<float4*>(xs + px(4 * c.tid)) = e;
+        } else {
+            // x as the host left it before this launch
+            *reinterpret_cast<float4*>(xs + px(4 * c.tid)) = ld_sys4(buf_rsrc(A.a.x, c.H * 4), c.tid * 16);
+        }
         __syncthreads();
     } else if (!gather_l(A, S, lbuf(A.lx2, kDecodeStrideX2, c.X), c.H, ptag(A, l - 1, 7), xs, c.tid)) {
         return false;  // x'' of the previous layer (phase R)
@@ -1027,19 +1040,6 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
 }
 
 // ================================================================= kernels ==
-// Embedding row of tokens[pos] into x (model.rs:225), bit-exact decode.
-__global__ __launch_bounds__(kBlock) void k_embed(DevMat emb, Acts a, ModelDims dm) {
-    const uint32_t pos = a.st->pos;
-    if (pos >= dm.ctx) return;  // reported by the step kernel
-    const uint32_t tok = a.tokens[pos];
-    if (tok >= dm.vocab) {
-        if (threadIdx.x == 0) atomicOr(&a.st->err, kErrToken);
-        return;
-    }
-    const uint8_t* row = emb.w + (size_t)tok * emb.drb;
-    for (uint32_t i = threadIdx.x; i < dm.hidden; i += kBlock) a.x[i] = dequant_value(row, emb.kind, emb.geo, i);
-}
-
 // XCD of the calling wave (hardware register XCC_ID, bits 3:0).
 __device__ __forceinline__ uint32_t xcc_id() {
     uint32_t x;
@@ -1075,6 +1075,11 @@ __global__ __launch_bounds__(kDT) void k_decode(DecodeArgs A) {
     __syncthreads();
     if (c.pos >= dm.ctx || (err0 & kErrToken)) {
         if (c.b == 0 && c.tid == 0 && c.pos >= dm.ctx) atomicOr(&A.a.st->err, kErrContext);
+        return;
+    }
+    c.tok = A.embed ? A.a.tokens[c.pos] : 0u;
+    if (c.tok >= dm.vocab) {  // model.rs:222; every workgroup reads the same id
+        if (c.b == 0 && c.tid == 0) atomicOr(&A.a.st->err, kErrToken);
         return;
     }
     if (ld_sys_u(A.abort_flag) != 0) {

@@ -45,7 +45,6 @@ template <int C> __global__ void k_down(LayerW, Acts, ModelDims);
 template <int C> __global__ void k_vocab(DevMat, const float*, Acts, ModelDims);
 __global__ void k_finish(Acts, ModelDims, uint32_t);
 // Persistent token step (decode.hip).
-__global__ void k_embed(DevMat, Acts, ModelDims);
 __global__ void k_decode(DecodeArgs);
 __global__ void k_xcd_map(uint32_t*);
 // Streaming quantised matvec (matvec.hip).
@@ -658,7 +657,7 @@ void clear_words(qh_ctx* c, void* p, size_t bytes) {
 
 // One cooperative launch of k_decode over layers [l0, l1); vocab: also the
 // final norm, vocab projection, argmax and position advance.
-void launch_decode(qh_ctx* c, uint32_t l0, uint32_t l1, bool vocab) {
+void launch_decode(qh_ctx* c, uint32_t l0, uint32_t l1, bool vocab, bool embed) {
     if (!(l0 < l1 && l1 <= c->layers.size())) throw Error("decode launch needs a non-empty layer range");
     const uint32_t phases = kDecodePhases * (l1 - l0) + (vocab ? 1 : 0);
     if (c->flag_base > 0xFFFFFFFFu - phases) {
@@ -672,6 +671,7 @@ void launch_decode(qh_ctx* c, uint32_t l0, uint32_t l1, bool vocab) {
     A.l0 = l0;
     A.l1 = l1;
     A.vocab = vocab ? 1u : 0u;
+    A.embed = embed ? 1u : 0u;
     c->flag_base += phases;
     void* args[] = {&A};
     HIP_OK(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_decode), dim3(c->nwg), dim3(512), args, 0,
@@ -681,8 +681,7 @@ void launch_decode(qh_ctx* c, uint32_t l0, uint32_t l1, bool vocab) {
 // One token step: the captured graph, or the same kernels launched directly.
 void launch_step(qh_ctx* c) {
     if (c->persist) {
-        hipLaunchKernelGGL(k_embed, dim3(1), dim3(kBlock), 0, c->s, c->emb, c->acts, c->dm);
-        launch_decode(c, 0, (uint32_t)c->layers.size(), true);
+        launch_decode(c, 0, (uint32_t)c->layers.size(), true, true);
         return;
     }
     if (c->use_graph) {
@@ -1712,7 +1711,7 @@ int qh_layer_forward(qh_ctx* c, size_t layer, float* x, size_t pos, const float*
         }
         put_state(c, (uint32_t)pos, (uint32_t)pos + 1);
         if (c->persist)
-            launch_decode(c, (uint32_t)layer, (uint32_t)layer + 1, false);
+            launch_decode(c, (uint32_t)layer, (uint32_t)layer + 1, false, false);
         else
             enqueue_layer(c, layer, false);
         HIP_OK(hipGetLastError());
@@ -1796,10 +1795,11 @@ int qh_profile_decode(qh_ctx* c, size_t steps, double* ms_embed, double* ms_deco
         double acc[2] = {0.0, 0.0};
         put_state(c, (uint32_t)c->pos, (uint32_t)c->pos);
         for (size_t s = 0; s < steps; s++) {
+            // the step is one launch (the embedding row included): the first
+            // interval is empty
             HIP_OK(hipEventRecord(ev[0], c->s));
-            hipLaunchKernelGGL(k_embed, dim3(1), dim3(kBlock), 0, c->s, c->emb, c->acts, c->dm);
             HIP_OK(hipEventRecord(ev[1], c->s));
-            launch_decode(c, 0, (uint32_t)c->layers.size(), true);
+            launch_decode(c, 0, (uint32_t)c->layers.size(), true, true);
             HIP_OK(hipEventRecord(ev[2], c->s));
             HIP_OK(hipEventSynchronize(ev[2]));
             for (int k = 0; k < 2; k++) {

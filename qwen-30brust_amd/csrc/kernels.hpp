@@ -132,6 +132,7 @@ struct DecodeArgs {
     uint64_t* tfin;        // [gridDim.x][2] vocab argmax partials (key, index)
     uint32_t base;         // tag before this launch's first phase
     uint32_t l0, l1, vocab;
+    uint32_t embed;        // 1: x of layer l0 is the embedding row of tokens[pos]; 0: the x the host left
 };
 
 // Device sampler (sample.hip): src/sampling.rs:26-63 over n logits in HBM.
