@@ -309,14 +309,16 @@ struct AttnPre {
 __device__ __forceinline__ void kv_slice(float4 (&kr)[4], float4 (&vr)[4], const float* kc, const float* vc,
                                          uint32_t g, uint32_t ctx, uint32_t tt, uint32_t t1, uint32_t pos,
                                          uint32_t tid) {
-    const uint32_t key = tt + (tid >> 3), j = (tid & 7) * 16;
+    // part p = tid % 8 holds dims 32 i + 4 p .. 32 i + 4 p + 3 (i < 4): load
+    // i of the 8 parts of a key is one contiguous 128-byte run
+    const uint32_t key = tt + (tid >> 3), j = (tid & 7) * 4;
     if (key < t1 && key != pos) {
         const float* ks = kc + ((size_t)g * ctx + key) * 128 + j;
         const float* vs = vc + ((size_t)g * ctx + key) * 128 + j;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            kr[i] = gld<float4>(ks + 4 * i);
-            vr[i] = gld<float4>(vs + 4 * i);
+            kr[i] = gld<float4>(ks + 32 * i);
+            vr[i] = gld<float4>(vs + 32 * i);
         }
     }
 }
@@ -443,8 +445,9 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
 
 // ============================================================ B: attention ==
 // Chunk j of the keys for the XCD's 4 query heads, in 64-key tiles:
-//   scores   thread (key tid/8, 16-dim part tid%8) holds its K slice in
-//            registers and reduces the 8 parts of each head on DPP;
+//   scores   thread (key tid/8, part p = tid%8: dims 32i+4p..32i+4p+3 for
+//            i < 4) holds its K slice in registers and reduces the 8 parts
+//            of each head on DPP;
 //   softmax  wave h < 4 owns head h (lane = key), online over the tiles;
 //   P.V      v_mfma_f32_16x16x4_f32: the heads are the M rows (4 of 16
 //            used), 16 dims per wave, 4 keys per step.
@@ -491,7 +494,7 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
         }
     }
     QH_MARK(1, 1);
-    float* qs = S.big;               // [4][160]  normalised, rotated queries (16-dim parts padded to 20)
+    float* qs = S.big;               // [4][160]  normalised, rotated queries (the 16 dims of a part padded to 20)
     float* kn = qs + 4 * 160;        // [160]     new key, same layout
     float* vn = kn + 160;            // [128]     new value
     float* vs = vn + 128;            // [64][kTP] value tile
@@ -509,8 +512,10 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
             o0 = y0 * cs.x - y1 * cs.y;
             o1 = y0 * cs.y + y1 * cs.x;
         }
-        dst[(lane / 16) * 20 + lane % 16] = o0;
-        dst[((lane + 64) / 16) * 20 + lane % 16] = o1;
+        // dim d belongs to part (d / 4) % 8, float4 d / 32 of it
+        const uint32_t e = ((lane >> 2) & 7) * 20 + (lane & 3);
+        dst[e + 4 * (lane >> 5)] = o0;
+        dst[e + 4 * ((lane + 64) >> 5)] = o1;
         if (append) {  // KV append (model.rs:241-243)
             L.kcache[((size_t)g * ctx + pos) * 128 + lane] = o0;
             L.kcache[((size_t)g * ctx + pos) * 128 + lane + 64] = o1;
@@ -540,10 +545,10 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 kr[i] = reinterpret_cast<const float4*>(kn + part * 20)[i];
-                vr[i] = reinterpret_cast<const float4*>(vn + part * 16)[i];
+                vr[i] = *reinterpret_cast<const float4*>(vn + 32 * i + 4 * part);
             }
         }
-        // scores: thread (key kt, 16-dim part) holds its K slice in registers;
+        // scores: thread (key kt, part) holds its 16 dims of K in registers;
         // the 8 parts of each head reduce on DPP
         float mine = 0.f;
 #pragma unroll
@@ -571,7 +576,7 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
             const bool in = kt < nt;
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                reinterpret_cast<float4*>(vs + kt * kTP + part * 16)[i] = in ? vr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                *reinterpret_cast<float4*>(vs + kt * kTP + 32 * i + 4 * part) = in ? vr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
             if (in && part < kHX) ps[part * kPP + kt] = mine / root;
         }
         if (tt + kDTile < t1) kv_slice(kr, vr, L.kcache, L.vcache, g, ctx, tt + kDTile, t1, pos, tid);
@@ -732,6 +737,13 @@ __device__ __forceinline__ bool phase_xr1(const DecodeArgs& A, DecodeLds& S, con
     return true;
 }
 
+// v (64-bit) of lane l of the wave, into scalar registers.
+__device__ __forceinline__ long long readlane64(long long v, uint32_t l) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(uint64_t)v, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), l);
+    return (long long)(((uint64_t)hi << 32) | lo);
+}
+
 // ============================================ E: routing, gate/up, SwiGLU ==
 // Gathers x' and the unscaled router logits u; the ffn RMSNorm scale
 // s = 1/sqrt(mean(x'^2) + eps) (ops.rs:3-15) gives logit e = s u_e.  Then
@@ -775,21 +787,25 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         return false;  // every workgroup sees the same logits
     }
     {
-        // thread (i, q) counts the keys of quarter q (32 of them) above expert i's
-        const uint32_t i = c.tid >> 2, q = c.tid & 3;
-        const long long ki = S.ck[i];
-        // all 16 reads issued before any compare (one LDS round trip)
-        longlong2 w2[16];
+        static_assert(kDW * 16 == 128, "eight waves rank 16 experts each");
+        // wave wv ranks experts 16 wv .. 16 wv + 15: each lane holds keys lane
+        // and lane + 64; expert i's key is read from its lane into scalar
+        // registers, and its rank is the number of set bits of two ballots
+        // "key above expert i's" (two LDS reads per lane, no LDS round trip
+        // per expert); lane t < 16 then places expert 16 wv + t
+        const long long k0 = S.ck[c.lane], k1 = S.ck[c.lane + 64];
+        const long long kw = c.wv < kDW / 2 ? k0 : k1;  // keys 16 wv .. 16 wv + 15 sit in lanes 16 (wv % 4) + t
+        uint32_t mine = 0;
 #pragma unroll
-        for (uint32_t k = 0; k < 16; k++) w2[k] = reinterpret_cast<const longlong2*>(S.ck + 32 * q)[k];
-        int32_t rank = 0;
-#pragma unroll
-        for (uint32_t k = 0; k < 16; k++) rank += (w2[k].x > ki) + (w2[k].y > ki);
-        rank += dpp_i<kDppXor1>(rank);
-        rank += dpp_i<kDppXor2>(rank);
-        if (q == 0 && i < E && (uint32_t)rank < top) {
-            S.sid[rank] = i;
-            S.sv[rank] = S.lg[i];
+        for (uint32_t t = 0; t < 16; t++) {
+            const long long ki = readlane64(kw, 16 * (c.wv & 3) + t);
+            const uint32_t rank = (uint32_t)(__popcll(__ballot(k0 > ki)) + __popcll(__ballot(k1 > ki)));
+            mine = c.lane == t ? rank : mine;
+        }
+        const uint32_t i = 16 * c.wv + c.lane;
+        if (c.lane < 16 && i < E && mine < top) {
+            S.sid[mine] = i;
+            S.sv[mine] = S.lg[i];
         }
     }
     __syncthreads();
