@@ -56,6 +56,7 @@ template <uint32_t K> __global__ void k_gemm_gateup(const _Float16*, uint32_t, E
 template <uint32_t K> __global__ void k_gemm_down(const _Float16*, ExpertTiles, DevMat, float*);
 __global__ void k_gemm_dense(const _Float16*, uint32_t, DenseSegs, float*, uint32_t, size_t);
 __global__ void k_pf_embed(DevMat, const uint32_t*, uint32_t, uint32_t, float*, DevState*);
+__global__ void k_tile_gemm(DevMat, uint32_t, uint8_t*);
 __global__ void k_pf_norm(float*, const float*, uint32_t, float, _Float16*, float*, const float*, size_t);
 __global__ void k_pf_qkrope(const float*, const float*, const float*, const float2*, uint32_t, uint32_t, uint32_t,
                             uint32_t, uint32_t, float, _Float16*, float*, float*, _Float16*, _Float16*, uint32_t);
@@ -220,7 +221,7 @@ struct qh_ctx {
 
     // persistent token step (k_decode): one cooperative launch per token
     bool persist_ok = false;  // the model's formats and shapes are covered
-    bool persist = false;     // and it is enabled (QH_NO_PERSIST=1 or qh_set_persistent(0) disable it)
+    bool persist = false;     // and it is enabled (qh_set_persistent(0) disables it; QH_NO_PERSIST=1 at load leaves it out)
     uint32_t nwg = 0;         // workgroups of k_decode (one per CU)
     uint32_t flag_base = 0;   // tag of the last phase launched
     DevBuf layers_dev, sync_buf;  // sync_buf: abort flag and tagged exchange words
@@ -244,6 +245,11 @@ struct qh_ctx {
         uint32_t *ids = nullptr, *goff = nullptr, *tok = nullptr, *asg = nullptr, *te = nullptr, *tm = nullptr,
                  *ntile = nullptr;
         uint32_t max_tiles = 0;
+        // tile-layout copies of the GEMMs' matrices (DevMat::wt of q, k, v,
+        // o, gate, up, down of every layer), built on the first batched
+        // prefill: as many bytes again as those matrices' row layout
+        DevBuf tiles;
+        bool tiled = false;
     } pf;
 
     // scratch for the API surfaces
@@ -271,6 +277,8 @@ struct qh_ctx {
         acts_buf.release();
         pf.buf.release();
         pf.cap = 0;
+        pf.tiles.release();
+        pf.tiled = false;
         layers_dev.release();
         sync_buf.release();
         rfold.release();
@@ -581,14 +589,20 @@ bool xcd_placement_ok(qh_ctx* c, uint32_t nwg) {
 }
 
 void setup_persist(qh_ctx* c) {
+    // QH_NO_PERSIST=1: no persistent step for this context (no placement
+    // probe, no router folds), so no cooperative launch at all
+    const char* np = std::getenv("QH_NO_PERSIST");
+    if (np && np[0] == '1') {
+        c->persist_ok = c->persist = false;
+        return;
+    }
     hipDeviceProp_t p;
     HIP_OK(hipGetDeviceProperties(&p, c->device));
     int per_cu = 0;
     HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(k_decode), 512, 0));
     const uint32_t nwg = (uint32_t)p.multiProcessorCount;
     c->persist_ok = per_cu >= 1 && persist_supported(c, nwg) && xcd_placement_ok(c, nwg);
-    const char* np = std::getenv("QH_NO_PERSIST");
-    c->persist = c->persist_ok && !(np && np[0] == '1');
+    c->persist = c->persist_ok;
     if (!c->persist_ok) return;
     c->nwg = nwg;
     const ModelDims& d = c->dm;
@@ -886,6 +900,37 @@ std::string prefill_gap(const qh_ctx* c) {
         if (L.router.kind != F32) return "router is not F32";
     }
     return "";
+}
+
+// The prefill GEMMs' tile-layout copies of every layer's q, k, v, o, gate,
+// up and down (once per model; the row layout stays for the token step).
+void prefill_tiles(qh_ctx* c) {
+    auto& P = c->pf;
+    if (P.tiled) return;
+    auto mats = [](LayerW& L) { return std::array<DevMat*, 7>{&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down}; };
+    auto bytes = [&](const DevMat& m) {
+        return m.expert_stride ? (size_t)c->dm.experts * m.expert_stride : (size_t)m.rows * m.drb;
+    };
+    size_t total = 0;
+    for (LayerW& L : c->layers)
+        for (DevMat* m : mats(L)) {
+            if (m->rows % 32 || !(m->kind == Q4_K || m->kind == Q6_K)) throw Error("tile layout needs Q4_K/Q6_K rows in groups of 32");
+            total += (bytes(*m) + 255) / 256 * 256;
+        }
+    P.tiles.alloc(total);
+    size_t off = 0;
+    for (LayerW& L : c->layers)
+        for (DevMat* m : mats(L)) {
+            uint8_t* dst = P.tiles.as<uint8_t>() + off;
+            const uint32_t experts = m->expert_stride ? c->dm.experts : 1;
+            const size_t nblk = (size_t)experts * (m->rows / 32) * m->geo.nb;
+            hipLaunchKernelGGL(k_tile_gemm, dim3((uint32_t)std::min<size_t>(nblk, 65535)), dim3(kBlock), 0, c->s, *m,
+                               experts, dst);
+            HIP_OK(hipGetLastError());
+            m->wt = dst;
+            off += (bytes(*m) + 255) / 256 * 256;
+        }
+    P.tiled = true;
 }
 
 // column splits of the prefill router logits (partial sums added in order)
@@ -1635,6 +1680,7 @@ int qh_prefill(qh_ctx* c, const uint32_t* prompt, size_t n, float* logits, size_
             c->stats.matvec_ms += now_ms() - t0;
             return;
         }
+        prefill_tiles(c);
         size_t chunk = kPrefillChunk;
         if (const char* e = std::getenv("QH_PREFILL_CHUNK")) chunk = std::max<long>(1, std::atol(e));
         const uint32_t cap = (uint32_t)std::min<size_t>({n, chunk, kPrefillChunk, c->context});

@@ -19,7 +19,24 @@ struct DevMat {
     uint32_t drb;       // device row stride (bytes)
     RowGeo geo;
     size_t expert_stride;  // bytes between experts (rows * drb); 0 for 2-D
+    // the batched-prefill GEMMs' copy of the same rows in the tile layout
+    // (Q4_K / Q6_K, rows a multiple of 32; built on the first batched
+    // prefill), or null.  Per expert, blocks (row group G of 32 rows,
+    // super-block b) at (G * nb + b) * tile_block_bytes(kind); expert e at
+    // e * expert_stride (the same size as the row layout).
+    const uint8_t* wt;
 };
+
+// Bytes of one tile-layout block: 32 rows x one 256-column super-block.
+//   Q4_K (4,608): headers [row][16]; quants [slice 4][lane 64][16], lane =
+//                 32 g + row holding bytes 32 slice + 16 g .. of the row's
+//                 128 quant bytes.
+//   Q6_K (6,720): low bits [half 2][part 2][lane 64][16] (bytes 64 half +
+//                 32 part + 16 g ..); high bits [half 2][lane 64][16] (bytes
+//                 32 half + 16 g ..); scales [slice 4][row][4]; d [row][2].
+// A wave's load of one field for 32 rows is one contiguous 1-KB run.
+constexpr uint32_t kTileQ4K = 4608, kTileQ6K = 6720;
+QH_HD uint32_t tile_block_bytes(uint32_t kind) { return kind == Q6_K ? kTileQ6K : kTileQ4K; }
 
 // Device-resident step state of one sequence.
 struct DevState {

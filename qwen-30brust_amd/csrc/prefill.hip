@@ -45,6 +45,7 @@ __device__ __forceinline__ h2v int_pair(uint32_t p, _Float16 bias) {
 // broadcast to both halves of a pair.
 struct SplitH {
     h2v hi, lo;
+    SplitH() = default;
     __device__ __forceinline__ explicit SplitH(float v) {
         const _Float16 h = (_Float16)v, l = (_Float16)(v - (float)h);
         hi = h2v{h, h};
@@ -212,6 +213,208 @@ __device__ __forceinline__ void gemm_tile(const _Float16* arow, const uint8_t* c
     }
 }
 
+// ------------------------------------------- GEMM, weights in registers --
+// The expert and dense GEMMs: 128 x 128 output tiles (rows: activations,
+// columns: weight rows), 4 waves; wave w owns weight rows [32w, 32w+32) over
+// all 128 tile rows as 4 row blocks of 32, one v_mfma_f32_32x32x16_f16 per
+// (row block, matrix, k-step).  K runs in 64-column slices (one sub-block
+// pair of a 256-column super-block), four k-steps of 16.
+// Lane l supplies weight row 32w + l%32 and column group g = l/32: in k-step
+// s its 8 B values are the slice columns 32(s/2) + 16g + 8(s%2) + (0..7).
+// The MFMA sums over k, so any assignment of the slice's columns to
+// (k-group, k-step) is exact as long as A uses the same one.  The B values
+// are dequantised from the lane's weight bytes straight into registers (no
+// LDS round trip, no barrier), by the same fp16 arithmetic as WSlice; the
+// activations go through LDS, double-buffered, one barrier per slice.
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+template <uint32_t KIND> struct WReg;
+
+// Four fp16 values fma(byte i of m, a, b), i = 0..3, into v[o .. o+3]: the
+// integer bytes convert exactly to f32 (v_cvt_f32_ubyteN) and each value is
+// rounded to fp16 once.
+__device__ __forceinline__ void bytes_affine(h8v& v, int o, uint32_t m, float a, float b) {
+    v[o] = (_Float16)fmaf((float)(m & 0xffu), a, b);
+    v[o + 1] = (_Float16)fmaf((float)((m >> 8) & 0xffu), a, b);
+    v[o + 2] = (_Float16)fmaf((float)((m >> 16) & 0xffu), a, b);
+    v[o + 3] = (_Float16)fmaf((float)(m >> 24), a, b);
+}
+// w & mk, opaque to the optimiser: knowing the mask, it would narrow each
+// byte extraction to a bit-field one and lose the byte-convert form
+__device__ __forceinline__ uint32_t and_opaque(uint32_t w, uint32_t mk) {
+    uint32_t r;
+    asm("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(w), "s"(mk));
+    return r;
+}
+
+template <> struct WReg<Q4_K> {
+    uint4 q, hdr;
+    // d*sc and -dmin*m of sub-blocks 2sl (low nibbles) and 2sl+1 (high
+    // nibbles, kept in place: their scale is divided by 16, exactly)
+    struct Sc { float a0, b0, a1, b1; };
+    // from tile block blk (32 rows, one super-block): the lane's row header
+    // and quant bytes 32 sl + 16 g .. of its row
+    __device__ __forceinline__ void load(const uint8_t* blk, uint32_t sl, uint32_t lane) {
+        hdr = ld16(blk + (lane & 31) * 16);
+        q = ld16(blk + 512 + sl * 1024 + lane * 16);
+    }
+    __device__ __forceinline__ Sc prep(uint32_t sl, uint32_t) const {
+        uint32_t scp, mp;
+        kscale_pair(hdr.y, hdr.z, hdr.w, sl, scp, mp);
+        const float d = h2f(hdr.x & 0xffffu), dm = h2f(hdr.x >> 16);
+        return {d * (float)(scp & 0xffu), -(dm * (float)(mp & 0xffu)), d * (float)(scp >> 8) * 0.0625f,
+                -(dm * (float)(mp >> 8))};
+    }
+    // k-step S: bytes 8(S%2) .. +7, low nibbles for S < 2, high for S >= 2;
+    // d*sc*q - dmin*m (src/quant.rs:50-62) rounded once to fp16
+    template <int S>
+    __device__ __forceinline__ h8v dequant(const Sc& c, uint32_t) const {
+        const uint32_t w0 = (S & 1) ? q.z : q.x, w1 = (S & 1) ? q.w : q.y;
+        const uint32_t mk = S < 2 ? 0x0f0f0f0fu : 0xf0f0f0f0u;
+        const float a = S < 2 ? c.a0 : c.a1, b = S < 2 ? c.b0 : c.b1;
+        h8v v;
+        bytes_affine(v, 0, and_opaque(w0, mk), a, b);
+        bytes_affine(v, 4, and_opaque(w1, mk), a, b);
+        return v;
+    }
+};
+
+template <> struct WReg<Q6_K> {
+    uint4 l0, l1, qh;
+    uint32_t sc4, d;
+    // d*sc and -32 d*sc of the lane's two scales (sets l0 and l1)
+    struct Sc { float a0, b0, a1, b1; };
+    // slice sl = 2c + p of the super-block (half c, nibble p), from tile
+    // block blk: low-bit bytes 64c + 16g .. and 64c + 32 + 16g .. of the
+    // lane's row (columns 16g.. and 32+16g..), their high-bit bytes
+    // 32c + 16g .., the slice's 4 scales and d
+    __device__ __forceinline__ void load(const uint8_t* blk, uint32_t sl, uint32_t lane) {
+        const uint32_t c = sl >> 1;
+        l0 = ld16(blk + c * 2048 + lane * 16);
+        l1 = ld16(blk + c * 2048 + 1024 + lane * 16);
+        qh = ld16(blk + 4096 + c * 1024 + lane * 16);
+        sc4 = gld<uint32_t>(blk + 6144 + sl * 128 + (lane & 31) * 4);
+        d = ld_u16(blk + 6656 + (lane & 31) * 2);
+    }
+    __device__ __forceinline__ Sc prep(uint32_t, uint32_t grp) const {
+        const float df = h2f(d);
+        const float a0 = df * (float)(int8_t)((sc4 >> (8 * grp)) & 0xffu);
+        const float a1 = df * (float)(int8_t)((sc4 >> (8 * (grp + 2))) & 0xffu);
+        return {a0, -32.f * a0, a1, -32.f * a1};
+    }
+    // k-step S: set S/2 (l0 with scale byte g, or l1 with byte g+2), bytes
+    // 8(S%2) .. +7; d*sc*(q-32) (src/quant.rs:63-77) with q = nibble p | two
+    // high bits << 4, rounded once to fp16
+    template <int S>
+    __device__ __forceinline__ h8v dequant(const Sc& c, uint32_t p) const {
+        const uint4& L = S < 2 ? l0 : l1;
+        const uint32_t x0 = (S & 1) ? L.z : L.x, x1 = (S & 1) ? L.w : L.y;
+        const uint32_t h0 = (S & 1) ? qh.z : qh.x, h1 = (S & 1) ? qh.w : qh.y;
+        const uint32_t hs = 2 * (2 * p + (S < 2 ? 0 : 1)), ls = 4 * p;
+        const uint32_t va = and_opaque(x0 >> ls, 0x0f0f0f0fu) | (and_opaque(h0 >> hs, 0x03030303u) << 4);
+        const uint32_t vb = and_opaque(x1 >> ls, 0x0f0f0f0fu) | (and_opaque(h1 >> hs, 0x03030303u) << 4);
+        const float a = S < 2 ? c.a0 : c.a1, b = S < 2 ? c.b0 : c.b1;
+        h8v v;
+        bytes_affine(v, 0, va, a, b);
+        bytes_affine(v, 4, vb, a, b);
+        return v;
+    }
+};
+
+// Weight row of this thread (tile column): wave w, lane l -> 32w + l%32.
+__device__ __forceinline__ uint32_t rtile_row() { return 32 * (threadIdx.x >> 6) + (threadIdx.x & 31); }
+// Tile row of this thread's A load i (i < 4): 32w + 8i + l/8.
+__device__ __forceinline__ uint32_t arow_row(uint32_t i) {
+    return 32 * (threadIdx.x >> 6) + 8 * i + ((threadIdx.x & 63) >> 3);
+}
+
+// Output element acc[.][mb][i] of this lane: tile row / tile column.
+__device__ __forceinline__ uint32_t racc_row(uint32_t mb, uint32_t i) {
+    return 32 * mb + 8 * (i >> 2) + 4 * ((threadIdx.x & 63) >> 5) + (i & 3);
+}
+__device__ __forceinline__ uint32_t racc_col() { return rtile_row(); }
+
+constexpr int kRA = 2 * kGM * kGL;  // halfs of LDS: the two A buffers
+
+// acc[nb][mb] += A[m0 .. m0+128) x W_nb[n0 .. n0+128)^T over columns
+// [kbeg, kbeg + K) (kbeg a multiple of 256, K of 64 * STAGES; STAGES even).
+// arows[i]: the A row of tile row arow_row(i) (any valid row past the tile's
+// rows: those outputs are not stored); wblk[nb]: tile block (G, 0) of matrix
+// nb for this wave's row group G = (n0 + 32w) / 32 (likewise clamped).  STAGES register stages
+// of weight loads run ahead; the loads are unconditional (clamped), so each
+// wait covers exactly one stage.
+template <uint32_t KIND, int NB, int STAGES>
+__device__ __forceinline__ void gemm_tile_r(const _Float16* const (&arows)[4], const uint8_t* const (&wblk)[NB],
+                                            uint32_t K, f16v (&acc)[NB][4], _Float16* As, uint32_t kbeg = 0) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63, grp = lane >> 5;
+    static_assert(STAGES % 2 == 0, "slice k uses A buffer k % 2 = its stage's parity");
+    const uint32_t nsl = K / kGK;
+    WReg<KIND> wr[STAGES][NB];
+    uint4 av[2][4];  // A slices k+1 and k+2 in flight while slice k is multiplied
+    auto wload = [&](int st, uint32_t k) {
+        const uint32_t k0 = kbeg + min(k, nsl - 1) * kGK;  // past the end: a harmless reload
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) wr[st][nb].load(wblk[nb] + (size_t)(k0 >> 8) * tile_block_bytes(KIND), (k0 >> 6) & 3, lane);
+    };
+    // A row r, 16-byte chunks 2i + grp of the slice (lanes l and l+32 read
+    // adjacent chunks of one row)
+    // A: load i of a wave covers 8 whole 128-byte slice rows, rows
+    // arow_row(i) (lane l: row 32w + 8i + l/8, 16-byte chunk l%8)
+    const uint32_t ach = lane & 7;
+    auto aload = [&](int j, uint32_t k) {
+        const uint32_t k0 = kbeg + min(k, nsl - 1) * kGK;
+#pragma unroll
+        for (int i = 0; i < 4; i++) av[j][i] = gld<uint4>(arows[i] + k0 + 8 * ach);
+    };
+    // A slice held in av[j] to LDS buffer j (slice k sits in buffer k % 2)
+    auto astore = [&](int j) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            *reinterpret_cast<uint4*>(As + j * kGM * kGL + arow_row(i) * kGL + 8 * ach) = av[j][i];
+    };
+#pragma unroll
+    for (int st = 0; st < STAGES; st++) wload(st, st);
+    aload(0, 0);
+    astore(0);
+    aload(1, 1);
+    aload(0, 2);
+    __syncthreads();
+    for (uint32_t k0 = 0; k0 < nsl; k0 += STAGES) {
+#pragma unroll
+        for (int st = 0; st < STAGES; st++) {
+            const uint32_t k = k0 + st;
+            const uint32_t sl = ((kbeg >> 6) + k) & 3, p = sl & 1;
+            const _Float16* Ab = As + (k & 1) * kGM * kGL;
+            typename WReg<KIND>::Sc sc[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) sc[nb] = wr[st][nb].prep(sl, grp);
+            auto kstep = [&](auto S_) {
+                constexpr int S = decltype(S_)::value;
+                const uint32_t col = 32 * (S >> 1) + 16 * grp + 8 * (S & 1);
+                h8v af[4], bf[NB];
+#pragma unroll
+                for (int mb = 0; mb < 4; mb++)
+                    af[mb] = *reinterpret_cast<const h8v*>(Ab + (32 * mb + (lane & 31)) * kGL + col);
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++) bf[nb] = wr[st][nb].template dequant<S>(sc[nb], p);
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+                    for (int mb = 0; mb < 4; mb++)
+                        acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mb], bf[nb], acc[nb][mb], 0, 0, 0);
+            };
+            kstep(std::integral_constant<int, 0>{});
+            kstep(std::integral_constant<int, 1>{});
+            kstep(std::integral_constant<int, 2>{});
+            kstep(std::integral_constant<int, 3>{});
+            wload(st, k + STAGES);
+            astore((st + 1) & 1);  // slice k + 1
+            aload((st + 1) & 1, k + 3);
+            __syncthreads();
+        }
+    }
+}
+
 // XCD-aware tile order.  Workgroup b runs on XCD b % 8 (each XCD has its own
 // L2).  The grid is 1-D: XCD x takes the row tiles t = x, x + 8, ... and, for
 // each in turn, all nn column tiles, so that one row tile's activations (read
@@ -239,74 +442,72 @@ __device__ __forceinline__ uint32_t acc_col(uint32_t nt) {
 template <uint32_t KIND>
 __global__ __launch_bounds__(kGT, 2) void k_gemm_gateup(const _Float16* Xn, uint32_t H, ExpertTiles G, DevMat Wg, DevMat Wu,
                                                      _Float16* Hs) {
-    __shared__ __align__(16) _Float16 smem[3 * kGM * kGL];
+    __shared__ __align__(16) _Float16 smem[kRA];
     uint32_t ty, tx;
     xcd_tile((Wg.rows + kGN - 1) / kGN, ty, tx);
     if (ty >= *G.ntile) return;
     const uint32_t e = G.te[ty], mt0 = G.tm[ty];
     const uint32_t base = G.goff[e], rows = G.goff[e + 1] - base;
-    const uint32_t n0 = tx * kGN, r = threadIdx.x >> 1, ff = Wg.rows;
-    const _Float16* arow = Xn + (size_t)(mt0 + r < rows ? G.tok[base + mt0 + r] : 0u) * H;
-    const uint32_t wr = min(n0 + r, ff - 1);
-    const uint8_t* const wrow[2] = {Wg.w + e * Wg.expert_stride + (size_t)wr * Wg.drb,
-                                    Wu.w + e * Wu.expert_stride + (size_t)wr * Wu.drb};
-    f4v acc[2][4][4];
+    const uint32_t n0 = tx * kGN, r = rtile_row(), ff = Wg.rows;
+    const _Float16* arows[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t ra = mt0 + arow_row(i);
+        arows[i] = Xn + (size_t)(ra < rows ? G.tok[base + ra] : 0u) * H;
+    }
+    const size_t gofs = (size_t)min((n0 >> 5) + (threadIdx.x >> 6), ff / 32 - 1) * Wg.geo.nb * tile_block_bytes(KIND);
+    const uint8_t* const wblk[2] = {Wg.wt + e * Wg.expert_stride + gofs, Wu.wt + e * Wu.expert_stride + gofs};
+    f16v acc[2][4];
 #pragma unroll
     for (int nb = 0; nb < 2; nb++)
 #pragma unroll
-        for (int mt = 0; mt < 4; mt++)
+        for (int mb = 0; mb < 4; mb++) acc[nb][mb] = f16v{};
+    gemm_tile_r<KIND, 2, 2>(arows, wblk, Wg.cols, acc, smem);
+    const uint32_t n = n0 + racc_col();
 #pragma unroll
-            for (int nt = 0; nt < 4; nt++) acc[nb][mt][nt] = f4v{0.f, 0.f, 0.f, 0.f};
-    gemm_tile<KIND, 2>(arow, wrow, Wg.geo, Wg.cols, acc, smem, smem + kGM * kGL);
+    for (int mb = 0; mb < 4; mb++)
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-        for (int nt = 0; nt < 4; nt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t m = mt0 + acc_row(mt, i), n = n0 + acc_col(nt);
-                if (m < rows && n < ff) {
+        for (int i = 0; i < 16; i++) {
+            const uint32_t m = mt0 + racc_row(mb, i);
+            if (m < rows && n < ff) {
 #pragma clang fp contract(off)
-                    const float gv = acc[0][mt][nt][i], uv = acc[1][mt][nt][i];
-                    Hs[(size_t)(base + m) * ff + n] = (_Float16)((gv / (1.f + expf(-gv))) * uv);
-                }
+                const float gv = acc[0][mb][i], uv = acc[1][mb][i];
+                Hs[(size_t)(base + m) * ff + n] = (_Float16)((gv / (1.f + expf(-gv))) * uv);
             }
+        }
 }
 
 // down of the routed experts: Y[asg][n] = Hs[goff[e] + r] . Wd_e[n].
 template <uint32_t KIND>
-__global__ __launch_bounds__(kGT) void k_gemm_down(const _Float16* Hs, ExpertTiles G, DevMat Wd, float* Y) {
-    __shared__ __align__(16) _Float16 smem[2 * kGM * kGL];
+__global__ __launch_bounds__(kGT, 2) void k_gemm_down(const _Float16* Hs, ExpertTiles G, DevMat Wd, float* Y) {
+    __shared__ __align__(16) _Float16 smem[kRA];
+    __shared__ uint32_t dsts[kGM];  // assignment index of each tile row
     uint32_t ty, tx;
     xcd_tile((Wd.rows + kGN - 1) / kGN, ty, tx);
     if (ty >= *G.ntile) return;
     const uint32_t e = G.te[ty], mt0 = G.tm[ty];
     const uint32_t base = G.goff[e], rows = G.goff[e + 1] - base;
-    const uint32_t n0 = tx * kGN, r = threadIdx.x >> 1, ff = Wd.cols, N = Wd.rows;
-    const _Float16* arow = Hs + (size_t)(base + min(mt0 + r, rows - 1)) * ff;
-    const uint8_t* const wrow[1] = {Wd.w + e * Wd.expert_stride + (size_t)min(n0 + r, N - 1) * Wd.drb};
-    // output rows of this lane's accumulators: their assignment indices,
-    // fetched now so the epilogue does not wait on them one by one
-    uint32_t dst[4][4];
+    const uint32_t n0 = tx * kGN, r = rtile_row(), ff = Wd.cols, N = Wd.rows;
+    // visible to the epilogue through the GEMM's barriers
+    if (threadIdx.x < kGM) dsts[threadIdx.x] = G.asg[base + min(mt0 + threadIdx.x, rows - 1)];
+    const _Float16* arows[4];
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
+    for (int i = 0; i < 4; i++) arows[i] = Hs + (size_t)(base + min(mt0 + arow_row(i), rows - 1)) * ff;
+    const uint8_t* const wblk[1] = {
+        Wd.wt + e * Wd.expert_stride +
+        (size_t)min((n0 >> 5) + (threadIdx.x >> 6), N / 32 - 1) * Wd.geo.nb * tile_block_bytes(KIND)};
+    f16v acc[1][4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) dst[mt][i] = G.asg[base + min(mt0 + acc_row(mt, i), rows - 1)];
-    f4v acc[1][4][4];
+    for (int mb = 0; mb < 4; mb++) acc[0][mb] = f16v{};
+    gemm_tile_r<KIND, 1, 2>(arows, wblk, ff, acc, smem);
+    const uint32_t n = n0 + racc_col();
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
+    for (int mb = 0; mb < 4; mb++)
 #pragma unroll
-        for (int nt = 0; nt < 4; nt++) acc[0][mt][nt] = f4v{0.f, 0.f, 0.f, 0.f};
-    gemm_tile<KIND, 1, 2>(arow, wrow, Wd.geo, ff, acc, smem, smem + kGM * kGL);
-#pragma unroll
-    for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-        for (int nt = 0; nt < 4; nt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t m = mt0 + acc_row(mt, i), n = n0 + acc_col(nt);
-                if (m < rows && n < N) Y[(size_t)dst[mt][i] * N + n] = acc[0][mt][nt][i];
-            }
+        for (int i = 0; i < 16; i++) {
+            const uint32_t ml = racc_row(mb, i), m = mt0 + ml;
+            if (m < rows && n < N) Y[(size_t)dsts[ml] * N + n] = acc[0][mb][i];
+        }
 }
 
 // Dense projections (the per-token q/k/v and o matvecs of model.rs:230-232,
@@ -315,35 +516,34 @@ __global__ __launch_bounds__(kGT) void k_gemm_down(const _Float16* Hs, ExpertTil
 // C[m][cofs_i + n] = X16[m] . W_i[n] (columns [kbeg, kbeg + K) of W_i, K =
 // cols / gridDim.z, split z of the columns writing to C + z * split_stride),
 // for m < S, n < W_i.rows.  Column tiles [t_i, t_{i+1}) of gridDim.x belong
-// to matrix i.  Tiles as the expert GEMMs, two register stages of loads ahead
-// of the LDS tile.
+// to matrix i.  Tiles as the expert GEMMs.
 template <uint32_t KIND>
 __device__ __forceinline__ void dense_body(const _Float16* X16, uint32_t S, const DevMat& W, uint32_t m0,
                                            uint32_t n0, uint32_t kbeg, uint32_t K, float* C, uint32_t ldc,
                                            uint32_t cofs, _Float16* smem) {
-    const uint32_t r = threadIdx.x >> 1, N = W.rows, ld = W.cols;
-    const _Float16* arow = X16 + (size_t)min(m0 + r, S - 1) * ld;
-    const uint8_t* const wrow[1] = {W.w + (size_t)min(n0 + r, N - 1) * W.drb};
-    f4v acc[1][4][4];
+    const uint32_t r = rtile_row(), N = W.rows, ld = W.cols;
+    const _Float16* arows[4];
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
+    for (int i = 0; i < 4; i++) arows[i] = X16 + (size_t)min(m0 + arow_row(i), S - 1) * ld;
+    const uint8_t* const wblk[1] = {
+        W.wt + (size_t)min((n0 >> 5) + (threadIdx.x >> 6), N / 32 - 1) * W.geo.nb * tile_block_bytes(KIND)};
+    f16v acc[1][4];
 #pragma unroll
-        for (int nt = 0; nt < 4; nt++) acc[0][mt][nt] = f4v{0.f, 0.f, 0.f, 0.f};
-    gemm_tile<KIND, 1, 2>(arow, wrow, W.geo, K, acc, smem, smem + kGM * kGL, kbeg);
+    for (int mb = 0; mb < 4; mb++) acc[0][mb] = f16v{};
+    gemm_tile_r<KIND, 1, 2>(arows, wblk, K, acc, smem, kbeg);
+    const uint32_t n = n0 + racc_col();
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
+    for (int mb = 0; mb < 4; mb++)
 #pragma unroll
-        for (int nt = 0; nt < 4; nt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t m = m0 + acc_row(mt, i), n = n0 + acc_col(nt);
-                if (m < S && n < N) C[(size_t)m * ldc + cofs + n] = acc[0][mt][nt][i];
-            }
+        for (int i = 0; i < 16; i++) {
+            const uint32_t m = m0 + racc_row(mb, i);
+            if (m < S && n < N) C[(size_t)m * ldc + cofs + n] = acc[0][mb][i];
+        }
 }
 
 __global__ __launch_bounds__(kGT, 2) void k_gemm_dense(const _Float16* X16, uint32_t S, DenseSegs G, float* C,
                                                     uint32_t ldc, size_t split_stride) {
-    __shared__ __align__(16) _Float16 smem[2 * kGM * kGL];
+    __shared__ __align__(16) _Float16 smem[kRA];
     uint32_t mt, t;
     xcd_tile(G.tile_end[2], mt, t);  // row tile (tokens), column tile
     if (mt * kGM >= S) return;
@@ -356,6 +556,57 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_dense(const _Float16* X16, uint
         dense_body<Q4_K>(X16, S, W, mt * kGM, (t - t0) * kGN, kbeg, K, Cz, ldc, G.cofs[i], smem);
     else
         dense_body<Q6_K>(X16, S, W, mt * kGM, (t - t0) * kGN, kbeg, K, Cz, ldc, G.cofs[i], smem);
+}
+
+// ------------------------------------------------------- tile layout --
+// Row-layout source byte of byte o of tile block (G, b) of a matrix whose
+// rows start at w (stride drb): the inverse of the layout described at
+// DevMat::wt.
+__device__ __forceinline__ const uint8_t* tile_src(const uint8_t* w, uint32_t drb, const RowGeo& g, uint32_t kind,
+                                                   uint32_t G, uint32_t b, uint32_t o) {
+    uint32_t row, off;
+    if (kind == Q6_K) {
+        if (o < 4096) {  // low bits
+            const uint32_t c = o >> 11, part = (o >> 10) & 1, lane = (o >> 4) & 63;
+            row = lane & 31;
+            off = g.off_a + b * 128 + c * 64 + part * 32 + (lane >> 5) * 16 + (o & 15);
+        } else if (o < 6144) {  // high bits
+            const uint32_t u = o - 4096, c = u >> 10, lane = (u >> 4) & 63;
+            row = lane & 31;
+            off = g.off_b + b * 64 + c * 32 + (lane >> 5) * 16 + (u & 15);
+        } else if (o < 6656) {  // scales
+            const uint32_t u = o - 6144, sl = u >> 7;
+            row = (u >> 2) & 31;
+            off = g.off_c + b * 16 + sl * 4 + (u & 3);
+        } else {  // d
+            const uint32_t u = o - 6656;
+            row = u >> 1;
+            off = g.off_d + b * 2 + (u & 1);
+        }
+    } else {
+        if (o < 512) {  // headers
+            row = o >> 4;
+            off = g.off_a + b * 16 + (o & 15);
+        } else {  // quants
+            const uint32_t u = o - 512, sl = u >> 10, lane = (u >> 4) & 63;
+            row = lane & 31;
+            off = g.off_b + b * 128 + sl * 32 + (lane >> 5) * 16 + (u & 15);
+        }
+    }
+    return w + (size_t)(32 * G + row) * drb + off;
+}
+
+// The tile copy of matrix m (every expert): workgroup = one block.
+__global__ __launch_bounds__(kBlock) void k_tile_gemm(DevMat m, uint32_t experts, uint8_t* __restrict__ dst) {
+    const uint32_t nb = m.geo.nb, groups = m.rows / 32, bb = tile_block_bytes(m.kind);
+    const size_t nblk = (size_t)experts * groups * nb;
+    for (size_t blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
+        const uint32_t e = (uint32_t)(blk / ((size_t)groups * nb)), rem = (uint32_t)(blk % ((size_t)groups * nb));
+        const uint32_t G = rem / nb, b = rem % nb;
+        const uint8_t* w = m.w + (size_t)e * m.expert_stride;
+        uint8_t* out = dst + (size_t)e * m.expert_stride + ((size_t)G * nb + b) * bb;
+        for (uint32_t o = threadIdx.x; o < bb; o += kBlock) out[o] = *tile_src(w, m.drb, m.geo, m.kind, G, b, o);
+    }
 }
 
 // ------------------------------------------------------ element kernels --
