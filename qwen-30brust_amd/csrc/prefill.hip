@@ -12,12 +12,10 @@
 // grouped gate/up GEMM with SwiGLU; grouped down GEMM; routing-weighted
 // combine + residual in slot order.
 //
-// GEMM: 128 x 128 output tiles, 4 waves (2 x 2) of 64 x 64, K in 64-column
-// slices.  Each slice of the weight rows is dequantised from the device row
-// layout (Q4_K / Q6_K) straight into LDS as fp16 -- 64 columns are one
-// sub-block pair of a 256-element super-block -- and fed to
-// v_mfma_f32_16x16x32_f16 with fp32 accumulation.  The next slice's global
-// loads are issued before the current slice's MFMAs.
+// GEMM: 128 x 128 output tiles, 4 waves, K in 64-column slices, fp16
+// operands on v_mfma_f32_32x32x16_f16 with fp32 accumulation; the weights
+// (Q4_K / Q6_K) are read from a tile-layout copy and dequantised straight into
+// the MFMA's B registers, the activations staged through LDS (gemm_tile_r).
 #include "qh_block.hpp"
 
 namespace qh {
@@ -27,191 +25,6 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 
 constexpr int kGM = 128, kGN = 128, kGK = 64, kGT = 256;
 constexpr int kGL = kGK + 8;  // LDS row pitch in halfs (144 bytes)
-
-// ------------------------------------------------------- weight slices --
-// Thread (row r, half h) of a 64-column slice s (0..3) of super-block b:
-// lo[i] = column 256 b + 64 s + 16 h + i, hi[i] = column 256 b + 64 s + 32 + 16 h + i.
-template <uint32_t KIND> struct WSlice;
-
-// fp16 pairs straight from small integers: v (< 64) in bits 0-7 and 16-23 of
-// p becomes 1024 + v in each half (0x6400 is 1024.0), exact; subtracting the
-// bias (1024 plus the format's offset) leaves the integer, also exact.
-typedef _Float16 h2v __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ h2v int_pair(uint32_t p, _Float16 bias) {
-    const h2v v = __builtin_bit_cast(h2v, p | 0x64006400u);
-    return v - h2v{bias, bias};
-}
-// An f32 value as an fp16 head plus the fp16 rounding of the rest, each
-// broadcast to both halves of a pair.
-struct SplitH {
-    h2v hi, lo;
-    SplitH() = default;
-    __device__ __forceinline__ explicit SplitH(float v) {
-        const _Float16 h = (_Float16)v, l = (_Float16)(v - (float)h);
-        hi = h2v{h, h};
-        lo = h2v{l, l};
-    }
-};
-// q a + b and q a for a pair of exact integers q
-__device__ __forceinline__ uint32_t affine(h2v q, const SplitH& a, const SplitH& b) {
-    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, a.hi, b.hi) + __builtin_elementwise_fma(q, a.lo, b.lo));
-}
-__device__ __forceinline__ uint32_t scale(h2v q, const SplitH& a) {
-    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, a.hi, q * a.lo));
-}
-// bytes i0 and i1 of w into bits 0-7 and 16-23 (v_perm_b32; selector 0x0c = zero byte)
-template <uint32_t SEL>
-__device__ __forceinline__ uint32_t byte_pair(uint32_t w) { return __builtin_amdgcn_perm(0u, w, SEL); }
-constexpr uint32_t kPair01 = 0x0c010c00u, kPair23 = 0x0c030c02u;
-
-template <> struct WSlice<Q4_K> {
-    uint4 q, hdr;
-    __device__ __forceinline__ void load(const uint8_t* row, const RowGeo& g, uint32_t b, uint32_t s, uint32_t h) {
-        hdr = ld16(row + g.off_a + b * 16);
-        q = ld16(row + g.off_b + b * 128 + s * 32 + h * 16);
-    }
-    // d*sc*q - dmin*m (src/quant.rs:50-62), sub-blocks 2s (low nibbles) and
-    // 2s+1, as packed fp16 pairs: lo[i] = columns 2i, 2i+1 of the thread's 16.
-    // q is exact; d*sc and dmin*m (exact in f32) are split into fp16 head and
-    // tail so that no rounding of theirs is shared by the sub-block:
-    // v = fma(q, a_hi, -b_hi) + fma(q, a_lo, -b_lo), two roundings of v.
-    __device__ __forceinline__ void dequant(uint32_t s, uint32_t, uint32_t (&lo)[8], uint32_t (&hi)[8]) const {
-        uint32_t scp, mp;
-        kscale_pair(hdr.y, hdr.z, hdr.w, s, scp, mp);
-        const float d = h2f(hdr.x & 0xffffu), dm = h2f(hdr.x >> 16);
-        const SplitH a0(d * (float)(scp & 0xffu)), b0(-(dm * (float)(mp & 0xffu)));
-        const SplitH a1(d * (float)(scp >> 8)), b1(-(dm * (float)(mp >> 8)));
-        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint32_t p01 = byte_pair<kPair01>(w[k]), p23 = byte_pair<kPair23>(w[k]);
-            lo[2 * k] = affine(int_pair(p01 & 0x000f000fu, 1024), a0, b0);
-            lo[2 * k + 1] = affine(int_pair(p23 & 0x000f000fu, 1024), a0, b0);
-            hi[2 * k] = affine(int_pair((p01 >> 4) & 0x000f000fu, 1024), a1, b1);
-            hi[2 * k + 1] = affine(int_pair((p23 >> 4) & 0x000f000fu, 1024), a1, b1);
-        }
-    }
-};
-
-template <> struct WSlice<Q6_K> {
-    uint4 l0, l1, qh;
-    uint2 sc;
-    uint32_t d;
-    __device__ __forceinline__ void load(const uint8_t* row, const RowGeo& g, uint32_t b, uint32_t s, uint32_t h) {
-        const uint32_t c = s >> 1;
-        l0 = ld16(row + g.off_a + b * 128 + c * 64 + h * 16);
-        l1 = ld16(row + g.off_a + b * 128 + c * 64 + 32 + h * 16);
-        qh = ld16(row + g.off_b + b * 64 + c * 32 + h * 16);
-        sc = gld<uint2>(row + g.off_c + b * 16 + c * 8);
-        d = ld_u16(row + g.off_d + b * 2);
-    }
-    // d*sc*(q-32) (src/quant.rs:63-77): quarters q0 = 2 (s & 1) and q0 + 1 of
-    // chunk s/2, as packed fp16 pairs (6-bit q exact; d*sc as head + tail:
-    // v = fma(q, a_hi, q a_lo), one rounding of v)
-    __device__ __forceinline__ void dequant(uint32_t s, uint32_t h, uint32_t (&lo)[8], uint32_t (&hi)[8]) const {
-        const uint32_t q0 = 2 * (s & 1), sh = (s & 1) * 4;
-        const uint32_t i0 = q0 * 2 + h, i1 = (q0 + 1) * 2 + h;  // scale bytes
-        const uint32_t s0 = i0 < 4 ? sc.x >> (8 * i0) : sc.y >> (8 * (i0 - 4));
-        const uint32_t s1 = i1 < 4 ? sc.x >> (8 * i1) : sc.y >> (8 * (i1 - 4));
-        const float df = h2f(d);
-        const SplitH a0(df * (float)(int8_t)(s0 & 0xffu)), a1(df * (float)(int8_t)(s1 & 0xffu));
-        const uint32_t L0[4] = {l0.x, l0.y, l0.z, l0.w}, L1[4] = {l1.x, l1.y, l1.z, l1.w};
-        const uint32_t QH[4] = {qh.x, qh.y, qh.z, qh.w};
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            // four 6-bit values per word: low nibble | two high bits << 4
-            const uint32_t va = ((L0[k] >> sh) & 0x0f0f0f0fu) | (((QH[k] >> (2 * q0)) & 0x03030303u) << 4);
-            const uint32_t vb = ((L1[k] >> sh) & 0x0f0f0f0fu) | (((QH[k] >> (2 * q0 + 2)) & 0x03030303u) << 4);
-            lo[2 * k] = scale(int_pair(byte_pair<kPair01>(va), 1056), a0);
-            lo[2 * k + 1] = scale(int_pair(byte_pair<kPair23>(va), 1056), a0);
-            hi[2 * k] = scale(int_pair(byte_pair<kPair01>(vb), 1056), a1);
-            hi[2 * k + 1] = scale(int_pair(byte_pair<kPair23>(vb), 1056), a1);
-        }
-    }
-};
-
-// 16 fp16 values (8 packed pairs) to LDS / global, two 16-byte stores
-__device__ __forceinline__ void st_p16(_Float16* dst, const uint32_t (&v)[8]) {
-    *reinterpret_cast<uint4*>(dst) = make_uint4(v[0], v[1], v[2], v[3]);
-    *reinterpret_cast<uint4*>(dst + 8) = make_uint4(v[4], v[5], v[6], v[7]);
-}
-
-// ---------------------------------------------------------------- GEMM --
-// acc[nb][mt][nt] += A[m0 .. m0+128) x W_nb[n0 .. n0+128)^T over columns
-// [kbeg, kbeg + K) (kbeg a multiple of 256).
-// arow: pointer to the fp16 row of tile row r (any valid row when r is past
-// the tile's rows: those outputs are not stored).  wrow[nb]: this thread's
-// weight row (row n0 + tid/2 of matrix nb; likewise any valid row past the
-// matrix).  Wave w owns output rows 64 (w & 1) .., columns 64 (w >> 1) ..
-// STAGES register stages of global loads run ahead of the LDS tile: with 2,
-// the loads of slice k + 2 are in flight while slice k is multiplied.  The
-// loads are unconditional, so each wait covers exactly one stage.
-template <uint32_t KIND, int NB, int STAGES = 1>
-__device__ __forceinline__ void gemm_tile(const _Float16* arow, const uint8_t* const (&wrow)[NB], const RowGeo& g,
-                                          uint32_t K, f4v (&acc)[NB][4][4], _Float16* As, _Float16* Ws,
-                                          uint32_t kbeg = 0) {
-    const uint32_t tid = threadIdx.x, r = tid >> 1, h = tid & 1, lane = tid & 63, w = tid >> 6;
-    const uint32_t wm = w & 1, wn = w >> 1;
-    uint4 av[STAGES][4];
-    WSlice<KIND> ws[STAGES][NB];
-    auto gload = [&](int st, uint32_t k0) {
-        k0 = kbeg + min(k0, K - kGK);  // past the end: a harmless reload of the last slice
-        const uint32_t b = k0 >> 8, s = (k0 >> 6) & 3;
-#pragma unroll
-        for (int i = 0; i < 4; i++) av[st][i] = gld<uint4>(arow + k0 + 32 * h + 8 * i);
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++) ws[st][nb].load(wrow[nb], g, b, s, h);
-    };
-    auto lstore = [&](int st, uint32_t k0) {
-        const uint32_t s = ((kbeg + k0) >> 6) & 3;
-#pragma unroll
-        for (int i = 0; i < 4; i++) *reinterpret_cast<uint4*>(As + r * kGL + 32 * h + 8 * i) = av[st][i];
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++) {
-            uint32_t lo[8], hi[8];
-            ws[st][nb].dequant(s, h, lo, hi);
-            _Float16* dst = Ws + nb * kGN * kGL + r * kGL;
-            st_p16(dst + 16 * h, lo);
-            st_p16(dst + 32 + 16 * h, hi);
-        }
-    };
-    auto mma = [&]() {
-#pragma unroll
-        for (uint32_t ks = 0; ks < 2; ks++) {
-            const uint32_t kc = 32 * ks + 8 * (lane >> 4);
-            h8v af[4];
-#pragma unroll
-            for (int mt = 0; mt < 4; mt++)
-                af[mt] = *reinterpret_cast<const h8v*>(As + (64 * wm + 16 * mt + (lane & 15)) * kGL + kc);
-#pragma unroll
-            for (int nb = 0; nb < NB; nb++) {
-#pragma unroll
-                for (int nt = 0; nt < 4; nt++) {
-                    const h8v bf = *reinterpret_cast<const h8v*>(Ws + nb * kGN * kGL +
-                                                                 (64 * wn + 16 * nt + (lane & 15)) * kGL + kc);
-#pragma unroll
-                    for (int mt = 0; mt < 4; mt++)
-                        acc[nb][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mt], bf, acc[nb][mt][nt], 0, 0, 0);
-                }
-            }
-        }
-    };
-    // K is a multiple of STAGES * 64 (the caller checks), so every stage of
-    // every round runs: straight-line code the compiler can count loads in
-#pragma unroll
-    for (int st = 0; st < STAGES; st++) gload(st, st * kGK);
-    for (uint32_t k0 = 0; k0 < K; k0 += STAGES * kGK) {
-#pragma unroll
-        for (int st = 0; st < STAGES; st++) {
-            const uint32_t kk = k0 + st * kGK;
-            lstore(st, kk);
-            __syncthreads();
-            gload(st, kk + STAGES * kGK);
-            mma();
-            __syncthreads();
-        }
-    }
-}
 
 // ------------------------------------------- GEMM, weights in registers --
 // The expert and dense GEMMs: 128 x 128 output tiles (rows: activations,
@@ -224,8 +37,12 @@ __device__ __forceinline__ void gemm_tile(const _Float16* arow, const uint8_t* c
 // The MFMA sums over k, so any assignment of the slice's columns to
 // (k-group, k-step) is exact as long as A uses the same one.  The B values
 // are dequantised from the lane's weight bytes straight into registers (no
-// LDS round trip, no barrier), by the same fp16 arithmetic as WSlice; the
-// activations go through LDS, double-buffered, one barrier per slice.
+// LDS round trip, no barrier), each value the fp16 rounding of the f32
+// d*sc*q - dmin*m (Q4_K) or d*sc*(q-32) (Q6_K); the weight bytes come from
+// the tile layout (DevMat::wt), where a wave's load of one field for its 32
+// rows is one contiguous 1-KB run.  The activations go through LDS,
+// double-buffered with two slices in flight in registers, one barrier per
+// slice; each A load of a wave covers 8 whole 128-byte slice rows.
 typedef float f16v __attribute__((ext_vector_type(16)));
 
 template <uint32_t KIND> struct WReg;
@@ -425,16 +242,6 @@ __device__ __forceinline__ void xcd_tile(uint32_t nn, uint32_t& t, uint32_t& n) 
     const uint32_t b = blockIdx.x, x = b & 7, i = b >> 3;
     t = x + 8 * (i / nn);
     n = i % nn;
-}
-
-// Output element of acc[.][mt][nt][i] for this lane: tile row / column.
-__device__ __forceinline__ uint32_t acc_row(uint32_t mt, uint32_t i) {
-    const uint32_t lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) & 1;
-    return 64 * wm + 16 * mt + 4 * (lane >> 4) + i;
-}
-__device__ __forceinline__ uint32_t acc_col(uint32_t nt) {
-    const uint32_t lane = threadIdx.x & 63, wn = threadIdx.x >> 7;
-    return 64 * wn + 16 * nt + (lane & 15);
 }
 
 // gate/up of the routed experts + SwiGLU (model.rs:266-274):
