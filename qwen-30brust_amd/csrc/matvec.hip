@@ -328,22 +328,26 @@ bool launch_mv_stream(const DevMat& m, const uint8_t* const* mats, uint32_t nb, 
     }
 }
 
-// Read-only stream: every 16-byte word of p[0, n16) loaded once (eight loads
-// in flight per thread), folded by xor (a word is stored only if the fold hits
-// one fixed value, so the loads cannot be dropped).  Its
-// rate is the device's practical read ceiling beside the matvec timings.
+// Read-only stream: every 16-byte word of p[0, n16) loaded once, folded by
+// xor (a word is stored only if the fold hits one fixed value, so the loads
+// cannot be dropped).  Each workgroup reads one contiguous range (XCD x, which
+// runs workgroups b = x mod 8, covers the x-th eighth), eight 16-byte loads
+// in flight per thread.  Its rate is the device's practical read ceiling
+// beside the matvec timings.
 __global__ __launch_bounds__(kMvT) void k_read_stream(const uint4* __restrict__ p, size_t n16, uint32_t* out) {
-    const size_t stride = (size_t)gridDim.x * kMvT;
+    const uint32_t nwg = gridDim.x, b = blockIdx.x;
+    const uint32_t slot = nwg % 8 == 0 ? (b % 8) * (nwg / 8) + b / 8 : b;
+    const size_t per = (n16 + nwg - 1) / nwg, beg = min((size_t)slot * per, n16), end = min(beg + per, n16);
     uint32_t acc = 0;
-    size_t i = (size_t)blockIdx.x * kMvT + threadIdx.x;
-    for (; i + 7 * stride < n16; i += 8 * stride) {
+    size_t i = beg + threadIdx.x;
+    for (; i + 7 * kMvT < end; i += 8 * kMvT) {
         uint4 v[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = gld<uint4>(p + i + k * stride);
+        for (int k = 0; k < 8; k++) v[k] = gld<uint4>(p + i + k * kMvT);
 #pragma unroll
         for (int k = 0; k < 8; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
     }
-    for (; i < n16; i += stride) {
+    for (; i < end; i += kMvT) {
         const uint4 v = gld<uint4>(p + i);
         acc ^= v.x ^ v.y ^ v.z ^ v.w;
     }
