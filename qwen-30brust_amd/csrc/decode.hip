@@ -737,6 +737,14 @@ __device__ __forceinline__ bool phase_xr1(const DecodeArgs& A, DecodeLds& S, con
     return true;
 }
 
+// The down rows of phase F, requested at the end of phase E by each wave as
+// soon as its own gate/up dots are done (the expert is known and this wave's
+// gate/up rows have arrived): Q6_K chunks, or Q4_K chunks kept in the ql/qh
+// fields (one copy of phase E for both layer kinds).
+struct DownPre {
+    Fmt<Q6_K>::Raw wd[kDownUnits];
+};
+
 // v (64-bit) of lane l of the wave, into scalar registers.
 __device__ __forceinline__ long long readlane64(long long v, uint32_t l) {
     const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(uint64_t)v, l);
@@ -751,7 +759,7 @@ __device__ __forceinline__ long long readlane64(long long v, uint32_t l) {
 // 24j + 3wv + k (k < 3), lane = chunk.
 template <uint32_t KG>
 __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
-                                          uint32_t l) {
+                                          uint32_t l, DownPre& D) {
     const Ctx c = fresh(c0);
     const uint32_t E = c.E, top = c.top, H = c.H;
     const float4 fn = gld<float4>(L.ffn_norm + 4 * c.tid);
@@ -846,6 +854,23 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
             }
         }
     }
+    {
+        // phase F's down rows of the same expert: row 64j + 8wv + lane/8,
+        // chunks lane%8 + 8i (i < 3)
+        const uint8_t* drow = L.down.w + (size_t)ex * L.down.expert_stride +
+                              (size_t)(kRowsWg * c.j + 8 * c.wv + (c.lane >> 3)) * L.down.drb;
+        if (L.down.kind == Q6_K) {
+#pragma unroll
+            for (uint32_t i = 0; i < kDownUnits; i++) D.wd[i] = Fmt<Q6_K>::load(drow, L.down.geo, (c.lane & 7) + 8 * i);
+        } else {
+#pragma unroll
+            for (uint32_t i = 0; i < kDownUnits; i++) {
+                const typename Fmt<Q4_K>::Raw t = Fmt<Q4_K>::load(drow, L.down.geo, (c.lane & 7) + 8 * i);
+                D.wd[i].ql = t.q;
+                D.wd[i].qh = t.h;
+            }
+        }
+    }
     QH_MARK(4, 3);
     __syncthreads();  // S.hv complete; every wave is done with xn, which the next gather overwrites
     if (c.tid < kFfWg)  // one store instruction
@@ -857,16 +882,11 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
 // Rows [64j, 64j+64) of expert rank X's down projection times its routing
 // weight, passed across XCDs.
 template <uint32_t KD>
-__device__ __forceinline__ bool phase_down(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
-                                           uint32_t l) {
+__device__ __forceinline__ bool phase_down(const DecodeArgs& A, DecodeLds& S, const Ctx& c0, uint32_t l,
+                                           const DownPre& D) {
     const Ctx c = fresh(c0);
-    // the down rows, requested before the wait for the SwiGLU outputs: row
-    // 64j + 8wv + lane/8, chunks lane%8 + 8i (i < 3)
-    const uint8_t* drow = L.down.w + (size_t)S.ids[c.X] * L.down.expert_stride +
-                          (size_t)(kRowsWg * c.j + 8 * c.wv + (c.lane >> 3)) * L.down.drb;
-    typename Fmt<KD>::Raw wd[kDownUnits];
-#pragma unroll
-    for (uint32_t i = 0; i < kDownUnits; i++) wd[i] = Fmt<KD>::load(drow, L.down.geo, (c.lane & 7) + 8 * i);
+    // the down rows (row 64j + 8wv + lane/8, chunks lane%8 + 8i, i < 3) were
+    // requested at the end of phase E
     QH_MARK(5, 0);
     float* xs = S.big;
     if (!gather_l(A, S, lbuf(A.lh, kDecodeStrideH, c.X), c.ff, ptag(A, l, 5), xs, c.tid))
@@ -878,7 +898,10 @@ __device__ __forceinline__ bool phase_down(const DecodeArgs& A, DecodeLds& S, co
         const uint32_t chn = (c.lane & 7) + 8 * i;
         float xa[16], xb[16], sa, sb;
         x_runs_p<KD>(xs, 0, chn, xa, xb, sa, sb);
-        acc += Fmt<KD>::dot(wd[i], chn, xa, xb, sa, sb);
+        if constexpr (KD == Q6_K)
+            acc += Fmt<Q6_K>::dot(D.wd[i], chn, xa, xb, sa, sb);
+        else
+            acc += Fmt<Q4_K>::dot({D.wd[i].ql, D.wd[i].qh}, chn, xa, xb, sa, sb);
     }
     acc = seg_sum(acc, 8);
     if ((c.lane & 7) == 0) S.po[8 * c.wv + (c.lane >> 3)] = S.wts[c.X] * acc;  // w * down (model.rs:281-284)
@@ -1130,8 +1153,9 @@ __global__ __launch_bounds__(kDT) void k_decode(DecodeArgs A) {
         if (!ok || !phase_attn(A, S, L, c, l, P)) return;
         if (!phase_oproj<Q4_K>(A, S, L, c, l)) return;
         if (!phase_xr1(A, S, c, l)) return;
-        ok = phase_moe<Q4_K>(A, S, L, c, l);
-        if (ok) QH_DISPATCH_KM(L.down.kind, KD, ok = phase_down<KD>(A, S, L, c, l));
+        DownPre D;
+        ok = phase_moe<Q4_K>(A, S, L, c, l, D);
+        if (ok) QH_DISPATCH_KM(L.down.kind, KD, ok = phase_down<KD>(A, S, c, l, D));
         if (!ok || !phase_xr2(A, S, c, l, l + 1 == A.l1)) return;
     }
     if (A.vocab) QH_DISPATCH_KM(A.out.kind, KV, phase_vocab<KV>(A, S, c));

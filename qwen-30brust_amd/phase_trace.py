@@ -43,7 +43,7 @@ MARKS = [
     ((4, 5), "E  ranks done"),
     ((4, 2), "E  routed"),
     ((4, 3), "E  SwiGLU done"),
-    ((5, 0), "F  down loads issued, wait for h"),
+    ((5, 0), "F  wait for h (down rows requested at the end of E)"),
     ((5, 1), "F  h gathered"),
     ((7, 1), "R  down partials received (cross-XCD)"),
     ((6, 0), "V  vocab loads issued, wait for x''"),
