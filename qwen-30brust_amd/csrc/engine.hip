@@ -934,7 +934,7 @@ void prefill_tiles(qh_ctx* c) {
 }
 
 // column splits of the prefill router logits (partial sums added in order)
-constexpr uint32_t kPfRouterSplit = 4;
+constexpr uint32_t kPfRouterSplit = 8;
 
 void prefill_alloc(qh_ctx* c, uint32_t cap) {
     auto& P = c->pf;
@@ -1027,7 +1027,7 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
     pf_dense(c, {{&L.o, 0u}}, P.O16, S, P.Y, H, 2, ostride);
     hipLaunchKernelGGL(k_pf_norm, dim3(S), dim3(kBlock), 0, c->s, P.X, L.ffn_norm, H, d.eps, P.Xn16, P.Xn32,
                        (const float*)P.Y, ostride);
-    hipLaunchKernelGGL(k_pf_router, dim3((S + 15) / 16, kPfRouterSplit), dim3(kBlock), 0, c->s, P.Xn32, L.router,
+    hipLaunchKernelGGL(k_pf_router, dim3((S + 63) / 64, kPfRouterSplit), dim3(kBlock), 0, c->s, P.Xn32, L.router,
                        S, H, d.experts, P.LR);
     hipLaunchKernelGGL(k_pf_topk, dim3((S + kWaves - 1) / kWaves), dim3(kBlock), 0, c->s, P.LR, kPfRouterSplit, S,
                        d.experts, d.top, P.ids, P.wts, c->acts.st, c->acts.route_log, d.layers, (uint32_t)l, p0);

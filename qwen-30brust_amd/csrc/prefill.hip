@@ -540,72 +540,86 @@ __global__ __launch_bounds__(kBlock) void k_pf_qkrope(const float* QKV, const fl
 }
 
 // Router logits (model.rs:249-256) in fp32 on the matrix cores
-// (v_mfma_f32_16x16x4_f32: fp32 operands and accumulation): 16 tokens per
-// workgroup, wave w takes experts [32 w, 32 w + 32) (E <= 128); 64-column
-// slices of x and of the F32 router rows are staged in LDS, the next slice's
-// loads issued before the current slice's MFMAs.  The columns are split over
-// gridDim.y workgroups (split ks writes its partial sums to LR + ks S E;
-// k_pf_topk adds them in split order): a slice is too little work to cover
-// its load latency, so more workgroups per CU take turns.
+// (v_mfma_f32_16x16x4_f32: fp32 operands and accumulation): 64 tokens per
+// workgroup (the router rows, 1 MB in all, are read once per 64 tokens),
+// wave w takes experts [32 w, 32 w + 32) (E <= 128); 64-column slices of x and
+// of the F32 router rows are staged in LDS, the next slice's loads issued
+// before the current slice's MFMAs.  The columns are split over gridDim.y
+// workgroups (split ks writes its partial sums to LR + ks S E; k_pf_topk adds
+// them in split order), so that the launch fills the device.
+constexpr uint32_t kRT = 64;  // tokens per router workgroup
 __global__ __launch_bounds__(kBlock) void k_pf_router(const float* Xn, DevMat R, uint32_t S, uint32_t H, uint32_t E,
                                                       float* LR) {
     constexpr uint32_t kP = 65;  // LDS pitch (floats)
-    __shared__ float xs[16 * kP];
+    __shared__ float xs[kRT * kP];
     __shared__ float rs[128 * kP];
-    const uint32_t t0 = blockIdx.x * 16, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint32_t t0 = blockIdx.x * kRT, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t grp = lane >> 4, col = lane & 15;
-    float4 xr, rr[8];
+    float4 xr[4], rr[8];
     auto gload = [&](uint32_t k0) {
-        const uint32_t tt = tid >> 4, kk = 4 * (tid & 15);
-        xr = t0 + tt < S ? gld<float4>(Xn + (size_t)(t0 + tt) * H + k0 + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t idx = tid + kBlock * i, tt = idx >> 4, kk = 4 * (idx & 15);
+            xr[i] = t0 + tt < S ? gld<float4>(Xn + (size_t)(t0 + tt) * H + k0 + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
 #pragma unroll
         for (uint32_t i = 0; i < 8; i++) {
             const uint32_t idx = tid + kBlock * i, ee = idx >> 4, k4 = 4 * (idx & 15);
             rr[i] = ee < E ? gld<float4>(R.w + (size_t)ee * R.drb + 4 * (k0 + k4)) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
-    f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
+    f4v acc[kRT / 16][2];
+#pragma unroll
+    for (uint32_t mt = 0; mt < kRT / 16; mt++) acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
     const uint32_t nsl = H / 64, per = (nsl + gridDim.y - 1) / gridDim.y;
     const uint32_t kb = min(blockIdx.y * per, nsl) * 64, ke = min((blockIdx.y + 1) * per, nsl) * 64;
     LR += (size_t)blockIdx.y * S * E;
     if (kb < ke) gload(kb);
     for (uint32_t k0 = kb; k0 < ke; k0 += 64) {
-        {
-            const uint32_t tt = tid >> 4, kk = 4 * (tid & 15);
-            float* xd = xs + tt * kP + kk;
-            xd[0] = xr.x;
-            xd[1] = xr.y;
-            xd[2] = xr.z;
-            xd[3] = xr.w;
 #pragma unroll
-            for (uint32_t i = 0; i < 8; i++) {
-                const uint32_t idx = tid + kBlock * i, ee = idx >> 4, k4 = 4 * (idx & 15);
-                float* rd = rs + ee * kP + k4;
-                rd[0] = rr[i].x;
-                rd[1] = rr[i].y;
-                rd[2] = rr[i].z;
-                rd[3] = rr[i].w;
-            }
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t idx = tid + kBlock * i, tt = idx >> 4, kk = 4 * (idx & 15);
+            float* xd = xs + tt * kP + kk;
+            xd[0] = xr[i].x;
+            xd[1] = xr[i].y;
+            xd[2] = xr[i].z;
+            xd[3] = xr[i].w;
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 8; i++) {
+            const uint32_t idx = tid + kBlock * i, ee = idx >> 4, k4 = 4 * (idx & 15);
+            float* rd = rs + ee * kP + k4;
+            rd[0] = rr[i].x;
+            rd[1] = rr[i].y;
+            rd[2] = rr[i].z;
+            rd[3] = rr[i].w;
         }
         __syncthreads();
         if (k0 + 64 < ke) gload(k0 + 64);
-#pragma unroll 4
+#pragma unroll 2
         for (uint32_t kk = 0; kk < 64; kk += 4) {
-            const float av = xs[col * kP + kk + grp];
+            float bv[2];
 #pragma unroll
-            for (uint32_t nt = 0; nt < 2; nt++)
-                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, rs[(32 * w + 16 * nt + col) * kP + kk + grp],
-                                                               acc[nt], 0, 0, 0);
+            for (uint32_t nt = 0; nt < 2; nt++) bv[nt] = rs[(32 * w + 16 * nt + col) * kP + kk + grp];
+#pragma unroll
+            for (uint32_t mt = 0; mt < kRT / 16; mt++) {
+                const float av = xs[(16 * mt + col) * kP + kk + grp];
+#pragma unroll
+                for (uint32_t nt = 0; nt < 2; nt++)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[nt], acc[mt][nt], 0, 0, 0);
+            }
         }
         __syncthreads();
     }
 #pragma unroll
-    for (uint32_t nt = 0; nt < 2; nt++)
+    for (uint32_t mt = 0; mt < kRT / 16; mt++)
 #pragma unroll
-        for (uint32_t i = 0; i < 4; i++) {
-            const uint32_t t = t0 + 4 * grp + i, e = 32 * w + 16 * nt + col;
-            if (t < S && e < E) LR[(size_t)t * E + e] = acc[nt][i];
-        }
+        for (uint32_t nt = 0; nt < 2; nt++)
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++) {
+                const uint32_t t = t0 + 16 * mt + 4 * grp + i, e = 32 * w + 16 * nt + col;
+                if (t < S && e < E) LR[(size_t)t * E + e] = acc[mt][nt][i];
+            }
 }
 
 // Top-k routing of one token per wave (ops.rs:45-56): the k largest logits
@@ -670,9 +684,21 @@ __global__ __launch_bounds__(1024) void k_pf_group(const uint32_t* ids, uint32_t
                                                    uint32_t* tm, uint32_t* ntile) {
     __shared__ uint32_t cnt[256], cur[256], tb[256];  // E <= 255
     for (uint32_t e = threadIdx.x; e < 256; e += 1024) cnt[e] = 0;
+    // this thread's assignments a = threadIdx.x + 1024 i, all loaded before
+    // any is used (one memory round trip instead of one per assignment)
+    constexpr uint32_t kPer = 16;  // 1024 x 16 = 16,384 = a 2,048-token chunk's top-8 assignments
+    uint32_t myid[kPer];
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; i++) {
+        const uint32_t a = threadIdx.x + 1024 * i;
+        myid[i] = a < n ? ids[a] : 0xffffffffu;
+    }
     __syncthreads();
-    for (uint32_t a = threadIdx.x; a < n; a += 1024)
-        if (ids[a] < E) atomicAdd(&cnt[ids[a]], 1u);  // ids < E unless routing failed (reported)
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; i++)
+        if (myid[i] < E) atomicAdd(&cnt[myid[i]], 1u);  // ids < E unless routing failed (reported)
+    for (uint32_t a = threadIdx.x + 1024 * kPer; a < n; a += 1024)  // chunks beyond 16,384 assignments
+        if (ids[a] < E) atomicAdd(&cnt[ids[a]], 1u);
     __syncthreads();
     if (threadIdx.x < 64) {
         // wave 0: exclusive prefix sums of the counts and of the tile counts,
@@ -713,7 +739,15 @@ __global__ __launch_bounds__(1024) void k_pf_group(const uint32_t* ids, uint32_t
             te[t] = e;
             tm[t] = m;
         }
-    for (uint32_t a = threadIdx.x; a < n; a += 1024) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; i++) {
+        const uint32_t a = threadIdx.x + 1024 * i;
+        if (myid[i] >= E) continue;
+        const uint32_t p = atomicAdd(&cur[myid[i]], 1u);
+        tok[p] = a / top;
+        asg[p] = a;
+    }
+    for (uint32_t a = threadIdx.x + 1024 * kPer; a < n; a += 1024) {
         if (ids[a] >= E) continue;
         const uint32_t p = atomicAdd(&cur[ids[a]], 1u);
         tok[p] = a / top;
