@@ -822,9 +822,9 @@ __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y,
 }
 
 // ----------------------------------------------------------- attention --
-// Causal GQA attention (ops.rs:57-98) of 32 chunk queries -- at positions
-// p0 + q -- for 4 of the G <= 8 query heads of KV head g (wave w: head
-// 4 hf + w, two 16-query tiles), over keys [0, p0 + q], on the fp16 matrix
+// Causal GQA attention (ops.rs:57-98) of 16-query blocks of the chunk -- at
+// positions p0 + q -- for 4 of the G <= 8 query heads of KV head g (wave w:
+// head 4 hf + w), over keys [0, p0 + q], on the fp16 matrix
 // cores with an online softmax in fp32.  Keys come from an fp16 copy of the
 // layer's K ([kvhead][pos][128]) and V, transposed ([kvhead][128][pos], row
 // pitch vp, a multiple of 64), so a
@@ -834,9 +834,10 @@ __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y,
 //                 order inside a 32-key step being the same permutation for
 //                 P and V),
 //   O  += P V    (queries x 128 dims).
-// Query blocks are launched last-first: the causal triangle gives the late
-// blocks the most keys, so they start first and the others fill in.
-constexpr uint32_t kAQ = 32, kAK = 64;
+// Workgroup b takes query blocks nqb-1-b and then b: the causal triangle
+// gives block q about q key blocks, so every workgroup has the same work
+// (about nqb/2 + 1 key blocks per pass pair) and two fit each CU.
+constexpr uint32_t kAQ = 16, kAK = 64;
 constexpr uint32_t kQT = kAQ / 16;  // 16-query tiles per wave
 constexpr uint32_t kKL = 128 + 8, kVL = kAK + 8;  // LDS pitches (halfs)
 
@@ -855,163 +856,168 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
                                                  uint32_t qd, _Float16* O16) {
     __shared__ __align__(16) _Float16 Kl[kAK * kKL];
     __shared__ __align__(16) _Float16 Vt[128 * kVL];
-    const uint32_t nqb = (S + kAQ - 1) / kAQ, q0 = (nqb - 1 - blockIdx.x) * kAQ;
-    const uint32_t g = blockIdx.y >> 1, hf = blockIdx.y & 1;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, grp = lane >> 4, col = lane & 15;
-    const uint32_t hh = 4 * hf + w;  // query head within the group (wave-uniform)
-    const bool hok = hh < G;
-    // scores / sqrt(128) (ops.rs:87), exponentiated base 2
-    const float sc2 = 1.4426950408889634f / sqrtf(128.0f);
-    h8v qf[kQT][4];
+    const uint32_t nqb = (S + kAQ - 1) / kAQ;
+    for (uint32_t pass = 0; pass < 2; pass++) {
+        const uint32_t qb = pass == 0 ? nqb - 1 - blockIdx.x : blockIdx.x;
+        if (pass == 1 && qb >= nqb - 1 - blockIdx.x) break;
+        const uint32_t q0 = qb * kAQ;
+        const uint32_t g = blockIdx.y >> 1, hf = blockIdx.y & 1;
+        const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, grp = lane >> 4, col = lane & 15;
+        const uint32_t hh = 4 * hf + w;  // query head within the group (wave-uniform)
+        const bool hok = hh < G;
+        // scores / sqrt(128) (ops.rs:87), exponentiated base 2
+        const float sc2 = 1.4426950408889634f / sqrtf(128.0f);
+        h8v qf[kQT][4];
 #pragma unroll
-    for (uint32_t qt = 0; qt < kQT; qt++) {
-        const uint32_t q = q0 + 16 * qt + col;
-        const bool ok = hok && q < S;
-        const _Float16* src = Q16 + ((size_t)(g * G + hh) * S + q) * 128 + 8 * grp;
-#pragma unroll
-        for (uint32_t ks = 0; ks < 4; ks++) {
-            if (ok) {
-                qf[qt][ks] = gld<h8v>(src + 32 * ks);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; i++) qf[qt][ks][i] = (_Float16)0.f;
-            }
-        }
-    }
-    // O^T tiles: lane holds dims 16 dt + 4 grp + i of query 16 qt + col, so the
-    // softmax statistics of its query are lane-local
-    f4v o[kQT][8];
-#pragma unroll
-    for (int qt = 0; qt < (int)kQT; qt++)
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++) o[qt][dt] = f4v{0.f, 0.f, 0.f, 0.f};
-    float m[kQT], l[kQT];
-#pragma unroll
-    for (int qt = 0; qt < (int)kQT; qt++) {
-        m[qt] = -INFINITY;
-        l[qt] = 0.f;
-    }
-    const uint32_t kend = p0 + min(q0 + kAQ, S);  // keys [0, kend) can be attended
-    const _Float16* kg = Kh + (size_t)g * ctx * 128;
-    const _Float16* vg = Vth + (size_t)g * 128 * vp;
-    // staging: K thread (key tid/4, 32 dims); V^T thread (dim tid/2, 32 keys)
-    const uint32_t skey = tid >> 2, sd0 = (tid & 3) * 32, sdim = tid >> 1, skk0 = (tid & 1) * 32;
-    uint4 kr[4], vr[4];
-    auto kvload = [&](uint32_t k0) {
-#pragma unroll
-        for (uint32_t i = 0; i < 4; i++)
-            kr[i] = k0 + skey < kend ? gld<uint4>(kg + (size_t)(k0 + skey) * 128 + sd0 + 8 * i) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-        for (uint32_t i = 0; i < 4; i++) {
-            const uint32_t kk = skk0 + 8 * i;
-            if (k0 + kk + 8 <= kend) {
-                vr[i] = gld<uint4>(vg + (size_t)sdim * vp + k0 + kk);
-            } else if (k0 + kk < kend) {  // partial group at the end: element by element
-                h8v t;
-#pragma unroll
-                for (uint32_t j = 0; j < 8; j++)
-                    t[j] = k0 + kk + j < kend ? vg[(size_t)sdim * vp + k0 + kk + j] : (_Float16)0.f;
-                vr[i] = __builtin_bit_cast(uint4, t);
-            } else {
-                vr[i] = make_uint4(0, 0, 0, 0);
-            }
-        }
-    };
-    kvload(0);
-    for (uint32_t k0 = 0; k0 < kend; k0 += kAK) {
-#pragma unroll
-        for (uint32_t i = 0; i < 4; i++) {
-            *reinterpret_cast<uint4*>(Kl + skey * kKL + sd0 + 8 * i) = kr[i];
-            *reinterpret_cast<uint4*>(Vt + sdim * kVL + skk0 + 8 * i) = vr[i];
-        }
-        __syncthreads();
-        if (k0 + kAK < kend) kvload(k0 + kAK);  // next block, during this one
-        if (hok) {  // wave-uniform
-            f4v st[4][kQT];
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-                for (int qt = 0; qt < (int)kQT; qt++) st[kt][qt] = f4v{0.f, 0.f, 0.f, 0.f};
+        for (uint32_t qt = 0; qt < kQT; qt++) {
+            const uint32_t q = q0 + 16 * qt + col;
+            const bool ok = hok && q < S;
+            const _Float16* src = Q16 + ((size_t)(g * G + hh) * S + q) * 128 + 8 * grp;
 #pragma unroll
             for (uint32_t ks = 0; ks < 4; ks++) {
+                if (ok) {
+                    qf[qt][ks] = gld<h8v>(src + 32 * ks);
+                } else {
 #pragma unroll
-                for (uint32_t kt = 0; kt < 4; kt++) {
-                    const h8v af = *reinterpret_cast<const h8v*>(Kl + (16 * kt + col) * kKL + 32 * ks + 8 * grp);
-#pragma unroll
-                    for (uint32_t qt = 0; qt < kQT; qt++)
-                        st[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, qf[qt][ks], st[kt][qt], 0, 0, 0);
-                }
-            }
-            // causal mask, online softmax per query
-#pragma unroll
-            for (uint32_t qt = 0; qt < kQT; qt++) {
-                const uint32_t qpos = p0 + q0 + 16 * qt + col;
-                float mx = -INFINITY;
-#pragma unroll
-                for (uint32_t kt = 0; kt < 4; kt++)
-#pragma unroll
-                    for (uint32_t i = 0; i < 4; i++) {
-                        const uint32_t kpos = k0 + 16 * kt + 4 * grp + i;
-                        const float v = (kpos <= qpos && kpos < kend) ? st[kt][qt][i] * sc2 : -INFINITY;
-                        st[kt][qt][i] = v;
-                        mx = fmaxf(mx, v);
-                    }
-                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                const float mn = fmaxf(m[qt], mx);
-                const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);  // 0 on the first block
-                float ls = 0.f;
-#pragma unroll
-                for (uint32_t kt = 0; kt < 4; kt++)
-#pragma unroll
-                    for (uint32_t i = 0; i < 4; i++) {
-                        const float pv = __builtin_amdgcn_exp2f(st[kt][qt][i] - mn);
-                        st[kt][qt][i] = pv;
-                        ls += pv;
-                    }
-                l[qt] = fmaf(l[qt], alpha, ls);
-                m[qt] = mn;
-#pragma unroll
-                for (uint32_t dt = 0; dt < 8; dt++) o[qt][dt] *= alpha;
-            }
-            // O^T += V^T P^T: A = V^T rows (dims) with keys in the same
-            // permuted order as this lane's probabilities, B = P^T
-#pragma unroll
-            for (uint32_t ks2 = 0; ks2 < 2; ks2++) {
-                h8v pb[kQT];
-#pragma unroll
-                for (uint32_t qt = 0; qt < kQT; qt++)
-#pragma unroll
-                    for (uint32_t i = 0; i < 4; i++) {
-                        pb[qt][i] = (_Float16)st[2 * ks2][qt][i];
-                        pb[qt][4 + i] = (_Float16)st[2 * ks2 + 1][qt][i];
-                    }
-#pragma unroll
-                for (uint32_t dt = 0; dt < 8; dt++) {
-                    const _Float16* vrow = Vt + (16 * dt + col) * kVL + 32 * ks2 + 4 * grp;
-                    const uint2 lo = *reinterpret_cast<const uint2*>(vrow), hi = *reinterpret_cast<const uint2*>(vrow + 16);
-                    const h8v va = __builtin_bit_cast(h8v, make_uint4(lo.x, lo.y, hi.x, hi.y));
-#pragma unroll
-                    for (uint32_t qt = 0; qt < kQT; qt++)
-                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[qt], o[qt][dt], 0, 0, 0);
+                    for (int i = 0; i < 8; i++) qf[qt][ks][i] = (_Float16)0.f;
                 }
             }
         }
-        __syncthreads();
-    }
-    if (!hok) return;
+        // O^T tiles: lane holds dims 16 dt + 4 grp + i of query 16 qt + col, so the
+        // softmax statistics of its query are lane-local
+        f4v o[kQT][8];
 #pragma unroll
-    for (uint32_t qt = 0; qt < kQT; qt++) {
-        float lt = l[qt] + __shfl_xor(l[qt], 16, 64);
-        lt += __shfl_xor(lt, 32, 64);
-        const float inv = 1.0f / lt;
-        const uint32_t q = q0 + 16 * qt + col;
-        if (q < S) {
-            _Float16* dst = O16 + (size_t)q * qd + (g * G + hh) * 128 + 4 * grp;
+        for (int qt = 0; qt < (int)kQT; qt++)
 #pragma unroll
-            for (uint32_t dt = 0; dt < 8; dt++)
-                *reinterpret_cast<uint2*>(dst + 16 * dt) =
-                    pack4h(o[qt][dt][0] * inv, o[qt][dt][1] * inv, o[qt][dt][2] * inv, o[qt][dt][3] * inv);
+            for (int dt = 0; dt < 8; dt++) o[qt][dt] = f4v{0.f, 0.f, 0.f, 0.f};
+        float m[kQT], l[kQT];
+#pragma unroll
+        for (int qt = 0; qt < (int)kQT; qt++) {
+            m[qt] = -INFINITY;
+            l[qt] = 0.f;
+        }
+        const uint32_t kend = p0 + min(q0 + kAQ, S);  // keys [0, kend) can be attended
+        const _Float16* kg = Kh + (size_t)g * ctx * 128;
+        const _Float16* vg = Vth + (size_t)g * 128 * vp;
+        // staging: K thread (key tid/4, 32 dims); V^T thread (dim tid/2, 32 keys)
+        const uint32_t skey = tid >> 2, sd0 = (tid & 3) * 32, sdim = tid >> 1, skk0 = (tid & 1) * 32;
+        uint4 kr[4], vr[4];
+        auto kvload = [&](uint32_t k0) {
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++)
+                kr[i] = k0 + skey < kend ? gld<uint4>(kg + (size_t)(k0 + skey) * 128 + sd0 + 8 * i) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++) {
+                const uint32_t kk = skk0 + 8 * i;
+                if (k0 + kk + 8 <= kend) {
+                    vr[i] = gld<uint4>(vg + (size_t)sdim * vp + k0 + kk);
+                } else if (k0 + kk < kend) {  // partial group at the end: element by element
+                    h8v t;
+#pragma unroll
+                    for (uint32_t j = 0; j < 8; j++)
+                        t[j] = k0 + kk + j < kend ? vg[(size_t)sdim * vp + k0 + kk + j] : (_Float16)0.f;
+                    vr[i] = __builtin_bit_cast(uint4, t);
+                } else {
+                    vr[i] = make_uint4(0, 0, 0, 0);
+                }
+            }
+        };
+        kvload(0);
+        for (uint32_t k0 = 0; k0 < kend; k0 += kAK) {
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++) {
+                *reinterpret_cast<uint4*>(Kl + skey * kKL + sd0 + 8 * i) = kr[i];
+                *reinterpret_cast<uint4*>(Vt + sdim * kVL + skk0 + 8 * i) = vr[i];
+            }
+            __syncthreads();
+            if (k0 + kAK < kend) kvload(k0 + kAK);  // next block, during this one
+            if (hok) {  // wave-uniform
+                f4v st[4][kQT];
+#pragma unroll
+                for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                    for (int qt = 0; qt < (int)kQT; qt++) st[kt][qt] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (uint32_t ks = 0; ks < 4; ks++) {
+#pragma unroll
+                    for (uint32_t kt = 0; kt < 4; kt++) {
+                        const h8v af = *reinterpret_cast<const h8v*>(Kl + (16 * kt + col) * kKL + 32 * ks + 8 * grp);
+#pragma unroll
+                        for (uint32_t qt = 0; qt < kQT; qt++)
+                            st[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, qf[qt][ks], st[kt][qt], 0, 0, 0);
+                    }
+                }
+                // causal mask, online softmax per query
+#pragma unroll
+                for (uint32_t qt = 0; qt < kQT; qt++) {
+                    const uint32_t qpos = p0 + q0 + 16 * qt + col;
+                    float mx = -INFINITY;
+#pragma unroll
+                    for (uint32_t kt = 0; kt < 4; kt++)
+#pragma unroll
+                        for (uint32_t i = 0; i < 4; i++) {
+                            const uint32_t kpos = k0 + 16 * kt + 4 * grp + i;
+                            const float v = (kpos <= qpos && kpos < kend) ? st[kt][qt][i] * sc2 : -INFINITY;
+                            st[kt][qt][i] = v;
+                            mx = fmaxf(mx, v);
+                        }
+                    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                    const float mn = fmaxf(m[qt], mx);
+                    const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);  // 0 on the first block
+                    float ls = 0.f;
+#pragma unroll
+                    for (uint32_t kt = 0; kt < 4; kt++)
+#pragma unroll
+                        for (uint32_t i = 0; i < 4; i++) {
+                            const float pv = __builtin_amdgcn_exp2f(st[kt][qt][i] - mn);
+                            st[kt][qt][i] = pv;
+                            ls += pv;
+                        }
+                    l[qt] = fmaf(l[qt], alpha, ls);
+                    m[qt] = mn;
+#pragma unroll
+                    for (uint32_t dt = 0; dt < 8; dt++) o[qt][dt] *= alpha;
+                }
+                // O^T += V^T P^T: A = V^T rows (dims) with keys in the same
+                // permuted order as this lane's probabilities, B = P^T
+#pragma unroll
+                for (uint32_t ks2 = 0; ks2 < 2; ks2++) {
+                    h8v pb[kQT];
+#pragma unroll
+                    for (uint32_t qt = 0; qt < kQT; qt++)
+#pragma unroll
+                        for (uint32_t i = 0; i < 4; i++) {
+                            pb[qt][i] = (_Float16)st[2 * ks2][qt][i];
+                            pb[qt][4 + i] = (_Float16)st[2 * ks2 + 1][qt][i];
+                        }
+#pragma unroll
+                    for (uint32_t dt = 0; dt < 8; dt++) {
+                        const _Float16* vrow = Vt + (16 * dt + col) * kVL + 32 * ks2 + 4 * grp;
+                        const uint2 lo = *reinterpret_cast<const uint2*>(vrow), hi = *reinterpret_cast<const uint2*>(vrow + 16);
+                        const h8v va = __builtin_bit_cast(h8v, make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+                        for (uint32_t qt = 0; qt < kQT; qt++)
+                            o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[qt], o[qt][dt], 0, 0, 0);
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        if (hok)
+#pragma unroll
+        for (uint32_t qt = 0; qt < kQT; qt++) {
+            float lt = l[qt] + __shfl_xor(l[qt], 16, 64);
+            lt += __shfl_xor(lt, 32, 64);
+            const float inv = 1.0f / lt;
+            const uint32_t q = q0 + 16 * qt + col;
+            if (q < S) {
+                _Float16* dst = O16 + (size_t)q * qd + (g * G + hh) * 128 + 4 * grp;
+#pragma unroll
+                for (uint32_t dt = 0; dt < 8; dt++)
+                    *reinterpret_cast<uint2*>(dst + 16 * dt) =
+                        pack4h(o[qt][dt][0] * inv, o[qt][dt][1] * inv, o[qt][dt][2] * inv, o[qt][dt][3] * inv);
+            }
         }
     }
 }
