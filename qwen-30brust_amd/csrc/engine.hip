@@ -893,6 +893,9 @@ std::string prefill_gap(const qh_ctx* c) {
     if (d.heads % d.kvheads || d.heads / d.kvheads > 8) return "more than 8 query heads per KV head";
     if (d.experts > 128) return "more than 128 experts";
     if (d.hidden % 64 || d.ff % 64) return "hidden or expert width not a multiple of 64";
+    // the o-projection runs as two column halves, each whole 256-column
+    // super-blocks (and an even number of 64-column GEMM slices)
+    if ((d.heads * 128) % 512) return "query width not a multiple of 512";
     for (const LayerW& L : c->layers) {
         if (!(km(L.q.kind) && km(L.k.kind) && km(L.v.kind) && km(L.o.kind) && km(L.gate.kind) &&
               L.up.kind == L.gate.kind && km(L.down.kind)))

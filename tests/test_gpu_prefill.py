@@ -149,3 +149,20 @@ def test_prefill_uncovered_model_runs_the_exact_step(dev):
         ref_lg = ref.forward(int(t))
     assert np.array_equal(lg, ref_lg)
     assert np.array_equal(nxt, ref.forward(int(np.argmax(ref_lg))))
+
+
+def test_prefill_odd_query_width_runs_the_exact_step(dev):
+    """Two query heads (query width 256): the o-projection's two column halves
+    would not be whole super-blocks, so the batched path leaves the model to
+    the exact token step (bit-equal to a stepwise forward) instead of failing."""
+    spec = synth.Spec(256, 1, 2, 1, 128, 8, 2, 256, 256, 64, types=synth._k_types(), seed=5)
+    img = synth.build_image(spec)
+    prompt = np.random.default_rng(3).integers(0, spec.vocab, 9).astype(np.uint32)
+    m = engine.Model(img, spec.context, device=dev)
+    am, lg = m.prefill(prompt)
+    assert m.position == 9
+    ref = engine.Model(img, spec.context, device=dev)
+    for t in prompt:
+        ref_lg = ref.forward(int(t))
+    assert np.array_equal(lg, ref_lg)
+    assert am == int(np.argmax(ref_lg))
