@@ -37,8 +37,8 @@ constexpr int kGL = kGK + 8;  // LDS row pitch in halfs (144 bytes)
 // The MFMA sums over k, so any assignment of the slice's columns to
 // (k-group, k-step) is exact as long as A uses the same one.  The B values
 // are dequantised from the lane's weight bytes straight into registers (no
-// LDS round trip, no barrier), each value the fp16 rounding of the f32
-// d*sc*q - dmin*m (Q4_K) or d*sc*(q-32) (Q6_K); the weight bytes come from
+// LDS round trip, no barrier), each value the f32 d*sc*q - dmin*m (Q4_K) or
+// d*sc*(q-32) (Q6_K) of one FMA, converted to fp16; the weight bytes come from
 // the tile layout (DevMat::wt), where a wave's load of one field for its 32
 // rows is one contiguous 1-KB run.  The activations go through LDS,
 // double-buffered with two slices in flight in registers, one barrier per
@@ -48,8 +48,8 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 template <uint32_t KIND> struct WReg;
 
 // Four fp16 values fma(byte i of m, a, b), i = 0..3, into v[o .. o+3]: the
-// integer bytes convert exactly to f32 (v_cvt_f32_ubyteN) and each value is
-// rounded to fp16 once.
+// integer bytes convert exactly to f32 (v_cvt_f32_ubyteN), one f32 FMA, then
+// the conversion to fp16.
 __device__ __forceinline__ void bytes_affine(h8v& v, int o, uint32_t m, float a, float b) {
     v[o] = (_Float16)fmaf((float)(m & 0xffu), a, b);
     v[o + 1] = (_Float16)fmaf((float)((m >> 8) & 0xffu), a, b);
