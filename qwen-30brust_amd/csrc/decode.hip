@@ -54,10 +54,13 @@
 // (X, j) only after it has read the other phase's slice j from every
 // workgroup (X', j), which those wrote after reading the layer-l contents.
 //
-// Each phase body is instantiated for the formats of the Q4_K_M mix (q, k,
-// o, gate, up: Q4_K; v, down, vocab: Q4_K or Q6_K) and selected once per
-// phase.  The host launches this path only for models and shapes it covers
-// (engine.hip: persist_supported); everything else runs the per-phase kernels.
+// The kernel is instantiated per main format KM (Q4_0, Q8_0, Q4_K, Q5_K or
+// Q6_K: the format of q, k, o, gate and up, as llama.cpp's mixes keep them);
+// v and down are KM or Q6_K per layer (the "more bits" layers of the K-quant
+// mixes), held in one register block so that one copy of each phase serves
+// both; the vocab projection may be any of the five.  The host launches this
+// path only for models and shapes it covers (engine.hip: persist_supported);
+// everything else runs the per-phase kernels.
 #include "qh_block.hpp"
 #include "qh_tile.hpp"
 
@@ -90,13 +93,62 @@ constexpr int kAuxG = 17;                   // sc0 sc1: past every cache
 
 static_assert(kQkvWg == 24 && kQkvWg % kDW == 0, "three q|k|v rows per wave");
 
-// Formats of the Q4_K_M mix; the host routes other models to the per-phase
-// kernels.
-#define QH_DISPATCH_KM(kind, K, ...)                                            \
+// A layer's v or down format: KM, or Q6_K (the host checks it is one of them).
+#define QH_DISPATCH_KM(kind, KM, K, ...)                                      \
+    if ((kind) == ::qh::Q6_K) {                                               \
+        constexpr uint32_t K = ::qh::Q6_K;                                    \
+        __VA_ARGS__;                                                          \
+    } else {                                                                  \
+        constexpr uint32_t K = KM;                                            \
+        __VA_ARGS__;                                                          \
+    }
+// The vocab projection's format: any block-quantised one.
+#define QH_DISPATCH_BLOCK(kind, K, ...)                                         \
     switch (kind) {                                                             \
+    case ::qh::Q4_0: { constexpr uint32_t K = ::qh::Q4_0; __VA_ARGS__; } break; \
+    case ::qh::Q8_0: { constexpr uint32_t K = ::qh::Q8_0; __VA_ARGS__; } break; \
     case ::qh::Q4_K: { constexpr uint32_t K = ::qh::Q4_K; __VA_ARGS__; } break; \
+    case ::qh::Q5_K: { constexpr uint32_t K = ::qh::Q5_K; __VA_ARGS__; } break; \
     default: { constexpr uint32_t K = ::qh::Q6_K; __VA_ARGS__; } break;         \
     }
+
+// One chunk of format KM or of Q6_K in one block of registers (v and down
+// rows), so that one copy of a phase serves both layer kinds.  Every put
+// writes all three words whole: the two branches then store the same fields
+// and the compiler keeps the box in registers (a byte copy, or stores of
+// different extents, would place it in scratch memory).
+template <uint32_t KM> struct ChunkBox {
+    uint4 v[3];
+    template <uint32_t K> __device__ __forceinline__ void put(const typename Fmt<K>::Raw& r) {
+        static_assert(K == KM || K == Q6_K, "the box holds KM or Q6_K");
+        if constexpr (K == Q4_K) {
+            v[0] = r.q, v[1] = r.h, v[2] = make_uint4(0u, 0u, 0u, 0u);
+        } else if constexpr (K == Q5_K) {
+            v[0] = r.q, v[1] = r.h, v[2] = r.qh;
+        } else if constexpr (K == Q6_K) {
+            v[0] = r.ql, v[1] = r.qh, v[2] = make_uint4(r.s8.x, r.s8.y, r.d, 0u);
+        } else if constexpr (K == Q4_0) {
+            v[0] = r.q, v[1] = make_uint4(r.d, 0u, 0u, 0u), v[2] = make_uint4(0u, 0u, 0u, 0u);
+        } else {
+            static_assert(K == Q8_0, "block formats only");
+            v[0] = r.a, v[1] = r.b, v[2] = make_uint4(r.d, 0u, 0u, 0u);
+        }
+    }
+    template <uint32_t K> __device__ __forceinline__ typename Fmt<K>::Raw get() const {
+        static_assert(K == KM || K == Q6_K, "the box holds KM or Q6_K");
+        if constexpr (K == Q4_K) {
+            return {v[0], v[1]};
+        } else if constexpr (K == Q5_K) {
+            return {v[0], v[1], v[2]};
+        } else if constexpr (K == Q6_K) {
+            return {v[0], v[1], make_uint2(v[2].x, v[2].y), v[2].z};
+        } else if constexpr (K == Q4_0) {
+            return {v[0], v[1].x};
+        } else {
+            return {v[0], v[1], v[2].x};
+        }
+    }
+};
 
 struct DecodeLds {
     float big[kDSmem];        // phase scratch (x, attention tiles, h, reductions)
@@ -349,11 +401,11 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
                                           uint32_t l, AttnPre& P) {
     const Ctx c = fresh(c0);
     const uint32_t g = c.X / 2;
-    // v rows are Q6_K or Q4_K (a Q4_K chunk kept in the ql/qh fields): one
-    // copy of the phase for both layer kinds keeps the step's code small
+    // v rows are Q6_K or KQ (one register block either way): one copy of
+    // the phase for both layer kinds keeps the step's code small
     const bool v6 = L.v.kind == Q6_K;
     typename Fmt<KQ>::Raw wq[3];
-    typename Fmt<Q6_K>::Raw wvv[3];
+    ChunkBox<KQ> wvv[3];
 #pragma unroll
     for (uint32_t k = 0; k < 3; k++) {
         const uint32_t r = kQkvWg * c.j + c.wv + kDW * k;  // wave-uniform, < 768
@@ -363,13 +415,10 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
             wq[k] = Fmt<KQ>::load(L.k.w + (size_t)(128 * g + r - 512) * L.k.drb, L.k.geo, c.lane);
         } else {
             const uint8_t* vrow = L.v.w + (size_t)(128 * g + r - 640) * L.v.drb;
-            if (v6) {
-                wvv[k] = Fmt<Q6_K>::load(vrow, L.v.geo, c.lane);
-            } else {
-                const typename Fmt<Q4_K>::Raw t = Fmt<Q4_K>::load(vrow, L.v.geo, c.lane);
-                wvv[k].ql = t.q;
-                wvv[k].qh = t.h;
-            }
+            if (v6)
+                wvv[k].template put<Q6_K>(Fmt<Q6_K>::load(vrow, L.v.geo, c.lane));
+            else
+                wvv[k].template put<KQ>(Fmt<KQ>::load(vrow, L.v.geo, c.lane));
         }
     }
     const float4 nw = gld<float4>(L.attn_norm + 4 * c.tid);
@@ -428,10 +477,9 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
         } else if (v6) {
             float ya[16], yb[16], ta, tb;
             x_runs_p<Q6_K>(xs, 0, c.lane, ya, yb, ta, tb);
-            acc = Fmt<Q6_K>::dot(wvv[k], c.lane, ya, yb, ta, tb);
+            acc = Fmt<Q6_K>::dot(wvv[k].template get<Q6_K>(), c.lane, ya, yb, ta, tb);
         } else {
-            static_assert(KQ == Q4_K, "Q4_K v rows reuse the q|k rows' x runs");
-            acc = Fmt<Q4_K>::dot({wvv[k].ql, wvv[k].qh}, c.lane, xa, xb, sa, sb);
+            acc = Fmt<KQ>::dot(wvv[k].template get<KQ>(), c.lane, xa, xb, sa, sb);  // the q|k rows' x runs
         }
         acc = wave_sum(acc);
         if (c.lane == 0) S.hv[c.wv + kDW * k] = acc;
@@ -739,10 +787,10 @@ __device__ __forceinline__ bool phase_xr1(const DecodeArgs& A, DecodeLds& S, con
 
 // The down rows of phase F, requested at the end of phase E by each wave as
 // soon as its own gate/up dots are done (the expert is known and this wave's
-// gate/up rows have arrived): Q6_K chunks, or Q4_K chunks kept in the ql/qh
-// fields (one copy of phase E for both layer kinds).
-struct DownPre {
-    Fmt<Q6_K>::Raw wd[kDownUnits];
+// gate/up rows have arrived): KM or Q6_K chunks (one copy of phase E for both
+// layer kinds).
+template <uint32_t KM> struct DownPre {
+    ChunkBox<KM> wd[kDownUnits];
 };
 
 // v (64-bit) of lane l of the wave, into scalar registers.
@@ -759,7 +807,7 @@ __device__ __forceinline__ long long readlane64(long long v, uint32_t l) {
 // 24j + 3wv + k (k < 3), lane = chunk.
 template <uint32_t KG>
 __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
-                                          uint32_t l, DownPre& D) {
+                                          uint32_t l, DownPre<KG>& D) {
     const Ctx c = fresh(c0);
     const uint32_t E = c.E, top = c.top, H = c.H;
     const float4 fn = gld<float4>(L.ffn_norm + 4 * c.tid);
@@ -861,14 +909,12 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
                               (size_t)(kRowsWg * c.j + 8 * c.wv + (c.lane >> 3)) * L.down.drb;
         if (L.down.kind == Q6_K) {
 #pragma unroll
-            for (uint32_t i = 0; i < kDownUnits; i++) D.wd[i] = Fmt<Q6_K>::load(drow, L.down.geo, (c.lane & 7) + 8 * i);
+            for (uint32_t i = 0; i < kDownUnits; i++)
+                D.wd[i].template put<Q6_K>(Fmt<Q6_K>::load(drow, L.down.geo, (c.lane & 7) + 8 * i));
         } else {
 #pragma unroll
-            for (uint32_t i = 0; i < kDownUnits; i++) {
-                const typename Fmt<Q4_K>::Raw t = Fmt<Q4_K>::load(drow, L.down.geo, (c.lane & 7) + 8 * i);
-                D.wd[i].ql = t.q;
-                D.wd[i].qh = t.h;
-            }
+            for (uint32_t i = 0; i < kDownUnits; i++)
+                D.wd[i].template put<KG>(Fmt<KG>::load(drow, L.down.geo, (c.lane & 7) + 8 * i));
         }
     }
     QH_MARK(4, 3);
@@ -881,9 +927,9 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
 // ========================================================= F: down projection ==
 // Rows [64j, 64j+64) of expert rank X's down projection times its routing
 // weight, passed across XCDs.
-template <uint32_t KD>
+template <uint32_t KD, uint32_t KM>
 __device__ __forceinline__ bool phase_down(const DecodeArgs& A, DecodeLds& S, const Ctx& c0, uint32_t l,
-                                           const DownPre& D) {
+                                           const DownPre<KM>& D) {
     const Ctx c = fresh(c0);
     // the down rows (row 64j + 8wv + lane/8, chunks lane%8 + 8i, i < 3) were
     // requested at the end of phase E
@@ -898,10 +944,7 @@ __device__ __forceinline__ bool phase_down(const DecodeArgs& A, DecodeLds& S, co
         const uint32_t chn = (c.lane & 7) + 8 * i;
         float xa[16], xb[16], sa, sb;
         x_runs_p<KD>(xs, 0, chn, xa, xb, sa, sb);
-        if constexpr (KD == Q6_K)
-            acc += Fmt<Q6_K>::dot(D.wd[i], chn, xa, xb, sa, sb);
-        else
-            acc += Fmt<Q4_K>::dot({D.wd[i].ql, D.wd[i].qh}, chn, xa, xb, sa, sb);
+        acc += Fmt<KD>::dot(D.wd[i].template get<KD>(), chn, xa, xb, sa, sb);
     }
     acc = seg_sum(acc, 8);
     if ((c.lane & 7) == 0) S.po[8 * c.wv + (c.lane >> 3)] = S.wts[c.X] * acc;  // w * down (model.rs:281-284)
@@ -1092,6 +1135,7 @@ __global__ __launch_bounds__(kDT) void k_xcd_map(uint32_t* out) {
     if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
 }
 
+template <uint32_t KM>
 __global__ __launch_bounds__(kDT) void k_decode(DecodeArgs A) {
     __shared__ __align__(16) DecodeLds S;
     Ctx c;
@@ -1149,16 +1193,22 @@ __global__ __launch_bounds__(kDT) void k_decode(DecodeArgs A) {
         const LayerW& L = *(const LayerW*)((const __attribute__((address_space(4))) LayerW*)A.layers + l);
         bool ok = true;
         AttnPre P;
-        ok = phase_qkv<Q4_K>(A, S, L, c, l, P);
+        ok = phase_qkv<KM>(A, S, L, c, l, P);
         if (!ok || !phase_attn(A, S, L, c, l, P)) return;
-        if (!phase_oproj<Q4_K>(A, S, L, c, l)) return;
+        if (!phase_oproj<KM>(A, S, L, c, l)) return;
         if (!phase_xr1(A, S, c, l)) return;
-        DownPre D;
-        ok = phase_moe<Q4_K>(A, S, L, c, l, D);
-        if (ok) QH_DISPATCH_KM(L.down.kind, KD, ok = phase_down<KD>(A, S, c, l, D));
+        DownPre<KM> D;
+        ok = phase_moe<KM>(A, S, L, c, l, D);
+        if (ok) QH_DISPATCH_KM(L.down.kind, KM, KD, ok = (phase_down<KD, KM>(A, S, c, l, D)));
         if (!ok || !phase_xr2(A, S, c, l, l + 1 == A.l1)) return;
     }
-    if (A.vocab) QH_DISPATCH_KM(A.out.kind, KV, phase_vocab<KV>(A, S, c));
+    if (A.vocab) QH_DISPATCH_BLOCK(A.out.kind, KV, phase_vocab<KV>(A, S, c));
 }
+
+template __global__ void k_decode<Q4_0>(DecodeArgs);
+template __global__ void k_decode<Q8_0>(DecodeArgs);
+template __global__ void k_decode<Q4_K>(DecodeArgs);
+template __global__ void k_decode<Q5_K>(DecodeArgs);
+template __global__ void k_decode<Q6_K>(DecodeArgs);
 
 }  // namespace qh

@@ -45,7 +45,7 @@ template <int C> __global__ void k_down(LayerW, Acts, ModelDims);
 template <int C> __global__ void k_vocab(DevMat, const float*, Acts, ModelDims);
 __global__ void k_finish(Acts, ModelDims, uint32_t);
 // Persistent token step (decode.hip).
-__global__ void k_decode(DecodeArgs);
+template <uint32_t KM> __global__ void k_decode(DecodeArgs);
 __global__ void k_xcd_map(uint32_t*);
 // Streaming quantised matvec (matvec.hip).
 bool launch_mv_stream(const DevMat&, const uint8_t* const*, uint32_t, const float*, float*, uint32_t, hipStream_t);
@@ -223,6 +223,7 @@ struct qh_ctx {
     bool persist_ok = false;  // the model's formats and shapes are covered
     bool persist = false;     // and it is enabled (qh_set_persistent(0) disables it; QH_NO_PERSIST=1 at load leaves it out)
     uint32_t nwg = 0;         // workgroups of k_decode (one per CU)
+    const void* decode_fn = nullptr;  // k_decode<KM> for the model's main format KM
     uint32_t flag_base = 0;   // tag of the last phase launched
     DevBuf layers_dev, sync_buf;  // sync_buf: abort flag and tagged exchange words
     DevBuf rfold;                 // router folds of every layer ([layers][experts][heads*d])
@@ -552,23 +553,39 @@ void capture_graph(qh_ctx* c) {
 }
 
 // Whether k_decode covers this model: the Qwen3-30B-A3B shapes (hidden
-// 2048, 32 query / 4 KV heads of 128, 128 experts, top 8, expert FFN 768),
-// the Q4_K_M formats (q/k/o/gate/up Q4_K; v/down/vocab Q4_K or Q6_K; F32
-// router), and a device of 8 XCDs x 32 CUs running one 512-thread workgroup
-// per CU.
+// 2048, 32 query / 4 KV heads of 128, up to 128 experts, top 8, expert FFN
+// 768), one main block format KM (Q4_0, Q8_0, Q4_K, Q5_K or Q6_K) for q, k,
+// o, gate and up with v and down in KM or Q6_K (llama.cpp's Q4_0, Q8_0,
+// Q4_K_S/M, Q5_K_S/M and Q6_K files), a block-quantised vocab projection and
+// an F32 router, and a device of 8 XCDs x 32 CUs running one 512-thread
+// workgroup per CU.
 bool persist_supported(const qh_ctx* c, uint32_t nwg) {
     const ModelDims& d = c->dm;
-    auto km = [](uint32_t k) { return k == Q4_K || k == Q6_K; };
+    auto block = [](uint32_t k) { return k == Q4_0 || k == Q8_0 || k == Q4_K || k == Q5_K || k == Q6_K; };
     if (nwg != kDecodeXcds * kDecodeWgPerXcd) return false;
     if (!(d.hidden == 2048 && d.heads == 32 && d.kvheads == 4 && d.head_dim == 128)) return false;
     if (!(d.experts >= 8 && d.experts <= 128 && d.top == kDecodeXcds && d.ff == 768)) return false;
-    if (!km(c->out.kind) || c->out.cols != d.hidden) return false;
+    if (!block(c->out.kind) || c->out.cols != d.hidden || c->layers.empty()) return false;
+    const uint32_t km = c->layers[0].q.kind;  // the main format
+    if (!block(km)) return false;
+    auto mv = [&](uint32_t k) { return k == km || k == Q6_K; };
     for (const LayerW& L : c->layers) {
-        if (!(L.q.kind == Q4_K && L.k.kind == Q4_K && L.o.kind == Q4_K && L.gate.kind == Q4_K &&
-              L.up.kind == Q4_K && km(L.v.kind) && km(L.down.kind) && L.router.kind == F32))
+        if (!(L.q.kind == km && L.k.kind == km && L.o.kind == km && L.gate.kind == km && L.up.kind == km &&
+              mv(L.v.kind) && mv(L.down.kind) && L.router.kind == F32))
             return false;
     }
     return true;
+}
+
+// k_decode for the main format of the model (persist_supported holds).
+const void* decode_kernel(uint32_t km) {
+    switch (km) {
+    case Q4_0: return reinterpret_cast<const void*>(k_decode<Q4_0>);
+    case Q8_0: return reinterpret_cast<const void*>(k_decode<Q8_0>);
+    case Q4_K: return reinterpret_cast<const void*>(k_decode<Q4_K>);
+    case Q5_K: return reinterpret_cast<const void*>(k_decode<Q5_K>);
+    default: return reinterpret_cast<const void*>(k_decode<Q6_K>);
+    }
 }
 
 // Whether workgroup b of a 256-workgroup launch runs on XCD b % 8 (read from
@@ -598,10 +615,15 @@ void setup_persist(qh_ctx* c) {
     }
     hipDeviceProp_t p;
     HIP_OK(hipGetDeviceProperties(&p, c->device));
-    int per_cu = 0;
-    HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(k_decode), 512, 0));
     const uint32_t nwg = (uint32_t)p.multiProcessorCount;
-    c->persist_ok = per_cu >= 1 && persist_supported(c, nwg) && xcd_placement_ok(c, nwg);
+    if (!persist_supported(c, nwg)) {
+        c->persist_ok = c->persist = false;
+        return;
+    }
+    c->decode_fn = decode_kernel(c->layers[0].q.kind);
+    int per_cu = 0;
+    HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, c->decode_fn, 512, 0));
+    c->persist_ok = per_cu >= 1 && xcd_placement_ok(c, nwg);
     c->persist = c->persist_ok;
     if (!c->persist_ok) return;
     c->nwg = nwg;
@@ -688,7 +710,7 @@ void launch_decode(qh_ctx* c, uint32_t l0, uint32_t l1, bool vocab, bool embed) 
     A.embed = embed ? 1u : 0u;
     c->flag_base += phases;
     void* args[] = {&A};
-    HIP_OK(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_decode), dim3(c->nwg), dim3(512), args, 0,
+    HIP_OK(hipLaunchCooperativeKernel(c->decode_fn, dim3(c->nwg), dim3(512), args, 0,
                                       c->s));
 }
 

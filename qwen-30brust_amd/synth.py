@@ -25,6 +25,8 @@ import numpy as np
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "libqwen_synth.so")
 NONE = 0xFFFFFFFF
+# GGML type ids (ggml.h)
+F32, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 2, 8, 12, 13, 14
 
 ROLES = ["token_embd", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate_inp",
          "ffn_gate_exps", "ffn_up_exps", "ffn_down_exps", "output"]

@@ -196,6 +196,38 @@ def test_persistent_layer_attention_chunking(dev, layer30b_q4k, pos):
     assert rel_err(xg, xr) <= REL
 
 
+@pytest.mark.parametrize("main,out", [(synth.Q4_0, synth.Q4_0), (synth.Q8_0, synth.Q8_0),
+                                      (synth.Q5_K, synth.Q5_K), (synth.Q6_K, synth.Q4_K)])
+def test_persistent_step_main_formats(dev, main, out):
+    """The persistent step for the other block formats (Q4_0, Q8_0, Q5_K,
+    Q6_K as the q/k/o/gate/up format): two 30B-shaped layers, the second with
+    Q6_K v/down (llama.cpp's more-bits rule), vocab projection in the given
+    format; logits of three tokens and one layer at position 700 against the
+    oracle."""
+    t = synth._k_types(attn=main, down=main, out=out, embd=main)
+    spec = synth.Spec(2048, 2, 32, 4, 128, 128, 8, 768, 512, 1024, types=t,
+                      more_bits_type=synth.Q6_K, seed=11)
+    img = synth.build_image(spec, threads=8)
+    om = oracle.Model(oracle.Gguf(img), spec.context)
+    m = engine.Model(img, spec.context, device=dev)
+    assert m.persistent
+    for tok in (5, 300, 77):
+        ref = om.forward(tok)
+        got = m.forward(tok)
+        assert rel_err(got, ref) <= REL
+        assert m.last_argmax == oracle.greedy(ref)
+    pos, kvd = 700, spec.kvheads * spec.head_dim
+    for layer in (0, 1):
+        x = synth.normal(41 + layer, spec.hidden)
+        kp = synth.normal(42 + layer, pos * kvd)
+        vp = synth.normal(43 + layer, pos * kvd)
+        xr, ids_r, w_r = om.layer_forward(layer, x, pos, kp, vp)
+        xg, ids_g, w_g = m.layer_forward(layer, x, pos, kp, vp)
+        assert np.array_equal(ids_g, ids_r)
+        assert np.allclose(w_g, w_r, rtol=1e-5, atol=1e-6)
+        assert rel_err(xg, xr) <= REL
+
+
 def test_greedy_30b_token_loop_matches_oracle(dev):
     """Config 4 token loop: the random-init 48-layer Qwen3-30B-A3B Q4_K_M
     model, a 32-token uniform random prompt, then 64 greedy tokens chained on
