@@ -202,11 +202,16 @@ int qh_position(const qh_ctx *ctx, size_t *out);
  * output.  Numerics: fp16
  * operands with fp32 accumulation (logits within about 1e-2 relative of the
  * FP32 path).  Models the batched path does not cover (head_dim != 128, more
- * than 8 query heads per KV head, more than 128 experts, projections other
- * than Q4_K/Q6_K) run the prompt through the exact token step instead, one
- * per token on the device (the same bits as n qh_forward calls). */
+ * than 8 query heads per KV head, more than 128 experts, widths that are not
+ * whole 256-column super-blocks, projections that are not block-quantised)
+ * run the prompt through the exact token step instead, one per token on the
+ * device (the same bits as n qh_forward calls). */
 int qh_prefill(qh_ctx *ctx, const uint32_t *prompt, size_t n, float *logits, size_t logits_cap,
                uint32_t *argmax);
+/* Prefill implementation (no counterpart in the reference, whose prompt loop
+ * is one forward per token): *out = 1 when qh_prefill runs the loaded model's
+ * prompts through the batched GEMM path, 0 when through the exact token step. */
+int qh_prefill_batched(const qh_ctx *ctx, int *out);
 
 /* One decoder layer (the loop body src/model.rs:227-287) applied to x[hidden]
  * in place at position `pos`, with this layer's KV history replaced by
@@ -219,7 +224,8 @@ int qh_layer_forward(qh_ctx *ctx, size_t layer, float *x, size_t pos, const floa
  * host-driven): *out = 1 when qh_forward / qh_generate / qh_layer_forward run
  * the persistent single-launch step (one workgroup per CU, phases handed over
  * through memory), 0 when they run the per-phase kernels.  The persistent
- * step covers the Q4_K_M formats at Qwen3-MoE shapes; other models always
+ * step covers Qwen3-MoE shapes with block-quantised projections (one format
+ * for q, k, o, gate and up, v and down in it or Q6_K); other models always
  * use the per-phase kernels. */
 int qh_persistent(const qh_ctx *ctx, int *out);
 /* Selects the implementation for the loaded model (enable = 0: per-phase

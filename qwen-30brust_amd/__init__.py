@@ -96,6 +96,7 @@ _SIGS = {
                                    C.c_void_p, C.c_void_p, C.c_void_p]),
     "qh_bench_decode": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(C.c_double)]),
     "qh_persistent": (C.c_int, [C.c_void_p, C.POINTER(C.c_int)]),
+    "qh_prefill_batched": (C.c_int, [C.c_void_p, C.POINTER(C.c_int)]),
     "qh_set_persistent": (C.c_int, [C.c_void_p, C.c_int]),
     "qh_profile_decode": (C.c_int, [C.c_void_p, C.c_size_t, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "qh_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t,
@@ -451,6 +452,14 @@ class Model:
         rather than the per-phase kernels."""
         v = C.c_int()
         self.dev._check(lib().qh_persistent(self.dev.h, C.byref(v)))
+        return bool(v.value)
+
+    @property
+    def prefill_batched(self):
+        """True when prefill() runs this model's prompts through the batched
+        GEMM path, False when through the exact token step."""
+        v = C.c_int()
+        self.dev._check(lib().qh_prefill_batched(self.dev.h, C.byref(v)))
         return bool(v.value)
 
     @persistent.setter

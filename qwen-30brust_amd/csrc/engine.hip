@@ -561,7 +561,7 @@ void capture_graph(qh_ctx* c) {
 // workgroup per CU.
 bool persist_supported(const qh_ctx* c, uint32_t nwg) {
     const ModelDims& d = c->dm;
-    auto block = [](uint32_t k) { return k == Q4_0 || k == Q8_0 || k == Q4_K || k == Q5_K || k == Q6_K; };
+    auto block = block_kind;
     if (nwg != kDecodeXcds * kDecodeWgPerXcd) return false;
     if (!(d.hidden == 2048 && d.heads == 32 && d.kvheads == 4 && d.head_dim == 128)) return false;
     if (!(d.experts >= 8 && d.experts <= 128 && d.top == kDecodeXcds && d.ff == 768)) return false;
@@ -910,18 +910,18 @@ constexpr uint32_t kPrefillChunk = 2048;  // most prompt tokens per batched pass
 // projection Q4_K or Q6_K with column counts in 64-column slices.
 std::string prefill_gap(const qh_ctx* c) {
     const ModelDims& d = c->dm;
-    auto km = [](uint32_t k) { return k == Q4_K || k == Q6_K; };
+    auto km = block_kind;
     if (d.head_dim != 128) return "head_dim " + std::to_string(d.head_dim) + " (needs 128)";
     if (d.heads % d.kvheads || d.heads / d.kvheads > 8) return "more than 8 query heads per KV head";
     if (d.experts > 128) return "more than 128 experts";
-    if (d.hidden % 64 || d.ff % 64) return "hidden or expert width not a multiple of 64";
+    if (d.hidden % 256 || d.ff % 256) return "hidden or expert width not a multiple of 256";
     // the o-projection runs as two column halves, each whole 256-column
     // super-blocks (and an even number of 64-column GEMM slices)
     if ((d.heads * 128) % 512) return "query width not a multiple of 512";
     for (const LayerW& L : c->layers) {
         if (!(km(L.q.kind) && km(L.k.kind) && km(L.v.kind) && km(L.o.kind) && km(L.gate.kind) &&
               L.up.kind == L.gate.kind && km(L.down.kind)))
-            return "a projection is not Q4_K or Q6_K";
+            return "a projection is not block-quantised (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K)";
         if (L.router.kind != F32) return "router is not F32";
     }
     return "";
@@ -939,7 +939,9 @@ void prefill_tiles(qh_ctx* c) {
     size_t total = 0;
     for (LayerW& L : c->layers)
         for (DevMat* m : mats(L)) {
-            if (m->rows % 32 || !(m->kind == Q4_K || m->kind == Q6_K)) throw Error("tile layout needs Q4_K/Q6_K rows in groups of 32");
+            if (m->rows % 32 || m->cols % 256 || !block_kind(m->kind) ||
+                (size_t)(m->rows / 32) * tile_group_bytes(m->kind, m->cols) > (size_t)m->rows * m->drb)
+                throw Error("tile layout needs block-quantised rows in groups of 32, columns in groups of 256");
             total += (bytes(*m) + 255) / 256 * 256;
         }
     P.tiles.alloc(total);
@@ -948,7 +950,7 @@ void prefill_tiles(qh_ctx* c) {
         for (DevMat* m : mats(L)) {
             uint8_t* dst = P.tiles.as<uint8_t>() + off;
             const uint32_t experts = m->expert_stride ? c->dm.experts : 1;
-            const size_t nblk = (size_t)experts * (m->rows / 32) * m->geo.nb;
+            const size_t nblk = (size_t)experts * (m->rows / 32) * (m->cols / 256);
             hipLaunchKernelGGL(k_tile_gemm, dim3((uint32_t)std::min<size_t>(nblk, 65535)), dim3(kBlock), 0, c->s, *m,
                                experts, dst);
             HIP_OK(hipGetLastError());
@@ -999,21 +1001,27 @@ void prefill_alloc(qh_ctx* c, uint32_t cap) {
 }
 
 template <class F> void dispatch_km(uint32_t kind, F f) {
-    if (kind == Q4_K) f(std::integral_constant<uint32_t, Q4_K>{});
-    else f(std::integral_constant<uint32_t, Q6_K>{});
+    switch (kind) {
+    case Q4_0: f(std::integral_constant<uint32_t, Q4_0>{}); break;
+    case Q8_0: f(std::integral_constant<uint32_t, Q8_0>{}); break;
+    case Q4_K: f(std::integral_constant<uint32_t, Q4_K>{}); break;
+    case Q5_K: f(std::integral_constant<uint32_t, Q5_K>{}); break;
+    case Q6_K: f(std::integral_constant<uint32_t, Q6_K>{}); break;
+    default: throw Error("prefill projection is not block-quantised");
+    }
 }
 
 // C[t][cofs_i + n] = X16[t] . W_i[n] for t < S and each matrix i of `mats`
 // (one launch; with `splits` > 1 the columns are split in equal parts, part z
 // written to C + z * split_stride): the MFMA GEMM on the quantised rows
-// (Q4_K / Q6_K dequantised into the tiles).
+// (dequantised into the tiles).
 void pf_dense(qh_ctx* c, std::initializer_list<std::pair<const DevMat*, uint32_t>> mats, const _Float16* X16,
               uint32_t S, float* C, uint32_t ldc, uint32_t splits = 1, size_t split_stride = 0) {
     DenseSegs G{};
     uint32_t tiles = 0;
     for (const auto& m : mats) {
         const DevMat& W = *m.first;
-        if (W.kind != Q4_K && W.kind != Q6_K) throw Error("prefill projection is not Q4_K or Q6_K");
+        if (!block_kind(W.kind)) throw Error("prefill projection is not block-quantised");
         if ((W.cols / splits) % 256 || W.cols % splits) throw Error("prefill projection width does not split");
         G.W[G.n] = W;
         tiles += (W.rows + 127) / 128;
@@ -1844,6 +1852,13 @@ int qh_persistent(const qh_ctx* c, int* out) {
     return guarded(const_cast<qh_ctx*>(c), [&] {
         need_model(const_cast<qh_ctx*>(c));
         *out = c->persist ? 1 : 0;
+    });
+}
+
+int qh_prefill_batched(const qh_ctx* c, int* out) {
+    return guarded(const_cast<qh_ctx*>(c), [&] {
+        need_model(const_cast<qh_ctx*>(c));
+        *out = prefill_gap(c).empty() ? 1 : 0;
     });
 }
 

@@ -20,23 +20,38 @@ struct DevMat {
     RowGeo geo;
     size_t expert_stride;  // bytes between experts (rows * drb); 0 for 2-D
     // the batched-prefill GEMMs' copy of the same rows in the tile layout
-    // (Q4_K / Q6_K, rows a multiple of 32; built on the first batched
+    // (rows a multiple of 32, columns of 256; built on the first batched
     // prefill), or null.  Per expert, blocks (row group G of 32 rows,
-    // super-block b) at (G * nb + b) * tile_block_bytes(kind); expert e at
-    // e * expert_stride (the same size as the row layout).
+    // 256-column super-block b) at G * tile_group_bytes + b *
+    // tile_block_bytes(kind); expert e at e * expert_stride (the same size as
+    // the row layout).
     const uint8_t* wt;
 };
 
-// Bytes of one tile-layout block: 32 rows x one 256-column super-block.
+// The block-quantised formats (the token step's and the prefill GEMMs').
+QH_HD bool block_kind(uint32_t k) { return k == Q4_0 || k == Q8_0 || k == Q4_K || k == Q5_K || k == Q6_K; }
+
+// Bytes of one tile-layout block: 32 rows x one 256-column super-block
+// (32 x the format's bytes per 256 columns).
 //   Q4_K (4,608): headers [row][16]; quants [slice 4][lane 64][16], lane =
 //                 32 g + row holding bytes 32 slice + 16 g .. of the row's
 //                 128 quant bytes.
+//   Q5_K (5,632): as Q4_K, then high bits [lane 64][16] (bytes 16 g .. of
+//                 the row's 32).
 //   Q6_K (6,720): low bits [half 2][part 2][lane 64][16] (bytes 64 half +
 //                 32 part + 16 g ..); high bits [half 2][lane 64][16] (bytes
 //                 32 half + 16 g ..); scales [slice 4][row][4]; d [row][2].
-// A wave's load of one field for 32 rows is one contiguous 1-KB run.
-constexpr uint32_t kTileQ4K = 4608, kTileQ6K = 6720;
-QH_HD uint32_t tile_block_bytes(uint32_t kind) { return kind == Q6_K ? kTileQ6K : kTileQ4K; }
+//   Q4_0 (4,608): d [row][8][2] (the eight 32-column blocks); quants
+//                 [slice 4][part 2][row][16] (block 2 slice + part).
+//   Q8_0 (8,704): d [row][8][2]; quants [slice 4][part 2][lane 64][16]
+//                 (bytes 16 g .. of block 2 slice + part).
+// A wave's load of one field for 32 rows is one contiguous run of 0.5-1 KB.
+constexpr uint32_t kTileQ4K = 4608, kTileQ5K = 5632, kTileQ6K = 6720, kTileQ4_0 = 4608, kTileQ8_0 = 8704;
+QH_HD uint32_t tile_block_bytes(uint32_t kind) {
+    return kind == Q6_K ? kTileQ6K : kind == Q5_K ? kTileQ5K : kind == Q8_0 ? kTileQ8_0 : kind == Q4_0 ? kTileQ4_0 : kTileQ4K;
+}
+// Bytes of one row group (32 rows, all super-blocks) of a cols-wide matrix.
+QH_HD size_t tile_group_bytes(uint32_t kind, uint32_t cols) { return (size_t)(cols / 256) * tile_block_bytes(kind); }
 
 // Device-resident step state of one sequence.
 struct DevState {

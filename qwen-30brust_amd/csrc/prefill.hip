@@ -138,6 +138,110 @@ template <> struct WReg<Q6_K> {
     }
 };
 
+template <> struct WReg<Q5_K> {
+    uint4 q, hdr, qh;
+    // d*sc and -dmin*m of sub-blocks 2sl and 2sl+1; the bit of the qh bytes
+    // that holds sub-block 2sl's fifth bits
+    struct Sc { float a0, b0, a1, b1; uint32_t hs; };
+    // from tile block blk: the lane's row header, quant bytes 32 sl + 16 g ..
+    // and high-bit bytes 16 g .. of its row
+    __device__ __forceinline__ void load(const uint8_t* blk, uint32_t sl, uint32_t lane) {
+        hdr = ld16(blk + (lane & 31) * 16);
+        q = ld16(blk + 512 + sl * 1024 + lane * 16);
+        qh = ld16(blk + 4608 + lane * 16);
+    }
+    __device__ __forceinline__ Sc prep(uint32_t sl, uint32_t) const {
+        uint32_t scp, mp;
+        kscale_pair(hdr.y, hdr.z, hdr.w, sl, scp, mp);
+        const float d = h2f(hdr.x & 0xffffu), dm = h2f(hdr.x >> 16);
+        return {d * (float)(scp & 0xffu), -(dm * (float)(mp & 0xffu)), d * (float)(scp >> 8),
+                -(dm * (float)(mp >> 8)), 2 * sl};
+    }
+    // k-step S: bytes 8(S%2) .. +7, low nibbles for S < 2, high for S >= 2,
+    // each with its fifth bit (qh bit 2sl + S/2) as bit 4;
+    // d*sc*q - dmin*m (src/quant.rs:50-62) rounded once to fp16
+    template <int S>
+    __device__ __forceinline__ h8v dequant(const Sc& c, uint32_t) const {
+        const uint32_t w0 = (S & 1) ? q.z : q.x, w1 = (S & 1) ? q.w : q.y;
+        const uint32_t h0 = (S & 1) ? qh.z : qh.x, h1 = (S & 1) ? qh.w : qh.y;
+        const uint32_t ls = S < 2 ? 0 : 4, hs = c.hs + (S < 2 ? 0 : 1);
+        const uint32_t va = and_opaque(w0 >> ls, 0x0f0f0f0fu) | (and_opaque(h0 >> hs, 0x01010101u) << 4);
+        const uint32_t vb = and_opaque(w1 >> ls, 0x0f0f0f0fu) | (and_opaque(h1 >> hs, 0x01010101u) << 4);
+        const float a = S < 2 ? c.a0 : c.a1, b = S < 2 ? c.b0 : c.b1;
+        h8v v;
+        bytes_affine(v, 0, va, a, b);
+        bytes_affine(v, 4, vb, a, b);
+        return v;
+    }
+};
+
+// d of blocks 2sl and 2sl+1 (32-column blocks) from the row's eight d
+// values of the super-block
+__device__ __forceinline__ uint32_t d_pair(const uint4& dd, uint32_t sl) {
+    return sl == 0 ? dd.x : sl == 1 ? dd.y : sl == 2 ? dd.z : dd.w;
+}
+
+template <> struct WReg<Q4_0> {
+    uint4 q0, q1, dd;
+    // d and -8d of blocks 2sl and 2sl+1; the nibble of the lane's group
+    // (low for columns 0-15 of a block, high for 16-31)
+    struct Sc { float a0, b0, a1, b1; uint32_t sh; };
+    // from tile block blk: the lane's row's d values and the 16 quant bytes
+    // of blocks 2sl and 2sl+1 (both lane groups read the same bytes)
+    __device__ __forceinline__ void load(const uint8_t* blk, uint32_t sl, uint32_t lane) {
+        dd = ld16(blk + (lane & 31) * 16);
+        q0 = ld16(blk + 512 + sl * 1024 + (lane & 31) * 16);
+        q1 = ld16(blk + 512 + sl * 1024 + 512 + (lane & 31) * 16);
+    }
+    __device__ __forceinline__ Sc prep(uint32_t sl, uint32_t grp) const {
+        const uint32_t w = d_pair(dd, sl);
+        const float d0 = h2f(w & 0xffffu), d1 = h2f(w >> 16);
+        return {d0, -8.f * d0, d1, -8.f * d1, 4 * grp};
+    }
+    // k-step S: block 2sl + S/2, bytes 8(S%2) .. +7, the group's nibble;
+    // d*(q-8) (src/quant.rs:40-45) rounded once to fp16
+    template <int S>
+    __device__ __forceinline__ h8v dequant(const Sc& c, uint32_t) const {
+        const uint4& Q = S < 2 ? q0 : q1;
+        const uint32_t w0 = (S & 1) ? Q.z : Q.x, w1 = (S & 1) ? Q.w : Q.y;
+        const float a = S < 2 ? c.a0 : c.a1, b = S < 2 ? c.b0 : c.b1;
+        h8v v;
+        bytes_affine(v, 0, and_opaque(w0 >> c.sh, 0x0f0f0f0fu), a, b);
+        bytes_affine(v, 4, and_opaque(w1 >> c.sh, 0x0f0f0f0fu), a, b);
+        return v;
+    }
+};
+
+template <> struct WReg<Q8_0> {
+    uint4 q0, q1, dd;
+    // d and -128d of blocks 2sl and 2sl+1
+    struct Sc { float a0, b0, a1, b1; };
+    // from tile block blk: the lane's row's d values and quant bytes 16g ..
+    // of blocks 2sl and 2sl+1
+    __device__ __forceinline__ void load(const uint8_t* blk, uint32_t sl, uint32_t lane) {
+        dd = ld16(blk + (lane & 31) * 16);
+        q0 = ld16(blk + 512 + sl * 2048 + lane * 16);
+        q1 = ld16(blk + 512 + sl * 2048 + 1024 + lane * 16);
+    }
+    __device__ __forceinline__ Sc prep(uint32_t sl, uint32_t) const {
+        const uint32_t w = d_pair(dd, sl);
+        const float d0 = h2f(w & 0xffffu), d1 = h2f(w >> 16);
+        return {d0, -128.f * d0, d1, -128.f * d1};
+    }
+    // k-step S: block 2sl + S/2, bytes 8(S%2) .. +7; the signed byte q as
+    // (q + 128) - 128, so d*q (src/quant.rs:46-49) is one FMA, rounded once to fp16
+    template <int S>
+    __device__ __forceinline__ h8v dequant(const Sc& c, uint32_t) const {
+        const uint4& Q = S < 2 ? q0 : q1;
+        const uint32_t w0 = (S & 1) ? Q.z : Q.x, w1 = (S & 1) ? Q.w : Q.y;
+        const float a = S < 2 ? c.a0 : c.a1, b = S < 2 ? c.b0 : c.b1;
+        h8v v;
+        bytes_affine(v, 0, w0 ^ 0x80808080u, a, b);
+        bytes_affine(v, 4, w1 ^ 0x80808080u, a, b);
+        return v;
+    }
+};
+
 // Weight row of this thread (tile column): wave w, lane l -> 32w + l%32.
 __device__ __forceinline__ uint32_t rtile_row() { return 32 * (threadIdx.x >> 6) + (threadIdx.x & 31); }
 // Tile row of this thread's A load i (i < 4): 32w + 8i + l/8.
@@ -262,7 +366,7 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_gateup(const _Float16* Xn, uint
         const uint32_t ra = mt0 + arow_row(i);
         arows[i] = Xn + (size_t)(ra < rows ? G.tok[base + ra] : 0u) * H;
     }
-    const size_t gofs = (size_t)min((n0 >> 5) + (threadIdx.x >> 6), ff / 32 - 1) * Wg.geo.nb * tile_block_bytes(KIND);
+    const size_t gofs = (size_t)min((n0 >> 5) + (threadIdx.x >> 6), ff / 32 - 1) * tile_group_bytes(KIND, Wg.cols);
     const uint8_t* const wblk[2] = {Wg.wt + e * Wg.expert_stride + gofs, Wu.wt + e * Wu.expert_stride + gofs};
     f16v acc[2][4];
 #pragma unroll
@@ -302,7 +406,7 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_down(const _Float16* Hs, Expert
     for (int i = 0; i < 4; i++) arows[i] = Hs + (size_t)(base + min(mt0 + arow_row(i), rows - 1)) * ff;
     const uint8_t* const wblk[1] = {
         Wd.wt + e * Wd.expert_stride +
-        (size_t)min((n0 >> 5) + (threadIdx.x >> 6), N / 32 - 1) * Wd.geo.nb * tile_block_bytes(KIND)};
+        (size_t)min((n0 >> 5) + (threadIdx.x >> 6), N / 32 - 1) * tile_group_bytes(KIND, Wd.cols)};
     f16v acc[1][4];
 #pragma unroll
     for (int mb = 0; mb < 4; mb++) acc[0][mb] = f16v{};
@@ -333,7 +437,7 @@ __device__ __forceinline__ void dense_body(const _Float16* X16, uint32_t S, cons
 #pragma unroll
     for (int i = 0; i < 4; i++) arows[i] = X16 + (size_t)min(m0 + arow_row(i), S - 1) * ld;
     const uint8_t* const wblk[1] = {
-        W.wt + (size_t)min((n0 >> 5) + (threadIdx.x >> 6), N / 32 - 1) * W.geo.nb * tile_block_bytes(KIND)};
+        W.wt + (size_t)min((n0 >> 5) + (threadIdx.x >> 6), N / 32 - 1) * tile_group_bytes(KIND, W.cols)};
     f16v acc[1][4];
 #pragma unroll
     for (int mb = 0; mb < 4; mb++) acc[0][mb] = f16v{};
@@ -359,10 +463,13 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_dense(const _Float16* X16, uint
     const DevMat& W = G.W[i];
     const uint32_t K = W.cols / gridDim.z, kbeg = blockIdx.z * K;
     float* Cz = C + blockIdx.z * split_stride;
-    if (W.kind == Q4_K)
-        dense_body<Q4_K>(X16, S, W, mt * kGM, (t - t0) * kGN, kbeg, K, Cz, ldc, G.cofs[i], smem);
-    else
-        dense_body<Q6_K>(X16, S, W, mt * kGM, (t - t0) * kGN, kbeg, K, Cz, ldc, G.cofs[i], smem);
+    switch (W.kind) {
+#define QH_DENSE(KD) \
+    case KD: dense_body<KD>(X16, S, W, mt * kGM, (t - t0) * kGN, kbeg, K, Cz, ldc, G.cofs[i], smem); break;
+        QH_DENSE(Q4_0) QH_DENSE(Q8_0) QH_DENSE(Q4_K) QH_DENSE(Q5_K) QH_DENSE(Q6_K)
+#undef QH_DENSE
+    default: break;
+    }
 }
 
 // ------------------------------------------------------- tile layout --
@@ -390,14 +497,31 @@ __device__ __forceinline__ const uint8_t* tile_src(const uint8_t* w, uint32_t dr
             row = u >> 1;
             off = g.off_d + b * 2 + (u & 1);
         }
-    } else {
+    } else if (kind == Q4_K || kind == Q5_K) {
         if (o < 512) {  // headers
             row = o >> 4;
             off = g.off_a + b * 16 + (o & 15);
-        } else {  // quants
+        } else if (o < 4608) {  // quants
             const uint32_t u = o - 512, sl = u >> 10, lane = (u >> 4) & 63;
             row = lane & 31;
-            off = g.off_b + b * 128 + sl * 32 + (lane >> 5) * 16 + (u & 15);
+            off = (kind == Q4_K ? g.off_b : g.off_c) + b * 128 + sl * 32 + (lane >> 5) * 16 + (u & 15);
+        } else {  // Q5_K high bits
+            const uint32_t u = o - 4608, lane = (u >> 4) & 63;
+            row = lane & 31;
+            off = g.off_b + b * 32 + (lane >> 5) * 16 + (u & 15);
+        }
+    } else {  // Q4_0, Q8_0: eight 32-column blocks per 256 columns
+        if (o < 512) {  // d of the eight blocks
+            row = o >> 4;
+            off = g.off_b + (8 * b + ((o & 15) >> 1)) * 2 + (o & 1);
+        } else if (kind == Q4_0) {  // 16 quant bytes of block 2sl + part
+            const uint32_t u = o - 512, sl = u >> 10, part = (u >> 9) & 1;
+            row = (u >> 4) & 31;
+            off = g.off_a + (8 * b + 2 * sl + part) * 16 + (u & 15);
+        } else {  // Q8_0: bytes 16g .. of block 2sl + part
+            const uint32_t u = o - 512, sl = u >> 11, part = (u >> 10) & 1, lane = (u >> 4) & 63;
+            row = lane & 31;
+            off = g.off_a + (8 * b + 2 * sl + part) * 32 + (lane >> 5) * 16 + (u & 15);
         }
     }
     return w + (size_t)(32 * G + row) * drb + off;
@@ -405,7 +529,7 @@ __device__ __forceinline__ const uint8_t* tile_src(const uint8_t* w, uint32_t dr
 
 // The tile copy of matrix m (every expert): workgroup = one block.
 __global__ __launch_bounds__(kBlock) void k_tile_gemm(DevMat m, uint32_t experts, uint8_t* __restrict__ dst) {
-    const uint32_t nb = m.geo.nb, groups = m.rows / 32, bb = tile_block_bytes(m.kind);
+    const uint32_t nb = m.cols / 256, groups = m.rows / 32, bb = tile_block_bytes(m.kind);
     const size_t nblk = (size_t)experts * groups * nb;
     for (size_t blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
         const uint32_t e = (uint32_t)(blk / ((size_t)groups * nb)), rem = (uint32_t)(blk % ((size_t)groups * nb));
@@ -1040,7 +1164,10 @@ __global__ __launch_bounds__(kBlock) void k_pf_kvh(const float* kcache, const fl
     template __global__ void k_gemm_gateup<K>(const _Float16*, uint32_t, ExpertTiles, DevMat, DevMat, _Float16*);     \
     template __global__ void k_gemm_down<K>(const _Float16*, ExpertTiles, DevMat, float*);                          \
 
+QH_INSTANTIATE_PREFILL_GEMM(Q4_0)
+QH_INSTANTIATE_PREFILL_GEMM(Q8_0)
 QH_INSTANTIATE_PREFILL_GEMM(Q4_K)
+QH_INSTANTIATE_PREFILL_GEMM(Q5_K)
 QH_INSTANTIATE_PREFILL_GEMM(Q6_K)
 
 }  // namespace qh

@@ -88,6 +88,7 @@ def test_prefill_matches_oracle(dev, model2, n):
     extra = [7, 300, 11, 499]
     refs, gap = oracle_logits(spec, img, prompt, extra)
     m = engine.Model(img, spec.context, device=dev)
+    assert m.prefill_batched
     am, lg = m.prefill(prompt)
     err = rel_err(lg, refs[0])
     margin = check_top1(am, refs[0])
@@ -99,6 +100,31 @@ def test_prefill_matches_oracle(dev, model2, n):
             e2 = rel_err(m.forward(t), ref)
             print(f"  decode after prefill: rel err {e2:.2e}")
             assert e2 <= 2 * TOL
+
+
+@pytest.mark.parametrize("main,out", [(synth.Q4_0, synth.Q4_0), (synth.Q8_0, synth.Q8_0),
+                                      (synth.Q5_K, synth.Q5_K), (synth.Q6_K, synth.Q4_K)])
+def test_prefill_main_formats(dev, main, out):
+    """The batched path's other weight formats (Q4_0, Q8_0, Q5_K, Q6_K
+    projections dequantised in the GEMM tiles): two 30B-shaped layers, the
+    second with Q6_K v/down; a 65-token prompt, then two decode steps."""
+    t = synth._k_types(attn=main, down=main, out=out, embd=main)
+    spec = synth.Spec(2048, 2, 32, 4, 128, 128, 8, 768, 512, 512, types=t, more_bits_type=synth.Q6_K, seed=12)
+    img = synth.build_image(spec, threads=min(16, os.cpu_count() or 1))
+    prompt = np.random.default_rng(65).integers(0, spec.vocab, 65).astype(np.uint32)
+    extra = [7, 300]
+    refs, gap = oracle_logits(spec, img, prompt, extra)
+    m = engine.Model(img, spec.context, device=dev)
+    assert m.prefill_batched
+    am, lg = m.prefill(prompt)
+    err = rel_err(lg, refs[0])
+    margin = check_top1(am, refs[0])
+    print(f"kind {main}: last-token logits rel err {err:.2e}, oracle top-1 margin {margin:.3e}, router gap {gap:.2e}")
+    check_logits(err, gap)
+    assert m.position == len(prompt)
+    if err <= TOL:
+        for t, ref in zip(extra, refs[1:]):
+            assert rel_err(m.forward(t), ref) <= 2 * TOL
 
 
 def test_prefill_chunks_match_one_pass(dev, model2, monkeypatch):
@@ -139,6 +165,7 @@ def test_prefill_uncovered_model_runs_the_exact_step(dev):
     from helpers import GOLDEN
     path = os.path.join(GOLDEN, "tiny-qwen3moe.gguf")
     m = engine.Model(path, 8, device=dev)
+    assert not m.prefill_batched
     prompt = np.array([1, 5, 2, 9], np.uint32)
     am, lg = m.prefill(prompt)
     assert m.position == 4
@@ -159,6 +186,7 @@ def test_prefill_odd_query_width_runs_the_exact_step(dev):
     img = synth.build_image(spec)
     prompt = np.random.default_rng(3).integers(0, spec.vocab, 9).astype(np.uint32)
     m = engine.Model(img, spec.context, device=dev)
+    assert not m.prefill_batched
     am, lg = m.prefill(prompt)
     assert m.position == 9
     ref = engine.Model(img, spec.context, device=dev)
