@@ -38,7 +38,8 @@ constexpr int kGL = kGK + 8;  // LDS row pitch in halfs (144 bytes)
 // (k-group, k-step) is exact as long as A uses the same one.  The B values
 // are dequantised from the lane's weight bytes straight into registers (no
 // LDS round trip, no barrier), each value the f32 d*sc*q - dmin*m (Q4_K) or
-// d*sc*(q-32) (Q6_K) of one FMA, converted to fp16; the weight bytes come from
+// d*sc*(q-32) (Q6_K) of one FMA, rounded to fp16 (bytes_affine: a byte
+// permute and one mixed-precision FMA per value); the weight bytes come from
 // the tile layout (DevMat::wt), where a wave's load of one field for its 32
 // rows is one contiguous 1-KB run.  The activations go through LDS,
 // double-buffered with two slices in flight in registers, one barrier per
@@ -47,15 +48,23 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 
 template <uint32_t KIND> struct WReg;
 
-// Four fp16 values fma(byte i of m, a, b), i = 0..3, into v[o .. o+3]: the
-// integer bytes convert exactly to f32 (v_cvt_f32_ubyteN), one f32 FMA, then
-// the conversion to fp16.
-__device__ __forceinline__ void bytes_affine(h8v& v, int o, uint32_t m, float a, float b) {
-    v[o] = (_Float16)fmaf((float)(m & 0xffu), a, b);
-    v[o + 1] = (_Float16)fmaf((float)((m >> 8) & 0xffu), a, b);
-    v[o + 2] = (_Float16)fmaf((float)((m >> 16) & 0xffu), a, b);
-    v[o + 3] = (_Float16)fmaf((float)(m >> 24), a, b);
+// Four fp16 values a * (byte i of m) + b, i = 0..3, into v[o .. o+3], from
+// c = b - 1024 a: v_perm_b32 puts byte i under the fp16 exponent of 1024
+// (the half 0x64XX is exactly 1024 + XX), and one v_fma_mix per value
+// computes (1024 + XX) * a + c in f32 from that half and rounds it to fp16;
+// the product is exact, so the value differs from fma(XX, a, b) only by the
+// f32 rounding of c (2^-24 of 1024 |a|).
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void bytes_affine(h8v& v, int o, uint32_t m, float a, float c) {
+    const h2v lo = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, m, 0x04010400u));  // bytes 0, 1
+    const h2v hi = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, m, 0x04030402u));  // bytes 2, 3
+    v[o] = (_Float16)fmaf((float)lo[0], a, c);
+    v[o + 1] = (_Float16)fmaf((float)lo[1], a, c);
+    v[o + 2] = (_Float16)fmaf((float)hi[0], a, c);
+    v[o + 3] = (_Float16)fmaf((float)hi[1], a, c);
 }
+// The bias c of bytes_affine for the value a * q + b.
+__device__ __forceinline__ float bias1024(float a, float b) { return fmaf(-1024.f, a, b); }
 // w & mk, opaque to the optimiser: knowing the mask, it would narrow each
 // byte extraction to a bit-field one and lose the byte-convert form
 __device__ __forceinline__ uint32_t and_opaque(uint32_t w, uint32_t mk) {
@@ -66,8 +75,9 @@ __device__ __forceinline__ uint32_t and_opaque(uint32_t w, uint32_t mk) {
 
 template <> struct WReg<Q4_K> {
     uint4 q, hdr;
-    // d*sc and -dmin*m of sub-blocks 2sl (low nibbles) and 2sl+1 (high
-    // nibbles, kept in place: their scale is divided by 16, exactly)
+    // d*sc and the bytes_affine bias of -dmin*m of sub-blocks 2sl (low
+    // nibbles) and 2sl+1 (high nibbles, kept in place: their scale is
+    // divided by 16, exactly)
     struct Sc { float a0, b0, a1, b1; };
     // from tile block blk (32 rows, one super-block): the lane's row header
     // and quant bytes 32 sl + 16 g .. of its row
@@ -79,8 +89,8 @@ template <> struct WReg<Q4_K> {
         uint32_t scp, mp;
         kscale_pair(hdr.y, hdr.z, hdr.w, sl, scp, mp);
         const float d = h2f(hdr.x & 0xffffu), dm = h2f(hdr.x >> 16);
-        return {d * (float)(scp & 0xffu), -(dm * (float)(mp & 0xffu)), d * (float)(scp >> 8) * 0.0625f,
-                -(dm * (float)(mp >> 8))};
+        const float a0 = d * (float)(scp & 0xffu), a1 = d * (float)(scp >> 8) * 0.0625f;
+        return {a0, bias1024(a0, -(dm * (float)(mp & 0xffu))), a1, bias1024(a1, -(dm * (float)(mp >> 8)))};
     }
     // k-step S: bytes 8(S%2) .. +7, low nibbles for S < 2, high for S >= 2;
     // d*sc*q - dmin*m (src/quant.rs:50-62) rounded once to fp16
@@ -99,7 +109,8 @@ template <> struct WReg<Q4_K> {
 template <> struct WReg<Q6_K> {
     uint4 l0, l1, qh;
     uint32_t sc4, d;
-    // d*sc and -32 d*sc of the lane's two scales (sets l0 and l1)
+    // d*sc and the bytes_affine bias of -32 d*sc, the lane's two scales
+    // (sets l0 and l1)
     struct Sc { float a0, b0, a1, b1; };
     // slice sl = 2c + p of the super-block (half c, nibble p), from tile
     // block blk: low-bit bytes 64c + 16g .. and 64c + 32 + 16g .. of the
@@ -117,7 +128,7 @@ template <> struct WReg<Q6_K> {
         const float df = h2f(d);
         const float a0 = df * (float)(int8_t)((sc4 >> (8 * grp)) & 0xffu);
         const float a1 = df * (float)(int8_t)((sc4 >> (8 * (grp + 2))) & 0xffu);
-        return {a0, -32.f * a0, a1, -32.f * a1};
+        return {a0, -1056.f * a0, a1, -1056.f * a1};  // bias1024(a, -32 a)
     }
     // k-step S: set S/2 (l0 with scale byte g, or l1 with byte g+2), bytes
     // 8(S%2) .. +7; d*sc*(q-32) (src/quant.rs:63-77) with q = nibble p | two
@@ -140,8 +151,8 @@ template <> struct WReg<Q6_K> {
 
 template <> struct WReg<Q5_K> {
     uint4 q, hdr, qh;
-    // d*sc and -dmin*m of sub-blocks 2sl and 2sl+1; the bit of the qh bytes
-    // that holds sub-block 2sl's fifth bits
+    // d*sc and the bytes_affine bias of -dmin*m of sub-blocks 2sl and 2sl+1;
+    // the bit of the qh bytes that holds sub-block 2sl's fifth bits
     struct Sc { float a0, b0, a1, b1; uint32_t hs; };
     // from tile block blk: the lane's row header, quant bytes 32 sl + 16 g ..
     // and high-bit bytes 16 g .. of its row
@@ -154,8 +165,8 @@ template <> struct WReg<Q5_K> {
         uint32_t scp, mp;
         kscale_pair(hdr.y, hdr.z, hdr.w, sl, scp, mp);
         const float d = h2f(hdr.x & 0xffffu), dm = h2f(hdr.x >> 16);
-        return {d * (float)(scp & 0xffu), -(dm * (float)(mp & 0xffu)), d * (float)(scp >> 8),
-                -(dm * (float)(mp >> 8)), 2 * sl};
+        const float a0 = d * (float)(scp & 0xffu), a1 = d * (float)(scp >> 8);
+        return {a0, bias1024(a0, -(dm * (float)(mp & 0xffu))), a1, bias1024(a1, -(dm * (float)(mp >> 8))), 2 * sl};
     }
     // k-step S: bytes 8(S%2) .. +7, low nibbles for S < 2, high for S >= 2,
     // each with its fifth bit (qh bit 2sl + S/2) as bit 4;
@@ -183,7 +194,8 @@ __device__ __forceinline__ uint32_t d_pair(const uint4& dd, uint32_t sl) {
 
 template <> struct WReg<Q4_0> {
     uint4 q0, q1, dd;
-    // d and -8d of blocks 2sl and 2sl+1; the nibble of the lane's group
+    // d and the bytes_affine bias of -8d, blocks 2sl and 2sl+1; the nibble
+    // of the lane's group
     // (low for columns 0-15 of a block, high for 16-31)
     struct Sc { float a0, b0, a1, b1; uint32_t sh; };
     // from tile block blk: the lane's row's d values and the 16 quant bytes
@@ -196,7 +208,7 @@ template <> struct WReg<Q4_0> {
     __device__ __forceinline__ Sc prep(uint32_t sl, uint32_t grp) const {
         const uint32_t w = d_pair(dd, sl);
         const float d0 = h2f(w & 0xffffu), d1 = h2f(w >> 16);
-        return {d0, -8.f * d0, d1, -8.f * d1, 4 * grp};
+        return {d0, -1032.f * d0, d1, -1032.f * d1, 4 * grp};  // bias1024(d, -8 d)
     }
     // k-step S: block 2sl + S/2, bytes 8(S%2) .. +7, the group's nibble;
     // d*(q-8) (src/quant.rs:40-45) rounded once to fp16
@@ -214,7 +226,7 @@ template <> struct WReg<Q4_0> {
 
 template <> struct WReg<Q8_0> {
     uint4 q0, q1, dd;
-    // d and -128d of blocks 2sl and 2sl+1
+    // d and the bytes_affine bias of -128d, blocks 2sl and 2sl+1
     struct Sc { float a0, b0, a1, b1; };
     // from tile block blk: the lane's row's d values and quant bytes 16g ..
     // of blocks 2sl and 2sl+1
@@ -226,7 +238,7 @@ template <> struct WReg<Q8_0> {
     __device__ __forceinline__ Sc prep(uint32_t sl, uint32_t) const {
         const uint32_t w = d_pair(dd, sl);
         const float d0 = h2f(w & 0xffffu), d1 = h2f(w >> 16);
-        return {d0, -128.f * d0, d1, -128.f * d1};
+        return {d0, -1152.f * d0, d1, -1152.f * d1};  // bias1024(d, -128 d)
     }
     // k-step S: block 2sl + S/2, bytes 8(S%2) .. +7; the signed byte q as
     // (q + 128) - 128, so d*q (src/quant.rs:46-49) is one FMA, rounded once to fp16
