@@ -1073,14 +1073,22 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
                 for (int kt = 0; kt < 4; kt++)
 #pragma unroll
                     for (int qt = 0; qt < (int)kQT; qt++) st[kt][qt] = f4v{0.f, 0.f, 0.f, 0.f};
+                // every K fragment of the block first (one LDS wait, not one
+                // per product)
+                h8v kf[4][4];
+#pragma unroll
+                for (uint32_t ks = 0; ks < 4; ks++)
+#pragma unroll
+                    for (uint32_t kt = 0; kt < 4; kt++)
+                        kf[ks][kt] = *reinterpret_cast<const h8v*>(Kl + (16 * kt + col) * kKL + 32 * ks + 8 * grp);
+                __builtin_amdgcn_sched_barrier(0);  // keeps the reads together, ahead of the products
 #pragma unroll
                 for (uint32_t ks = 0; ks < 4; ks++) {
 #pragma unroll
                     for (uint32_t kt = 0; kt < 4; kt++) {
-                        const h8v af = *reinterpret_cast<const h8v*>(Kl + (16 * kt + col) * kKL + 32 * ks + 8 * grp);
 #pragma unroll
                         for (uint32_t qt = 0; qt < kQT; qt++)
-                            st[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, qf[qt][ks], st[kt][qt], 0, 0, 0);
+                            st[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[ks][kt], qf[qt][ks], st[kt][qt], 0, 0, 0);
                     }
                 }
                 // causal mask, online softmax per query
@@ -1127,15 +1135,20 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
                             pb[qt][i] = (_Float16)st[2 * ks2][qt][i];
                             pb[qt][4 + i] = (_Float16)st[2 * ks2 + 1][qt][i];
                         }
+                    // the eight V^T fragments of this key half first
+                    h8v va[8];
 #pragma unroll
                     for (uint32_t dt = 0; dt < 8; dt++) {
                         const _Float16* vrow = Vt + (16 * dt + col) * kVL + 32 * ks2 + 4 * grp;
                         const uint2 lo = *reinterpret_cast<const uint2*>(vrow), hi = *reinterpret_cast<const uint2*>(vrow + 16);
-                        const h8v va = __builtin_bit_cast(h8v, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                        va[dt] = __builtin_bit_cast(h8v, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (uint32_t dt = 0; dt < 8; dt++)
 #pragma unroll
                         for (uint32_t qt = 0; qt < kQT; qt++)
-                            o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[qt], o[qt][dt], 0, 0, 0);
-                    }
+                            o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt], pb[qt], o[qt][dt], 0, 0, 0);
                 }
             }
             __syncthreads();
