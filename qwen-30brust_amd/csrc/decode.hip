@@ -680,6 +680,31 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
 // attention columns (chunks 16X..16X+15): wave wv rows 64j + 8wv + rr + 4i
 // (i < 2), lane = (rr lane/16, chunk lane%16).  The router fold
 // F[e] . a over the same columns for experts 4j..4j+3 (two waves each).
+// Brings the scalar-cache lines of one layer descriptor (576 bytes, 64-byte
+// aligned: nine lines) in with one s_load_dword per line and a single wait, so
+// that the layer's own descriptor loads hit the scalar cache instead of each
+// waiting for a line that the weight stream of the previous token evicted.
+// The outputs are early-clobber: none may share a register with the base
+// address, which the later loads of the block still read.
+__device__ __forceinline__ void warm_layer(const LayerW* p) {
+    static_assert(sizeof(LayerW) == 576, "nine 64-byte lines");
+    uint32_t d0, d1, d2, d3, d4, d5, d6, d7, d8;
+    asm volatile(
+        "s_load_dword %0, %9, 0x0\n"
+        "s_load_dword %1, %9, 0x40\n"
+        "s_load_dword %2, %9, 0x80\n"
+        "s_load_dword %3, %9, 0xc0\n"
+        "s_load_dword %4, %9, 0x100\n"
+        "s_load_dword %5, %9, 0x140\n"
+        "s_load_dword %6, %9, 0x180\n"
+        "s_load_dword %7, %9, 0x1c0\n"
+        "s_load_dword %8, %9, 0x200\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&s"(d0), "=&s"(d1), "=&s"(d2), "=&s"(d3), "=&s"(d4), "=&s"(d5), "=&s"(d6), "=&s"(d7), "=&s"(d8)
+        : "s"(p)
+        : "memory");
+}
+
 template <uint32_t KO>
 __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
                                             uint32_t l) {
@@ -691,6 +716,8 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
         w[i] = Fmt<KO>::load(L.o.w + (size_t)(kRowsWg * c.j + 8 * c.wv + rr + 4 * i) * L.o.drb, L.o.geo, ch);
     const uint32_t fe = min(kExpWg * c.j + (c.tid >> 7), c.E - 1), fc = 512 * c.X + 4 * (c.tid & 127);
     const float4 f = gld<float4>(L.rfold + (size_t)fe * c.qd + fc);
+    // the next layer's descriptor, while this phase waits for the partials
+    if (l + 1 < A.l1) warm_layer(A.layers + l + 1);
     QH_MARK(2, 0);
     float* ps = S.big;             // [nch][4][130] chunk partials (padded layout)
     float* xs = S.big + 9216;      // [512] merged attention output (padded layout)
@@ -1155,6 +1182,7 @@ __global__ __launch_bounds__(kDT) void k_decode(DecodeArgs A) {
     }
     c.pos = A.a.st->pos;
     const uint32_t err0 = A.a.st->err;
+    if (A.l0 < A.l1) warm_layer(A.layers + A.l0);  // while the state loads are in flight
     __syncthreads();
     if (c.pos >= dm.ctx || (err0 & kErrToken)) {
         if (c.b == 0 && c.tid == 0 && c.pos >= dm.ctx) atomicOr(&A.a.st->err, kErrContext);
