@@ -1183,6 +1183,26 @@ __global__ __launch_bounds__(kDT) void k_decode(DecodeArgs A) {
     c.pos = A.a.st->pos;
     const uint32_t err0 = A.a.st->err;
     if (A.l0 < A.l1) warm_layer(A.layers + A.l0);  // while the state loads are in flight
+    {
+        // the launch's arguments, likewise (seven 64-byte lines, read
+        // throughout every layer)
+        static_assert(sizeof(DecodeArgs) <= 448, "seven 64-byte lines");
+        const auto* ka = (const __attribute__((address_space(4))) uint8_t*)__builtin_amdgcn_kernarg_segment_ptr();
+        uint32_t d0, d1, d2, d3, d4, d5, d6, d7;
+        asm volatile(
+            "s_load_dword %0, %8, 0x0\n"
+            "s_load_dword %1, %8, 0x40\n"
+            "s_load_dword %2, %8, 0x80\n"
+            "s_load_dword %3, %8, 0xc0\n"
+            "s_load_dword %4, %8, 0x100\n"
+            "s_load_dword %5, %8, 0x140\n"
+            "s_load_dword %6, %8, 0x180\n"
+            "s_load_dword %7, %8, 0x1b4\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&s"(d0), "=&s"(d1), "=&s"(d2), "=&s"(d3), "=&s"(d4), "=&s"(d5), "=&s"(d6), "=&s"(d7)
+            : "s"(ka)
+            : "memory");
+    }
     __syncthreads();
     if (c.pos >= dm.ctx || (err0 & kErrToken)) {
         if (c.b == 0 && c.tid == 0 && c.pos >= dm.ctx) atomicOr(&A.a.st->err, kErrContext);
