@@ -672,14 +672,6 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
     return true;
 }
 
-// ============================================= C: merge + o-projection ==
-// Every workgroup gathers the XCD's chunk partials and merges them:
-// a = sum_c o_c exp(m_c - M) / sum_c l_c exp(m_c - M) for the 4 heads (the
-// chunk weights by wave 0, lane = (head, chunk), then thread = (head, dim)).
-// Then rows [64j, 64j+64) of the o-projection restricted to this XCD's 512
-// attention columns (chunks 16X..16X+15): wave wv rows 64j + 8wv + rr + 4i
-// (i < 2), lane = (rr lane/16, chunk lane%16).  The router fold
-// F[e] . a over the same columns for experts 4j..4j+3 (two waves each).
 // Brings the scalar-cache lines of one layer descriptor (576 bytes, 64-byte
 // aligned: nine lines) in with one s_load_dword per line and a single wait, so
 // that the layer's own descriptor loads hit the scalar cache instead of each
@@ -705,6 +697,14 @@ __device__ __forceinline__ void warm_layer(const LayerW* p) {
         : "memory");
 }
 
+// ============================================= C: merge + o-projection ==
+// Every workgroup gathers the XCD's chunk partials and merges them:
+// a = sum_c o_c exp(m_c - M) / sum_c l_c exp(m_c - M) for the 4 heads (the
+// chunk weights by wave 0, lane = (head, chunk), then thread = (head, dim)).
+// Then rows [64j, 64j+64) of the o-projection restricted to this XCD's 512
+// attention columns (chunks 16X..16X+15): wave wv rows 64j + 8wv + rr + 4i
+// (i < 2), lane = (rr lane/16, chunk lane%16).  The router fold
+// F[e] . a over the same columns for experts 4j..4j+3 (two waves each).
 template <uint32_t KO>
 __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, const LayerW& L, const Ctx& c0,
                                             uint32_t l) {
