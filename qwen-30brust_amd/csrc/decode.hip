@@ -95,13 +95,15 @@ static_assert(kQkvWg == 24 && kQkvWg % kDW == 0, "three q|k|v rows per wave");
 
 // A layer's v or down format: KM, or Q6_K (the host checks it is one of them).
 #define QH_DISPATCH_KM(kind, KM, K, ...)                                      \
-    if ((kind) == ::qh::Q6_K) {                                               \
-        constexpr uint32_t K = ::qh::Q6_K;                                    \
-        __VA_ARGS__;                                                          \
-    } else {                                                                  \
-        constexpr uint32_t K = KM;                                            \
-        __VA_ARGS__;                                                          \
-    }
+    do {                                                                      \
+        if ((kind) == ::qh::Q6_K) {                                           \
+            constexpr uint32_t K = ::qh::Q6_K;                                \
+            __VA_ARGS__;                                                      \
+        } else {                                                              \
+            constexpr uint32_t K = KM;                                        \
+            __VA_ARGS__;                                                      \
+        }                                                                     \
+    } while (0)
 // The vocab projection's format: any block-quantised one.
 #define QH_DISPATCH_BLOCK(kind, K, ...)                                         \
     switch (kind) {                                                             \
