@@ -57,6 +57,19 @@ __device__ __forceinline__ T gld(const void* p) {
 #endif
 }
 __device__ __forceinline__ uint4 ld16(const uint8_t* p) { return gld<uint4>(p); }
+// The same load marked non-temporal (the weight chunks of load() below: the
+// token step reads each weight row once per token, and keeping those
+// streams from allocating as reusable lines in the vector L1 measured 1.5 %
+// faster per token).
+__device__ __forceinline__ uint4 ld16s(const uint8_t* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+    const u4v t = __builtin_nontemporal_load((gptr<u4v>)p);
+    return make_uint4(t.x, t.y, t.z, t.w);
+#else
+    return *reinterpret_cast<const uint4*>(p);  // host pass: never executed
+#endif
+}
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return gld<uint16_t>(p); }
 
 // Hides a value from the optimiser's known-bits analysis, so that byte k of a
@@ -104,7 +117,7 @@ template <> struct Fmt<Q4_K> {
     static __device__ __forceinline__ uint32_t xoff_b(uint32_t c) { return xoff_a(c) + 32; }
     static __device__ __forceinline__ Raw load(const uint8_t* row, const RowGeo& g, uint32_t c) {
         uint32_t b = c >> 3, j = c & 7;
-        return {ld16(row + g.off_b + b * 128 + j * 16), ld16(row + g.off_a + b * 16)};
+        return {ld16s(row + g.off_b + b * 128 + j * 16), ld16s(row + g.off_a + b * 16)};
     }
     static __device__ __forceinline__ float dot(const Raw& r, uint32_t c, const float* xa,
                                                 const float* xb, float sa, float sb) {
@@ -131,8 +144,8 @@ template <> struct Fmt<Q5_K> {
     static __device__ __forceinline__ uint32_t xoff_b(uint32_t c) { return xoff_a(c) + 32; }
     static __device__ __forceinline__ Raw load(const uint8_t* row, const RowGeo& g, uint32_t c) {
         uint32_t b = c >> 3, j = c & 7;
-        return {ld16(row + g.off_c + b * 128 + j * 16), ld16(row + g.off_a + b * 16),
-                ld16(row + g.off_b + b * 32 + (j & 1) * 16)};
+        return {ld16s(row + g.off_c + b * 128 + j * 16), ld16s(row + g.off_a + b * 16),
+                ld16s(row + g.off_b + b * 32 + (j & 1) * 16)};
     }
     static __device__ __forceinline__ float dot(const Raw& r, uint32_t c, const float* xa,
                                                 const float* xb, float sa, float sb) {
@@ -171,8 +184,8 @@ template <> struct Fmt<Q6_K> {
     static __device__ __forceinline__ uint32_t xoff_b(uint32_t c) { return xoff_a(c) + 64; }
     static __device__ __forceinline__ Raw load(const uint8_t* row, const RowGeo& g, uint32_t c) {
         uint32_t b = c >> 3, j = c & 7;
-        return {ld16(row + g.off_a + b * 128 + j * 16),
-                ld16(row + g.off_b + b * 64 + (j >> 2) * 32 + (j & 1) * 16),
+        return {ld16s(row + g.off_a + b * 128 + j * 16),
+                ld16s(row + g.off_b + b * 64 + (j >> 2) * 32 + (j & 1) * 16),
                 gld<uint2>(row + g.off_c + b * 16 + (j >> 2) * 8),
                 gld<uint32_t>(row + g.off_d + (b >> 1) * 4)};
     }
@@ -209,7 +222,7 @@ template <> struct Fmt<Q4_0> {
     static __device__ __forceinline__ uint32_t xoff_b(uint32_t c) { return c * 32 + 16; }
     static __device__ __forceinline__ Raw load(const uint8_t* row, const RowGeo& g, uint32_t c) {
         // d in the aligned 32-bit word holding it (the row is padded past it)
-        return {ld16(row + g.off_a + c * 16), gld<uint32_t>(row + g.off_b + (c >> 1) * 4)};
+        return {ld16s(row + g.off_a + c * 16), gld<uint32_t>(row + g.off_b + (c >> 1) * 4)};
     }
     static __device__ __forceinline__ float dot(const Raw& r, uint32_t c, const float* xa,
                                                 const float* xb, float sa, float sb) {
@@ -230,7 +243,7 @@ template <> struct Fmt<Q8_0> {
     static __device__ __forceinline__ uint32_t xoff_a(uint32_t c) { return c * 32; }
     static __device__ __forceinline__ uint32_t xoff_b(uint32_t c) { return c * 32 + 16; }
     static __device__ __forceinline__ Raw load(const uint8_t* row, const RowGeo& g, uint32_t c) {
-        return {ld16(row + g.off_a + c * 32), ld16(row + g.off_a + c * 32 + 16),
+        return {ld16s(row + g.off_a + c * 32), ld16s(row + g.off_a + c * 32 + 16),
                 gld<uint32_t>(row + g.off_b + (c >> 1) * 4)};
     }
     static __device__ __forceinline__ float dot(const Raw& r, uint32_t c, const float* xa,
@@ -253,7 +266,7 @@ template <> struct Fmt<F16> {
     static __device__ __forceinline__ uint32_t xoff_b(uint32_t c) { return c * 32 + 16; }
     static __device__ __forceinline__ Raw load(const uint8_t* row, const RowGeo&, uint32_t c) {
         const uint8_t* p = row + c * 64;
-        return {ld16(p), ld16(p + 16), ld16(p + 32), ld16(p + 48)};
+        return {ld16s(p), ld16s(p + 16), ld16s(p + 32), ld16s(p + 48)};
     }
     static __device__ __forceinline__ float dot(const Raw& r, uint32_t, const float* xa,
                                                 const float* xb, float, float) {
