@@ -44,16 +44,20 @@ constexpr int mv_xv() { return NT == kMvT ? (int)(kMvMaxXFloats / 4 + kMvT - 1) 
 
 // Chunk loads of a row through a buffer resource: the row's byte offset is
 // one 32-bit add per lane, the field offsets (RowGeo) go in the scalar offset.
+// The loads carry the non-temporal hint (cache policy nt): every weight byte
+// is read once per launch, and streams that do not allocate as reusable
+// lines in the vector L1 measured 5-7 % faster on the 256 MB vocab matrix.
+constexpr int kMvAux = 2;  // nt
 __device__ __forceinline__ uint4 bld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kMvAux);
     return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
 }
 __device__ __forceinline__ uint2 bld8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, kMvAux);
     return make_uint2((uint32_t)v[0], (uint32_t)v[1]);
 }
 __device__ __forceinline__ uint32_t bld4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, kMvAux);
 }
 
 // The same bytes as Fmt<KIND>::load (qh_device.hpp), for the row at byte
@@ -328,9 +332,10 @@ bool launch_mv_stream(const DevMat& m, const uint8_t* const* mats, uint32_t nb, 
     }
 }
 
-// Read-only stream: every 16-byte word of p[0, n16) loaded once, folded by
-// xor (a word is stored only if the fold hits one fixed value, so the loads
-// cannot be dropped).  Each workgroup reads one contiguous range (XCD x, which
+// Read-only stream: every 16-byte word of p[0, n16) loaded once (with the
+// non-temporal hint, as the matvec's weight loads), folded by xor (a word is
+// stored only if the fold hits one fixed value, so the loads cannot be
+// dropped).  Each workgroup reads one contiguous range (XCD x, which
 // runs workgroups b = x mod 8, covers the x-th eighth), eight 16-byte loads
 // in flight per thread.  Its rate is the device's practical read ceiling
 // beside the matvec timings.
@@ -343,7 +348,11 @@ __global__ __launch_bounds__(kMvT) void k_read_stream(const uint4* __restrict__ 
     for (; i + 7 * kMvT < end; i += 8 * kMvT) {
         uint4 v[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = gld<uint4>(p + i + k * kMvT);
+        for (int k = 0; k < 8; k++) {
+            typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+            const u4v t = __builtin_nontemporal_load((gptr<u4v>)(p + i + k * kMvT));
+            v[k] = make_uint4(t.x, t.y, t.z, t.w);
+        }
 #pragma unroll
         for (int k = 0; k < 8; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
     }
