@@ -896,6 +896,15 @@ __global__ __launch_bounds__(1024) void k_pf_group(const uint32_t* ids, uint32_t
 // next layer's attention RMSNorm weights) the block also writes that norm's
 // fp16 output (k_pf_norm's arithmetic, with the sum of squares taken in this
 // kernel's element order), so the next layer starts on its GEMM.
+
+// A float4 read once (non-temporal hint): the combine's expert rows, 134 MB
+// per layer at 30B, each read by exactly one workgroup.
+__device__ __forceinline__ float4 ld4s(const float* p) {
+    typedef float f4s __attribute__((ext_vector_type(4)));
+    const f4s t = __builtin_nontemporal_load((gptr<f4s>)p);
+    return make_float4(t.x, t.y, t.z, t.w);
+}
+
 __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y, const float* wts, uint32_t H,
                                                        uint32_t top, const float* nw, float eps, _Float16* Xn16) {
     __shared__ float red[kWaves];
@@ -911,7 +920,7 @@ __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y,
         // their values unused)
         float4 y[8];
 #pragma unroll
-        for (uint32_t k = 0; k < 8; k++) y[k] = *reinterpret_cast<const float4*>(Y + (t * top + min(k, top - 1)) * H + i);
+        for (uint32_t k = 0; k < 8; k++) y[k] = ld4s(Y + (t * top + min(k, top - 1)) * H + i);
         float4 xv = *reinterpret_cast<const float4*>(X + t * H + i);
         float4 moe = make_float4(0.f, 0.f, 0.f, 0.f);
         {
