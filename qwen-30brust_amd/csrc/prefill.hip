@@ -275,10 +275,13 @@ constexpr int kRA = 2 * kGM * kGL;  // halfs of LDS: the two A buffers
 // rows: those outputs are not stored); wblk[nb]: tile block (G, 0) of matrix
 // nb for this wave's row group G = (n0 + 32w) / 32 (likewise clamped).  STAGES register stages
 // of weight loads run ahead; the loads are unconditional (clamped), so each
-// wait covers exactly one stage.
+// wait covers exactly one stage.  With full false (workgroup-uniform: a tile
+// whose valid rows fit in the first 64) row blocks 2 and 3 are skipped, and
+// acc[.][2..3] stay as they are.
 template <uint32_t KIND, int NB, int STAGES>
 __device__ __forceinline__ void gemm_tile_r(const _Float16* const (&arows)[4], const uint8_t* const (&wblk)[NB],
-                                            uint32_t K, f16v (&acc)[NB][4], _Float16* As, uint32_t kbeg = 0) {
+                                            uint32_t K, f16v (&acc)[NB][4], _Float16* As, uint32_t kbeg = 0,
+                                            bool full = true) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, grp = lane >> 5;
     static_assert(STAGES % 2 == 0, "slice k uses A buffer k % 2 = its stage's parity");
     const uint32_t nsl = K / kGK;
@@ -326,15 +329,25 @@ __device__ __forceinline__ void gemm_tile_r(const _Float16* const (&arows)[4], c
                 const uint32_t col = 32 * (S >> 1) + 16 * grp + 8 * (S & 1);
                 h8v af[4], bf[NB];
 #pragma unroll
-                for (int mb = 0; mb < 4; mb++)
+                for (int mb = 0; mb < 2; mb++)
                     af[mb] = *reinterpret_cast<const h8v*>(Ab + (32 * mb + (lane & 31)) * kGL + col);
 #pragma unroll
                 for (int nb = 0; nb < NB; nb++) bf[nb] = wr[st][nb].template dequant<S>(sc[nb], p);
 #pragma unroll
                 for (int nb = 0; nb < NB; nb++)
 #pragma unroll
-                    for (int mb = 0; mb < 4; mb++)
+                    for (int mb = 0; mb < 2; mb++)
                         acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mb], bf[nb], acc[nb][mb], 0, 0, 0);
+                if (full) {
+#pragma unroll
+                    for (int mb = 2; mb < 4; mb++)
+                        af[mb] = *reinterpret_cast<const h8v*>(Ab + (32 * mb + (lane & 31)) * kGL + col);
+#pragma unroll
+                    for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+                        for (int mb = 2; mb < 4; mb++)
+                            acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mb], bf[nb], acc[nb][mb], 0, 0, 0);
+                }
             };
             kstep(std::integral_constant<int, 0>{});
             kstep(std::integral_constant<int, 1>{});
@@ -385,7 +398,9 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_gateup(const _Float16* Xn, uint
     for (int nb = 0; nb < 2; nb++)
 #pragma unroll
         for (int mb = 0; mb < 4; mb++) acc[nb][mb] = f16v{};
-    gemm_tile_r<KIND, 2, 2>(arows, wblk, Wg.cols, acc, smem);
+    // a tile of at most 64 valid rows (an expert's remainder past its full
+    // tiles) multiplies two row blocks, not four
+    gemm_tile_r<KIND, 2, 2>(arows, wblk, Wg.cols, acc, smem, 0, rows - mt0 > 64);
     const uint32_t n = n0 + racc_col();
 #pragma unroll
     for (int mb = 0; mb < 4; mb++)
@@ -422,7 +437,7 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_down(const _Float16* Hs, Expert
     f16v acc[1][4];
 #pragma unroll
     for (int mb = 0; mb < 4; mb++) acc[0][mb] = f16v{};
-    gemm_tile_r<KIND, 1, 2>(arows, wblk, ff, acc, smem);
+    gemm_tile_r<KIND, 1, 2>(arows, wblk, ff, acc, smem, 0, rows - mt0 > 64);  // as in k_gemm_gateup
     const uint32_t n = n0 + racc_col();
 #pragma unroll
     for (int mb = 0; mb < 4; mb++)
