@@ -554,16 +554,32 @@ __device__ __forceinline__ const uint8_t* tile_src(const uint8_t* w, uint32_t dr
     return w + (size_t)(32 * G + row) * drb + off;
 }
 
-// The tile copy of matrix m (every expert): workgroup = one block.
+// Whether the 16 tile bytes at o (a multiple of 16) are 16 consecutive source
+// bytes: every field but Q6_K's scales (4-byte runs) and d (2-byte runs).
+__device__ __forceinline__ bool tile_run16(uint32_t kind, uint32_t o) { return kind != Q6_K || o < 6144; }
+
+// The tile copy of matrix m (every expert): workgroup = one block, 16-byte
+// copies where the layout keeps 16 source bytes together (a 16-byte aligned
+// matrix), single bytes elsewhere.
 __global__ __launch_bounds__(kBlock) void k_tile_gemm(DevMat m, uint32_t experts, uint8_t* __restrict__ dst) {
     const uint32_t nb = m.cols / 256, groups = m.rows / 32, bb = tile_block_bytes(m.kind);
     const size_t nblk = (size_t)experts * groups * nb;
+    const bool vec = (reinterpret_cast<uintptr_t>(m.w) % 16 == 0) && m.drb % 16 == 0 && m.expert_stride % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(dst) % 16 == 0;
     for (size_t blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
         const uint32_t e = (uint32_t)(blk / ((size_t)groups * nb)), rem = (uint32_t)(blk % ((size_t)groups * nb));
         const uint32_t G = rem / nb, b = rem % nb;
         const uint8_t* w = m.w + (size_t)e * m.expert_stride;
         uint8_t* out = dst + (size_t)e * m.expert_stride + ((size_t)G * nb + b) * bb;
-        for (uint32_t o = threadIdx.x; o < bb; o += kBlock) out[o] = *tile_src(w, m.drb, m.geo, m.kind, G, b, o);
+        for (uint32_t o = 16 * threadIdx.x; o < bb; o += 16 * kBlock) {  // bb is a multiple of 16
+            if (vec && tile_run16(m.kind, o)) {
+                *reinterpret_cast<uint4*>(out + o) =
+                    *reinterpret_cast<const uint4*>(tile_src(w, m.drb, m.geo, m.kind, G, b, o));
+            } else {
+#pragma unroll 4
+                for (uint32_t k = 0; k < 16; k++) out[o + k] = *tile_src(w, m.drb, m.geo, m.kind, G, b, o + k);
+            }
+        }
     }
 }
 
