@@ -906,8 +906,9 @@ uint64_t matvecs_per_token(const qh_ctx* c) { return c->cfg.layers * (5 + 3 * c-
 constexpr uint32_t kPrefillChunk = 2048;  // most prompt tokens per batched pass
 
 // Whether the batched prefill covers the model: head_dim 128 with at most 8
-// query heads per KV head, at most 128 experts, F32 router, and every
-// projection Q4_K or Q6_K with column counts in 64-column slices.
+// query heads per KV head, at most 128 experts, F32 router, widths in whole
+// 256-column super-blocks, and every projection block-quantised (gate and up
+// in one format).  Empty when covered, else the first reason it is not.
 std::string prefill_gap(const qh_ctx* c) {
     const ModelDims& d = c->dm;
     auto km = block_kind;
