@@ -161,7 +161,6 @@ struct DecodeLds {
     float red[2 * kDW];
     float ra[kExpWg];         // router term of this XCD's columns for experts 4j..4j+3
     float lg[128];            // router logits
-    float mw[kHX * kMaxChunks];  // merge weight of each (head, chunk)
     alignas(16) long long ck[128];  // composite top-k keys
     float sv[8];
     uint32_t sid[8];
@@ -727,7 +726,9 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
     if (!gather_l(A, S, lbuf(A.lpart, kDecodeStridePart, c.X), nch * kHX * kPartWords, ptag(A, l, 2), ps, c.tid))
         return false;  // the chunk partials (phase B)
     QH_MARK(2, 1);
-    if (c.wv == 0) {
+    {
+        // every wave computes the 64 merge weights (lane = (head, chunk)) and
+        // reads its head's from its own lanes: no hand-over through LDS
         const uint32_t h = c.lane >> 4, ck = c.lane & 15, pb = (ck * kHX + h) * kPartWords;
         const bool on = ck < nch;
         const float m = on ? ps[px(pb + 128)] : -INFINITY;
@@ -737,13 +738,12 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
         M = fmaxf(M, dpp_f<kDppMirror>(M));  // max over the head's 16 lanes
         const float e = on ? expf(m - M) : 0.f;
         const float Ls = seg_sum(on ? ps[px(pb + 129)] * e : 0.f, 16);
-        S.mw[c.lane] = e / Ls;
-    }
-    __syncthreads();
-    {
-        const uint32_t h = c.tid >> 7, d = c.tid & 127;
+        const float mw = e / Ls;
+        const uint32_t hw = __builtin_amdgcn_readfirstlane(c.tid >> 7), d = c.tid & 127;  // head of this wave
         float a = 0.f;
-        for (uint32_t ck = 0; ck < nch; ck++) a = fmaf(ps[px((ck * kHX + h) * kPartWords + d)], S.mw[h * 16 + ck], a);
+        for (uint32_t k = 0; k < nch; k++)
+            a = fmaf(ps[px((k * kHX + hw) * kPartWords + d)],
+                     __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(mw), hw * 16 + k)), a);
         xs[px(c.tid)] = a;
     }
     __syncthreads();
