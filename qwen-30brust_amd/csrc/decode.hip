@@ -654,7 +654,9 @@ __device__ __forceinline__ bool phase_attn(const DecodeArgs& A, DecodeLds& S, co
             const float vb = vs[key * kTP + 16 * wv + col];
             oacc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vb, oacc, 0, 0, 0);
         }
-        __syncthreads();
+        // the next tile rewrites vs and ps; after the last one the output
+        // goes to ot, a region of its own
+        if (tt + kDTile < t1) __syncthreads();
     }
     QH_MARK(1, 2);
     // O to LDS as [head][128]; wave h < 4 passes head h's partial on
