@@ -1015,7 +1015,13 @@ __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y,
 // (about nqb/2 + 1 key blocks per pass pair) and two fit each CU.
 constexpr uint32_t kAQ = 16, kAK = 64;
 constexpr uint32_t kQT = kAQ / 16;  // 16-query tiles per wave
-constexpr uint32_t kKL = 128 + 8, kVL = kAK + 8;  // LDS pitches (halfs)
+// LDS pitches (halfs).  K rows of 272 bytes, their 16-byte column chunks
+// swizzled (kchunk) so that the staging writes (four threads per key) spread
+// over the banks like the fragment reads (one chunk per 8 lanes); V^T rows of
+// 136 bytes, so that the 16 rows one 8-byte fragment read spans fall on
+// distinct banks (written 8 bytes at a time).
+constexpr uint32_t kKL = 128 + 8, kVL = kAK + 4;
+__device__ __forceinline__ uint32_t kchunk(uint32_t c) { return c ^ (2 * (c >> 3)); }
 
 __device__ __forceinline__ uint2 pack4h(float a, float b, float c, float d) {
     h8v t;  // only the first four used
@@ -1102,8 +1108,10 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
         for (uint32_t k0 = 0; k0 < kend; k0 += kAK) {
 #pragma unroll
             for (uint32_t i = 0; i < 4; i++) {
-                *reinterpret_cast<uint4*>(Kl + skey * kKL + sd0 + 8 * i) = kr[i];
-                *reinterpret_cast<uint4*>(Vt + sdim * kVL + skk0 + 8 * i) = vr[i];
+                *reinterpret_cast<uint4*>(Kl + skey * kKL + 8 * kchunk(sd0 / 8 + i)) = kr[i];
+                uint2* vd = reinterpret_cast<uint2*>(Vt + sdim * kVL + skk0 + 8 * i);
+                vd[0] = make_uint2(vr[i].x, vr[i].y);
+                vd[1] = make_uint2(vr[i].z, vr[i].w);
             }
             __syncthreads();
             if (k0 + kAK < kend) kvload(k0 + kAK);  // next block, during this one
@@ -1120,7 +1128,7 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
                 for (uint32_t ks = 0; ks < 4; ks++)
 #pragma unroll
                     for (uint32_t kt = 0; kt < 4; kt++)
-                        kf[ks][kt] = *reinterpret_cast<const h8v*>(Kl + (16 * kt + col) * kKL + 32 * ks + 8 * grp);
+                        kf[ks][kt] = *reinterpret_cast<const h8v*>(Kl + (16 * kt + col) * kKL + 8 * kchunk(4 * ks + grp));
                 __builtin_amdgcn_sched_barrier(0);  // keeps the reads together, ahead of the products
 #pragma unroll
                 for (uint32_t ks = 0; ks < 4; ks++) {
