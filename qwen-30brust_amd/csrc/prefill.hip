@@ -845,11 +845,15 @@ __global__ __launch_bounds__(kBlock) void k_pf_topk(const float* LR, uint32_t nk
 // Groups the S*top (token, slot) assignments by expert (one workgroup):
 // goff = exclusive prefix of the per-expert counts, tok/asg = the
 // assignments sorted by expert (order within an expert is arbitrary), and
-// the list of 128-row GEMM tiles (te, tm).
+// the list of 128-row GEMM tiles (te, tm).  Up to 16,384 assignments are
+// placed in LDS first and stored in order (coalesced: stored straight to
+// their sorted positions, every store instruction of a wave touched up to 64
+// cache lines).
 __global__ __launch_bounds__(1024) void k_pf_group(const uint32_t* ids, uint32_t n, uint32_t top, uint32_t E,
                                                    uint32_t* goff, uint32_t* tok, uint32_t* asg, uint32_t* te,
                                                    uint32_t* tm, uint32_t* ntile) {
     __shared__ uint32_t cnt[256], cur[256], tb[256];  // E <= 255
+    __shared__ uint32_t srt[16384], ntot;              // sorted assignments, their count
     for (uint32_t e = threadIdx.x; e < 256; e += 1024) cnt[e] = 0;
     // this thread's assignments a = threadIdx.x + 1024 i, all loaded before
     // any is used (one memory round trip instead of one per assignment)
@@ -898,7 +902,10 @@ __global__ __launch_bounds__(1024) void k_pf_group(const uint32_t* ids, uint32_t
             off += c4[k];
             toff += t4[k];
         }
-        if (lane == 63) *ntile = ti;
+        if (lane == 63) {
+            *ntile = ti;
+            ntot = ci;
+        }
     }
     __syncthreads();
     for (uint32_t e = threadIdx.x; e < E; e += 1024)
@@ -906,13 +913,26 @@ __global__ __launch_bounds__(1024) void k_pf_group(const uint32_t* ids, uint32_t
             te[t] = e;
             tm[t] = m;
         }
+    const bool staged = n <= 1024 * kPer;  // workgroup-uniform
 #pragma unroll
     for (uint32_t i = 0; i < kPer; i++) {
         const uint32_t a = threadIdx.x + 1024 * i;
         if (myid[i] >= E) continue;
         const uint32_t p = atomicAdd(&cur[myid[i]], 1u);
-        tok[p] = a / top;
-        asg[p] = a;
+        if (staged) {
+            srt[p] = a;
+        } else {
+            tok[p] = a / top;
+            asg[p] = a;
+        }
+    }
+    if (staged) {
+        __syncthreads();
+        for (uint32_t p = threadIdx.x; p < ntot; p += 1024) {
+            const uint32_t a = srt[p];
+            tok[p] = a / top;
+            asg[p] = a;
+        }
     }
     for (uint32_t a = threadIdx.x + 1024 * kPer; a < n; a += 1024) {
         if (ids[a] >= E) continue;
