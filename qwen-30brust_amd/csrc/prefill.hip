@@ -1019,8 +1019,9 @@ __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y,
 
 // ----------------------------------------------------------- attention --
 // Causal GQA attention (ops.rs:57-98) of 16-query blocks of the chunk -- at
-// positions p0 + q -- for 4 of the G <= 8 query heads of KV head g (wave w:
-// head 4 hf + w), over keys [0, p0 + q], on the fp16 matrix
+// positions p0 + q -- for the G <= 8 query heads of KV head g (wave w: heads
+// 2w and 2w + 1, which share every K and V fragment the wave reads from LDS),
+// over keys [0, p0 + q], on the fp16 matrix
 // cores with an online softmax in fp32.  Keys come from an fp16 copy of the
 // layer's K ([kvhead][pos][128]) and V, transposed ([kvhead][128][pos], row
 // pitch vp, a multiple of 64), so a
@@ -1030,11 +1031,13 @@ __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y,
 //                 order inside a 32-key step being the same permutation for
 //                 P and V),
 //   O  += P V    (queries x 128 dims).
-// Workgroup b takes query blocks nqb-1-b and then b: the causal triangle
+// Workgroup (b, g) takes query blocks nqb-1-b and then b: the causal triangle
 // gives block q about q key blocks, so every workgroup has the same work
-// (about nqb/2 + 1 key blocks per pass pair) and two fit each CU.
+// (about nqb/2 + 1 key blocks per pass pair).  Two heads per wave halve the
+// LDS reads per product against one head per wave (twice the workgroups):
+// -4 % per launch at 2,048 tokens.
 constexpr uint32_t kAQ = 16, kAK = 64;
-constexpr uint32_t kQT = kAQ / 16;  // 16-query tiles per wave
+constexpr uint32_t kQT = 2;  // query heads per wave (index qt), each over the block's 16 queries
 // LDS pitches (halfs).  K rows of 272 bytes, their 16-byte column chunks
 // swizzled (kchunk) so that the staging writes (four threads per key) spread
 // over the banks like the fragment reads (one chunk per 8 lanes); V^T rows of
@@ -1063,17 +1066,16 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
         const uint32_t qb = pass == 0 ? nqb - 1 - blockIdx.x : blockIdx.x;
         if (pass == 1 && qb >= nqb - 1 - blockIdx.x) break;
         const uint32_t q0 = qb * kAQ;
-        const uint32_t g = blockIdx.y >> 1, hf = blockIdx.y & 1;
+        const uint32_t g = blockIdx.y;
         const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, grp = lane >> 4, col = lane & 15;
-        const uint32_t hh = 4 * hf + w;  // query head within the group (wave-uniform)
-        const bool hok = hh < G;
+        const bool hok = kQT * w < G;  // the wave's first head exists (wave-uniform)
         // scores / sqrt(128) (ops.rs:87), exponentiated base 2
         const float sc2 = 1.4426950408889634f / sqrtf(128.0f);
         h8v qf[kQT][4];
 #pragma unroll
         for (uint32_t qt = 0; qt < kQT; qt++) {
-            const uint32_t q = q0 + 16 * qt + col;
-            const bool ok = hok && q < S;
+            const uint32_t q = q0 + col, hh = kQT * w + qt;
+            const bool ok = hh < G && q < S;
             const _Float16* src = Q16 + ((size_t)(g * G + hh) * S + q) * 128 + 8 * grp;
 #pragma unroll
             for (uint32_t ks = 0; ks < 4; ks++) {
@@ -1162,7 +1164,7 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
                 // causal mask, online softmax per query
 #pragma unroll
                 for (uint32_t qt = 0; qt < kQT; qt++) {
-                    const uint32_t qpos = p0 + q0 + 16 * qt + col;
+                    const uint32_t qpos = p0 + q0 + col;
                     float mx = -INFINITY;
 #pragma unroll
                     for (uint32_t kt = 0; kt < 4; kt++)
@@ -1227,8 +1229,8 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
             float lt = l[qt] + __shfl_xor(l[qt], 16, 64);
             lt += __shfl_xor(lt, 32, 64);
             const float inv = 1.0f / lt;
-            const uint32_t q = q0 + 16 * qt + col;
-            if (q < S) {
+            const uint32_t q = q0 + col, hh = kQT * w + qt;
+            if (q < S && hh < G) {
                 _Float16* dst = O16 + (size_t)q * qd + (g * G + hh) * 128 + 4 * grp;
 #pragma unroll
                 for (uint32_t dt = 0; dt < 8; dt++)
