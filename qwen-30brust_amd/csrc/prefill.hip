@@ -1034,8 +1034,7 @@ __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y,
 // Workgroup (b, g) takes query blocks nqb-1-b and then b: the causal triangle
 // gives block q about q key blocks, so every workgroup has the same work
 // (about nqb/2 + 1 key blocks per pass pair).  Two heads per wave halve the
-// LDS reads per product against one head per wave (twice the workgroups):
-// -4 % per launch at 2,048 tokens.
+// LDS reads per product against one head per wave (twice the workgroups).
 constexpr uint32_t kAQ = 16, kAK = 64;
 constexpr uint32_t kQT = 2;  // query heads per wave (index qt), each over the block's 16 queries
 // LDS pitches (halfs).  K rows of 272 bytes, their 16-byte column chunks
