@@ -479,7 +479,10 @@ __device__ __forceinline__ void dense_body(const _Float16* X16, uint32_t S, cons
         }
 }
 
-__global__ __launch_bounds__(kGT, 2) void k_gemm_dense(const _Float16* X16, uint32_t S, DenseSegs G, float* C,
+// Three workgroups per CU (168 VGPRs, 4 of them spilled): the q|k|v grid of
+// 16 x 40 tiles at 2,048 tokens then runs in one round of 768 workgroup slots
+// rather than 1.25 rounds of 512.
+__global__ __launch_bounds__(kGT, 3) void k_gemm_dense(const _Float16* X16, uint32_t S, DenseSegs G, float* C,
                                                     uint32_t ldc, size_t split_stride) {
     __shared__ __align__(16) _Float16 smem[kRA];
     uint32_t mt, t;
