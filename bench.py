@@ -61,6 +61,29 @@ def algorithmic_bytes(model, pos_avg):
     return b
 
 
+def active_weight_bytes(model):
+    """Weight bytes one decode token must read (no activations, no KV): the
+    embedding row, every layer's attention matrices, router and norms, the
+    routed experts' gate/up/down rows, the final norm and the vocab matrix."""
+    c = model.config
+    H, top, ff = c["hidden"], c["top"], c["intermediate"]
+    w = tensor_bytes(model, "token_embd.weight", 1) + tensor_bytes(model, "output_norm.weight")
+    for i in range(c["layers"]):
+        p = f"blk.{i}."
+        w += sum(tensor_bytes(model, p + n) for n in ("attn_q.weight", "attn_k.weight", "attn_v.weight",
+                                                        "attn_output.weight", "ffn_gate_inp.weight",
+                                                        "attn_norm.weight", "attn_q_norm.weight",
+                                                        "attn_k_norm.weight", "ffn_norm.weight"))
+        w += top * (tensor_bytes(model, p + "ffn_gate_exps.weight", ff) + tensor_bytes(model, p + "ffn_up_exps.weight", ff)
+                    + tensor_bytes(model, p + "ffn_down_exps.weight", H))
+    out = "output.weight"
+    try:
+        model.tensor(out)
+    except Exception:
+        out = "token_embd.weight"
+    return w + tensor_bytes(model, out)
+
+
 def prefill_flops(model, n):
     """Algorithmic flops of a batched prefill of n tokens from position 0:
     every projection (q, k, v, o, F32 router, the top experts' gate/up/down)
@@ -184,6 +207,9 @@ def main():
                     help="skip the per-phase kernels' comparison line (profiler runs of k_decode alone)")
     ap.add_argument("--prefill", type=int, default=2048,
                     help="tokens of the batched-prefill measurement (0: skip)")
+    ap.add_argument("--long-pos", type=int, default=3584,
+                    help="also time decode steps from this position, the KV cache filled by a batched "
+                         "prefill (0: skip)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (a known-size "
                          "kernel that calibrates HBM byte counters)")
@@ -289,7 +315,25 @@ def main():
         log(f"batched prefill {args.prefill} tokens: {pms:.1f} ms, {args.prefill / pms * 1e3:.0f} tok/s, "
             f"{tfs:.0f} TFLOP/s")
 
-    w_active = sum(bytes_cls[k] for k in ("qkv", "oproj", "gateup", "down", "vocab"))
+    long_ctx = None
+    if args.long_pos > 0 and args.long_pos + 24 <= spec.context:
+        # decode late in the context (--ctx 4096): the KV cache of the first
+        # long_pos positions filled by the batched prefill, then event-timed
+        # greedy steps; the KV history read grows by 196,608 B per position
+        model.reset()
+        model.prefill(rng.integers(0, spec.vocab, args.long_pos).astype(np.uint32), want_logits=False)
+        lw, ls = 4, 16
+        lms = model.bench_decode(lw, ls) / ls
+        lp = args.long_pos + lw + ls / 2
+        lbytes = sum(algorithmic_bytes(model, lp).values())
+        long_ctx = {"positions": [args.long_pos + lw, args.long_pos + lw + ls], "ms_per_token": round(lms, 4),
+                    "tok_s": round(1000.0 / lms, 2), "algorithmic_bytes_per_token": int(lbytes),
+                    "GB_s": round(lbytes / (lms * 1e-3) / 1e9, 1),
+                    "frac": round(lbytes / (lms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"decode at positions {args.long_pos + lw}-{args.long_pos + lw + ls}: {lms:.3f} ms/token, "
+            f"{1000.0 / lms:.1f} tok/s ({long_ctx['GB_s']:.0f} GB/s)")
+
+    w_active = active_weight_bytes(model)
     matvec = [] if args.no_matvec else matvec_cases(engine, synth, dev)
     cpu = None if args.no_cpu else cpu_baseline(img, spec, threads, int(pos_dec) if persistent else int(pos_mid))
 
@@ -324,6 +368,7 @@ def main():
         "per_phase_kernels": None if ms_alt is None else {"ms_per_token": round(ms_alt, 4),
                                                           "tok_s": round(1000.0 / ms_alt, 2), "breakdown": classes},
         "prefill": prefill,
+        "long_context": long_ctx,
         "matvec": matvec,
         "cpu_baseline": cpu,
     }

@@ -205,7 +205,11 @@ int qh_position(const qh_ctx *ctx, size_t *out);
  * than 8 query heads per KV head, more than 128 experts, widths that are not
  * whole 256-column super-blocks, projections that are not block-quantised)
  * run the prompt through the exact token step instead, one per token on the
- * device (the same bits as n qh_forward calls). */
+ * device (the same bits as n qh_forward calls).  Errors as that loop of
+ * forwards: the first prompt token at the context limit fails with "context
+ * limit N reached", a token outside the vocabulary with "token outside
+ * vocabulary" (src/model.rs:219-223), and every failure leaves a clean cache
+ * at position 0 (src/model.rs:209-216). */
 int qh_prefill(qh_ctx *ctx, const uint32_t *prompt, size_t n, float *logits, size_t logits_cap,
                uint32_t *argmax);
 /* Prefill implementation (no counterpart in the reference, whose prompt loop
@@ -238,8 +242,13 @@ int qh_set_persistent(qh_ctx *ctx, int enable);
  * in rank order, as the last step that processed each position (qh_forward,
  * qh_generate, qh_prefill, either step implementation) chose them;
  * qh_read_kv copies layer `layer`'s K and V for those positions in the
- * reference's time-major layout [t][kvheads][head_dim] (src/ops.rs:84,93). */
+ * reference's time-major layout [t][kvheads][head_dim] (src/ops.rs:84,93);
+ * qh_route_gap_log copies, for the same steps, how close each routing
+ * decision was: gaps[n][layers] = (top-th - (top+1)-th largest router logit)
+ * / max |router logit| (+inf when every expert is routed), a decision with a
+ * gap near 0 being one that rounding may turn either way. */
 int qh_route_log(qh_ctx *ctx, size_t pos0, size_t n, uint32_t *ids);
+int qh_route_gap_log(qh_ctx *ctx, size_t pos0, size_t n, float *gaps);
 int qh_read_kv(qh_ctx *ctx, size_t layer, size_t pos0, size_t n, float *k, float *v);
 
 /* Fault injection for tests of the failure paths (no counterpart in the

@@ -162,6 +162,7 @@ struct or_model {
     float *output_norm; /* [H] */
     size_t position, context;
     float *last_router; /* [layers][experts] */
+    uint32_t *forced;   /* [layers][top] expert ids for the next step only, or NULL */
 };
 
 static size_t norm_stride(const or_config *c) { return 2 * c->hidden + 2 * c->head_dim; }
@@ -345,6 +346,7 @@ void or_model_free(or_model *m) {
     free(m->norms);
     free(m->output_norm);
     free(m->last_router);
+    free(m->forced);
     free(m);
 }
 
@@ -408,7 +410,18 @@ static int layer_body(or_model *m, size_t i, float *x, size_t pos, kvbuf *kv, si
     if (or_rms(xn, nm + H + 2 * d, H, c->eps)) goto out;
     MV("ffn_gate_inp", -1, xn, H, logits);
     memcpy(m->last_router + i * c->experts, logits, c->experts * sizeof(float));
-    if (or_route(logits, c->experts, c->top, ids, w)) goto out;
+    if (m->forced) {
+        /* checker hook: the caller's expert ids in the caller's rank order,
+         * weighted by the softmax over this path's own logits at those ids
+         * (the arithmetic of ops.rs:45-56 after its selection) */
+        for (size_t s = 0; s < c->top; s++) {
+            ids[s] = m->forced[i * c->top + s];
+            w[s] = logits[ids[s]];
+        }
+        if (or_softmax(w, c->top)) goto out;
+    } else if (or_route(logits, c->experts, c->top, ids, w)) {
+        goto out;
+    }
     for (size_t j = 0; j < H; j++) moe[j] = 0.f;
     for (size_t s = 0; s < c->top; s++) {
         MV("ffn_gate_exps", (int64_t)ids[s], xn, H, gate);
@@ -466,6 +479,8 @@ out:
 /* model.rs:209-216: roll back to a clean cache on any error */
 static int forward_checked(or_model *m, uint32_t token, float *logits, int threads, int vocab) {
     int rc = forward_inner(m, token, logits, threads, vocab);
+    free(m->forced); /* a forced routing holds for one step */
+    m->forced = NULL;
     if (rc) {
         char saved[512];
         snprintf(saved, sizeof saved, "%s", or_last_error());
@@ -512,6 +527,22 @@ int or_model_kv(const or_model *m, size_t layer, float *k, float *v, size_t cap)
         memcpy(v, b->v, b->len * sizeof(float));
     }
     return (int)0;
+}
+
+int or_model_force_routes(or_model *m, const uint32_t *ids, size_t n) {
+    const or_config *c = &m->c;
+    if (n != c->layers * c->top) return or_fail("forced routes need layers x top ids");
+    for (size_t i = 0; i < c->layers; i++)
+        for (size_t s = 0; s < c->top; s++) {
+            uint32_t e = ids[i * c->top + s];
+            if (e >= c->experts) return or_fail("forced expert out of range");
+            for (size_t t = 0; t < s; t++)
+                if (ids[i * c->top + t] == e) return or_fail("forced experts repeat");
+        }
+    free(m->forced);
+    m->forced = malloc(n * sizeof(uint32_t));
+    memcpy(m->forced, ids, n * sizeof(uint32_t));
+    return 0;
 }
 
 int or_model_last_router(const or_model *m, size_t layer, float *out, size_t n) {

@@ -115,6 +115,11 @@ int or_layer_forward(or_model *m, size_t layer, float *x, size_t pos,
                      int threads);
 /* Read the model's KV cache for one layer (time-major), for tests. */
 int or_model_kv(const or_model *m, size_t layer, float *k, float *v, size_t cap);
+/* Checker hook (no reference counterpart): the next forward/step routes
+ * layer i to ids[i*top .. i*top+top) in that rank order instead of its own
+ * top-k, with weights = softmax of its own router logits at those ids (the
+ * arithmetic of ops.rs:45-56 after the selection).  Holds for one step. */
+int or_model_force_routes(or_model *m, const uint32_t *ids, size_t n);
 /* Router logits of the last forward (per layer, experts floats), for near-tie
  * diagnostics of end-to-end runs. */
 int or_model_last_router(const or_model *m, size_t layer, float *out, size_t n);

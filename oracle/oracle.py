@@ -73,6 +73,7 @@ def _load():
                                    C.c_void_p, C.c_void_p, i32]),
         "or_model_kv": (i32, [C.c_void_p, sz, _f32p, _f32p, sz]),
         "or_model_last_router": (i32, [C.c_void_p, sz, _f32p, sz]),
+        "or_model_force_routes": (i32, [C.c_void_p, _u32p, sz]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -315,16 +316,27 @@ class Model:
     def reset(self):
         lib().or_model_reset(self.h)
 
-    def forward(self, token, threads=None):
+    def force_routes(self, ids):
+        """Route the next forward/step to `ids` ([layers][top], in rank
+        order) instead of the oracle's own top-k; the weights are the softmax
+        of the oracle's own router logits at those ids.  One step only."""
+        ids = np.ascontiguousarray(ids, np.uint32).reshape(-1)
+        _check(lib().or_model_force_routes(self.h, ids, ids.size))
+
+    def forward(self, token, threads=None, routes=None):
+        if routes is not None:
+            self.force_routes(routes)
         out = np.empty(self.config["vocab"], np.float32)
         _check(lib().or_model_forward(self.h, token, out.ctypes.data,
                                       self.threads if threads is None else threads))
         return out
 
-    def step(self, token, threads=None):
+    def step(self, token, threads=None, routes=None):
         """forward() without the final norm and vocab projection: the layers,
         the KV append and the position advance only (for long prompts whose
         intermediate logits are not compared)."""
+        if routes is not None:
+            self.force_routes(routes)
         _check(lib().or_model_step(self.h, token, self.threads if threads is None else threads))
 
     def routes(self):

@@ -104,6 +104,7 @@ _SIGS = {
     "qh_model_generation": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint64)]),
     "qh_fault_inject": (C.c_int, [C.c_void_p, C.c_uint32]),
     "qh_route_log": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
+    "qh_route_gap_log": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
     "qh_read_kv": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p]),
     "qh_profile_step": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]),
     "qh_bench_read": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p]),
@@ -348,6 +349,16 @@ class Model:
         c = self.config
         out = np.zeros((max(n, 1), c["layers"], c["top"]), np.uint32)
         self.dev._check(lib().qh_route_log(self.dev.h, pos0, n, _ptr(out)))
+        return out[:n]
+
+    def route_gaps(self, pos0, n):
+        """[n][layers] relative gap between the top-th and (top+1)-th router
+        logit of each routing decision recorded for positions pos0..pos0+n
+        (diagnostics: how near a tie each choice was)."""
+        self._live()
+        c = self.config
+        out = np.zeros((max(n, 1), c["layers"]), np.float32)
+        self.dev._check(lib().qh_route_gap_log(self.dev.h, pos0, n, _ptr(out)))
         return out[:n]
 
     def read_kv(self, layer, pos0, n):

@@ -163,6 +163,8 @@ struct DecodeLds {
     float lg[128];            // router logits
     alignas(16) long long ck[128];  // composite top-k keys
     float sv[8];
+    float s9;                 // router logit of rank top (+inf gap when none), for the gap log
+    float slast;              // smallest router logit
     uint32_t sid[8];
     float wts[8];             // routing weights of the current layer
     uint32_t ids[8];          // routed experts of the current layer
@@ -867,6 +869,7 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
         S.ck[c.tid] = c.tid < E ? (long long)(((uint64_t)(uint32_t)total_key(lv) << 32) | (uint32_t)~c.tid)
                                 : LLONG_MIN;
     }
+    if (c.tid == 0) S.s9 = -INFINITY;  // stays when every expert is routed
     __syncthreads();
     QH_MARK(4, 4);
     if (S.bad) {
@@ -894,6 +897,8 @@ __device__ __forceinline__ bool phase_moe(const DecodeArgs& A, DecodeLds& S, con
             S.sid[mine] = i;
             S.sv[mine] = S.lg[i];
         }
+        if (c.lane < 16 && i < E && mine == top) S.s9 = S.lg[i];
+        if (c.lane < 16 && i < E && mine == E - 1) S.slast = S.lg[i];
     }
     __syncthreads();
     QH_MARK(4, 5);
@@ -1020,6 +1025,9 @@ __device__ __forceinline__ bool phase_xr2(const DecodeArgs& A, DecodeLds& S, con
             A.a.wts[c.tid] = S.wts[c.tid];
             A.a.route_log[((size_t)c.pos * A.dm.layers + l) * c.top + c.tid] = S.ids[c.tid];
         }
+        if (c.tid == 0)
+            A.a.gap_log[(size_t)c.pos * A.dm.layers + l] =
+                (S.sv[c.top - 1] - S.s9) / fmaxf(fabsf(S.sv[0]), fabsf(S.slast));
         if (c.tid < c.E) A.a.logits_r[c.tid] = S.lg[c.tid];
     }
     return true;
@@ -1190,7 +1198,8 @@ __global__ __launch_bounds__(kDT) void k_decode(DecodeArgs A) {
     {
         // the launch's arguments, likewise (seven 64-byte lines, read
         // throughout every layer)
-        static_assert(sizeof(DecodeArgs) <= 448, "seven 64-byte lines");
+        static_assert(sizeof(DecodeArgs) >= 0x1b4 + 4 && sizeof(DecodeArgs) <= 448,
+                      "seven 64-byte lines, the last one holding offset 0x1b4");
         const auto* ka = (const __attribute__((address_space(4))) uint8_t*)__builtin_amdgcn_kernarg_segment_ptr();
         uint32_t d0, d1, d2, d3, d4, d5, d6, d7;
         asm volatile(

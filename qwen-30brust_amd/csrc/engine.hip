@@ -65,7 +65,7 @@ __global__ void k_pf_attn(const _Float16*, const _Float16*, const _Float16*, uin
 __global__ void k_pf_kvh(const float*, const float*, uint32_t, uint32_t, uint32_t, uint32_t, _Float16*, _Float16*);
 __global__ void k_pf_router(const float*, DevMat, uint32_t, uint32_t, uint32_t, float*);
 __global__ void k_pf_topk(const float*, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t*, float*, DevState*, uint32_t*,
-                          uint32_t, uint32_t, uint32_t);
+                          float*, uint32_t, uint32_t, uint32_t);
 __global__ void k_pf_group(const uint32_t*, uint32_t, uint32_t, uint32_t, uint32_t*, uint32_t*, uint32_t*, uint32_t*,
                            uint32_t*, uint32_t*);
 __global__ void k_pf_combine(float*, const float*, const float*, uint32_t, uint32_t, const float*, float, _Float16*);
@@ -415,6 +415,7 @@ void alloc_acts(qh_ctx* c) {
         {kMaxGrid * 4, (void**)&a.fin_idx},
         {pad32h(c->context + 2) * 4, (void**)&a.tokens},
         {(uint64_t)c->context * d.layers * d.top * 4, (void**)&a.route_log},
+        {(uint64_t)c->context * d.layers * 4, (void**)&a.gap_log},
         {256, (void**)&a.st},
     };
     size_t total = 0;
@@ -1064,7 +1065,8 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
     hipLaunchKernelGGL(k_pf_router, dim3((S + 63) / 64, kPfRouterSplit), dim3(kBlock), 0, c->s, P.Xn32, L.router,
                        S, H, d.experts, P.LR);
     hipLaunchKernelGGL(k_pf_topk, dim3((S + kWaves - 1) / kWaves), dim3(kBlock), 0, c->s, P.LR, kPfRouterSplit, S,
-                       d.experts, d.top, P.ids, P.wts, c->acts.st, c->acts.route_log, d.layers, (uint32_t)l, p0);
+                       d.experts, d.top, P.ids, P.wts, c->acts.st, c->acts.route_log, c->acts.gap_log, d.layers,
+                       (uint32_t)l, p0);
     hipLaunchKernelGGL(k_pf_group, dim3(1), dim3(1024), 0, c->s, P.ids, S * d.top, d.top, d.experts, P.goff, P.tok,
                        P.asg, P.te, P.tm, P.ntile);
     const ExpertTiles T{P.goff, P.tok, P.asg, P.te, P.tm, P.ntile};
@@ -1535,9 +1537,10 @@ int qh_argmax(qh_ctx* c, const float* logits, size_t n, uint32_t* out) {
 
 // Launch geometry of k_attention_api for `heads` query heads over T keys:
 // keys per chunk tc (the LDS budget), chunks nch, dynamic LDS bytes.
+constexpr size_t kAttnApiMaxChunks = 64;  // most key chunks per KV head of k_attention_api
 struct AttnGeo {
     size_t T;
-    uint32_t tc, nch;
+    uint32_t tc, nch, span;
     size_t lds;
 };
 AttnGeo attn_geometry(size_t klen, size_t heads, size_t kvheads, size_t d) {
@@ -1547,11 +1550,20 @@ AttnGeo attn_geometry(size_t klen, size_t heads, size_t kvheads, size_t d) {
     g.T = klen / (kvheads * d);
     if (g.T == 0) throw Error("empty KV cache");
     const uint32_t G = (uint32_t)(heads / kvheads);
-    auto lds = [&](uint32_t tc) { return (size_t)(G * d + tc * (d + 1) + tc * d + G * tc + 2 * G) * 4; };
+    auto lds = [&](uint32_t tc) { return (size_t)(2 * G * d + tc * (d + 1) + tc * d + G * tc + 3 * G) * 4; };
     g.tc = 64;
     while (g.tc > 1 && lds(g.tc) > 60 * 1024) g.tc /= 2;
     if (lds(g.tc) > 64 * 1024) throw Error("attention shape exceeds the LDS budget");
-    g.nch = (uint32_t)((g.T + g.tc - 1) / g.tc);
+    // at most kAttnApiMaxChunks chunks per KV head, fewer when one chunk's
+    // partials of every head would not fit the no-allocation scratch that
+    // many times: a chunk then takes several tiles (both entry points use
+    // this geometry, so they give the same bits)
+    const size_t tiles = (g.T + g.tc - 1) / g.tc, per_chunk = heads * (d + 2) * 4;
+    const size_t fit = (kNoAllocScratchBytes - 4096) / per_chunk;
+    const size_t cap = std::max<size_t>(1, std::min<size_t>(kAttnApiMaxChunks, fit));
+    const size_t span_tiles = (tiles + std::min(tiles, cap) - 1) / std::min(tiles, cap);
+    g.span = (uint32_t)(span_tiles * g.tc);
+    g.nch = (uint32_t)((g.T + g.span - 1) / g.span);
     g.lds = lds(g.tc);
     return g;
 }
@@ -1585,6 +1597,7 @@ int qh_attention(qh_ctx* c, const float* q, const float* k, const float* v, size
         a.d = (uint32_t)d;
         a.tc = tc;
         a.max_chunks = nch;
+        a.span = geo.span;
         a.part = dpart;
         a.counter = cnt;
         a.out = dout;
@@ -1623,6 +1636,7 @@ int qh_attention_noalloc(qh_ctx* c, const float* q, const float* k, const float*
         a.d = (uint32_t)d;
         a.tc = geo.tc;
         a.max_chunks = geo.nch;
+        a.span = geo.span;
         a.part = reinterpret_cast<float*>(base);
         a.counter = cnt;
         a.out = out;
@@ -1688,15 +1702,39 @@ int qh_generate(qh_ctx* c, const uint32_t* prompt, size_t n_prompt, size_t n_new
     });
 }
 
+static void prefill_body(qh_ctx* c, const uint32_t* prompt, size_t n, float* logits, size_t logits_cap,
+                         uint32_t* argmax, double t0);
+
 int qh_prefill(qh_ctx* c, const uint32_t* prompt, size_t n, float* logits, size_t logits_cap, uint32_t* argmax) {
     return guarded(c, [&] {
         double t0 = now_ms();
         need_model(c);
+        // the reference's prompt loop is one Model::forward per token
+        // (src/main.rs:250-256): the prompt fails at its first token that
+        // fails forward's checks (src/model.rs:219-223: the context limit,
+        // then the vocabulary), and any error leaves a clean cache
+        // (src/model.rs:209-216), here whatever failed
+        try {
+            prefill_body(c, prompt, n, logits, logits_cap, argmax, t0);
+        } catch (...) {
+            try {
+                reset_model(c);
+            } catch (...) {
+            }
+            throw;
+        }
+    });
+}
+
+static void prefill_body(qh_ctx* c, const uint32_t* prompt, size_t n, float* logits, size_t logits_cap,
+                         uint32_t* argmax, double t0) {
+    {
         need_logits_room(c, logits, logits_cap);
         if (n == 0) throw Error("empty prompt");
-        if (c->pos + n > c->context) throw Error("prompt + max-tokens exceed --ctx");
-        for (size_t i = 0; i < n; i++)
+        for (size_t i = 0; i < n; i++) {
+            if (c->pos + i >= c->context) throw Error("context limit " + std::to_string(c->context) + " reached");
             if (prompt[i] >= c->cfg.vocab) throw Error("token outside vocabulary");
+        }
         if (!prefill_gap(c).empty()) {
             // outside the batched path's coverage (formats, head_dim, ...):
             // the prompt runs through the exact token step, one per token, on
@@ -1747,7 +1785,7 @@ int qh_prefill(qh_ctx* c, const uint32_t* prompt, size_t n, float* logits, size_
         c->pos += n;
         c->stats.matvecs += matvecs_per_token(c) * n;
         c->stats.matvec_ms += now_ms() - t0;
-    });
+    }
 }
 
 int qh_reset(qh_ctx* c) {
@@ -1810,6 +1848,16 @@ int qh_route_log(qh_ctx* c, size_t pos0, size_t n, uint32_t* ids) {
         if (pos0 + n > c->context) throw Error("routing log range beyond the context");
         const size_t row = (size_t)c->dm.layers * c->dm.top;
         HIP_OK(hipMemcpyAsync(ids, c->acts.route_log + pos0 * row, n * row * 4, hipMemcpyDeviceToHost, c->s));
+        sync(c);
+    });
+}
+
+int qh_route_gap_log(qh_ctx* c, size_t pos0, size_t n, float* gaps) {
+    return guarded(c, [&] {
+        need_model(c);
+        if (pos0 + n > c->context) throw Error("routing log range beyond the context");
+        const size_t row = c->dm.layers;
+        HIP_OK(hipMemcpyAsync(gaps, c->acts.gap_log + pos0 * row, n * row * 4, hipMemcpyDeviceToHost, c->s));
         sync(c);
     });
 }

@@ -120,71 +120,95 @@ __global__ __launch_bounds__(kBlock) void k_argmax(const float* logits, uint32_t
 // ================================================================ attention ==
 // GQA causal attention for one query vector over T cached positions
 // (src/ops.rs:57-98).  Grid (kvheads, chunks); chunk c covers keys
-// [c*tc, min(T, (c+1)*tc)).  Element j of head g at time t lives at
+// [c*span, min(T, (c+1)*span)), taken in tiles of tc keys with an online
+// softmax (running max m, running sum l, exp-weighted V sum rescaled by
+// exp(m_old - m_new) per tile), so the chunk count, and with it the partial
+// buffer, stays bounded for any T.  Element j of head g at time t lives at
 // K[g*sh + t*st + j].  Each block computes, for the G = heads/kvheads query
-// heads of its KV head, the chunk's max score m, sum of exp(s - m) and the
-// exp-weighted V sum; the last block of each KV head merges the chunks.
-// Scores are (q . k) / sqrt(d), as the reference divides (ops.rs:87).
+// heads of its KV head, the chunk's (m, l, o); the last block of each KV
+// head merges the chunks.  Scores are (q . k) / sqrt(d), as the reference
+// divides (ops.rs:87).
 
 __device__ __forceinline__ void attention_block(const AttnArgs& a, uint32_t T) {
     extern __shared__ float4 smem4[];
     float* sm = reinterpret_cast<float*>(smem4);
     const uint32_t g = blockIdx.x, ch = blockIdx.y;
-    const uint32_t nch = (T + a.tc - 1) / a.tc;
+    const uint32_t span = a.span, nch = (T + span - 1) / span;
     if (nch > a.max_chunks || nch > gridDim.y) {  // never index past the partial buffer
         if (a.err && g == 0 && ch == 0 && threadIdx.x == 0) atomicOr(a.err, kErrContext);
         return;
     }
     if (ch >= nch) return;
     const uint32_t G = a.heads / a.kvheads, d = a.d, tc = a.tc;
-    const uint32_t t0 = ch * tc, n = min(T, t0 + tc) - t0;
+    const uint32_t k0 = ch * span, k1 = min(T, k0 + span);
     float* qs = sm;                    // [G][d]
     float* ks = qs + G * d;            // [tc][d+1]
     float* vs = ks + tc * (d + 1);     // [tc][d]
     float* ps = vs + tc * d;           // [G][tc]
-    float* ml = ps + G * tc;           // [G][2]
-    for (uint32_t i = threadIdx.x; i < G * d; i += kBlock) qs[i] = a.q[(g * G) * d + i];
-    for (uint32_t i = threadIdx.x; i < n * d; i += kBlock) {
-        uint32_t t = i / d, j = i % d;
-        size_t off = (size_t)g * a.sh + (size_t)(t0 + t) * a.st + j;
-        ks[t * (d + 1) + j] = a.k[off];
-        vs[t * d + j] = a.v[off];
+    float* ml = ps + G * tc;           // [G][2]  running max and sum
+    float* al = ml + 2 * G;            // [G]     rescale factor of the current tile
+    float* os = al + G;                // [G][d]  running exp-weighted V sum
+    for (uint32_t i = threadIdx.x; i < G * d; i += kBlock) {
+        qs[i] = a.q[(g * G) * d + i];
+        os[i] = 0.f;
     }
-    __syncthreads();
+    for (uint32_t h = threadIdx.x; h < G; h += kBlock) {
+        ml[2 * h] = -INFINITY;
+        ml[2 * h + 1] = 0.f;
+    }
     const float root = sqrtf((float)d);
-    for (uint32_t p = threadIdx.x; p < G * n; p += kBlock) {
-        uint32_t h = p / n, t = p % n;
-        const float* qh = qs + h * d;
-        const float* kt = ks + t * (d + 1);
-        float s = 0.f;
-        for (uint32_t j = 0; j < d; j++) s = fmaf(qh[j], kt[j], s);
-        ps[h * tc + t] = s / root;
-    }
-    __syncthreads();
     const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (uint32_t h = wv; h < G; h += kWaves) {
-        float m = -INFINITY;
-        for (uint32_t t = lane; t < n; t += 64) m = fmaxf(m, ps[h * tc + t]);
-        m = wave_max(m);
-        float l = 0.f;
-        for (uint32_t t = lane; t < n; t += 64) {
-            float e = expf(ps[h * tc + t] - m);
-            ps[h * tc + t] = e;
-            l += e;
+    for (uint32_t t0 = k0; t0 < k1; t0 += tc) {
+        const uint32_t n = min(k1, t0 + tc) - t0;
+        __syncthreads();  // the previous tile's readers are done
+        for (uint32_t i = threadIdx.x; i < n * d; i += kBlock) {
+            uint32_t t = i / d, j = i % d;
+            size_t off = (size_t)g * a.sh + (size_t)(t0 + t) * a.st + j;
+            ks[t * (d + 1) + j] = a.k[off];
+            vs[t * d + j] = a.v[off];
         }
-        l = wave_sum(l);
-        if (lane == 0) {
-            ml[2 * h] = m;
-            ml[2 * h + 1] = l;
+        __syncthreads();
+        for (uint32_t p = threadIdx.x; p < G * n; p += kBlock) {
+            uint32_t h = p / n, t = p % n;
+            const float* qh = qs + h * d;
+            const float* kt = ks + t * (d + 1);
+            float s = 0.f;
+            for (uint32_t j = 0; j < d; j++) s = fmaf(qh[j], kt[j], s);
+            ps[h * tc + t] = s / root;
+        }
+        __syncthreads();
+        for (uint32_t h = wv; h < G; h += kWaves) {
+            float mt = -INFINITY;
+            for (uint32_t t = lane; t < n; t += 64) mt = fmaxf(mt, ps[h * tc + t]);
+            const float mo = ml[2 * h], M = fmaxf(mo, wave_max(mt));
+            float l = 0.f;
+            for (uint32_t t = lane; t < n; t += 64) {
+                float e = expf(ps[h * tc + t] - M);
+                ps[h * tc + t] = e;
+                l += e;
+            }
+            l = wave_sum(l);
+            const float alpha = expf(mo - M);  // 0 on the first tile
+            if (lane == 0) {
+                ml[2 * h] = M;
+                ml[2 * h + 1] = fmaf(ml[2 * h + 1], alpha, l);
+                al[h] = alpha;
+            }
+        }
+        __syncthreads();
+        for (uint32_t p = threadIdx.x; p < G * d; p += kBlock) {
+            uint32_t h = p / d, j = p % d;
+            float o = os[p] * al[h];
+            for (uint32_t t = 0; t < n; t++) o = fmaf(ps[h * tc + t], vs[t * d + j], o);
+            os[p] = o;
         }
     }
-    __syncthreads();
+    // each thread writes the os entries it owns; ml was written before the
+    // last barrier
     for (uint32_t p = threadIdx.x; p < G * d; p += kBlock) {
         uint32_t h = p / d, j = p % d;
-        float o = 0.f;
-        for (uint32_t t = 0; t < n; t++) o = fmaf(ps[h * tc + t], vs[t * d + j], o);
         float* dst = a.part + ((size_t)(g * G + h) * a.max_chunks + ch) * (d + 2);
-        dst[2 + j] = o;
+        dst[2 + j] = os[p];
         if (j == 0) {
             dst[0] = ml[2 * h];
             dst[1] = ml[2 * h + 1];

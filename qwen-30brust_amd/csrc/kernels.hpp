@@ -111,6 +111,7 @@ struct Acts {
     uint32_t* fin_idx;   // [final blocks]
     uint32_t* tokens;    // [ctx+2]
     uint32_t* route_log; // [ctx][layers][top] routed experts of every layer at every position (diagnostics)
+    float* gap_log;      // [ctx][layers] (top-th - (top+1)-th router logit) / max |logit| (diagnostics)
     const float2* rope;  // [ctx][d/2] (cos, sin)
     DevState* st;
 };
@@ -122,6 +123,7 @@ struct AttnArgs {
     const float* v;
     size_t sh, st;      // element (t, g, j) at k[g*sh + t*st + j]
     uint32_t heads, kvheads, d, tc, max_chunks;
+    uint32_t span;      // keys per chunk (k_attention_api: whole tiles of tc)
     float* part;        // [heads][max_chunks][d+2]
     uint32_t* counter;  // [kvheads]
     float* out;         // [heads*d]

@@ -798,8 +798,8 @@ __global__ __launch_bounds__(kBlock) void k_pf_router(const float* Xn, DevMat R,
 // router's nks partial sums, added in split order.
 __global__ __launch_bounds__(kBlock) void k_pf_topk(const float* LR, uint32_t nks, uint32_t S, uint32_t E,
                                                     uint32_t top, uint32_t* ids, float* wts, DevState* st,
-                                                    uint32_t* route_log, uint32_t layers, uint32_t layer,
-                                                    uint32_t p0) {
+                                                    uint32_t* route_log, float* gap_log, uint32_t layers,
+                                                    uint32_t layer, uint32_t p0) {
     const uint32_t lane = threadIdx.x & 63, t = blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (t >= S) return;  // wave-uniform
     float v0 = lane < E ? LR[(size_t)t * E + lane] : 0.f, v1 = lane + 64 < E ? LR[(size_t)t * E + lane + 64] : 0.f;
@@ -830,6 +830,19 @@ __global__ __launch_bounds__(kBlock) void k_pf_topk(const float* LR, uint32_t nk
             sel = bi < 64 ? w0 : w1;
         }
     }
+    // the gap log: rank top's logit (the next pick) against rank top - 1's,
+    // relative to the largest |logit|
+    float gap = INFINITY;
+    {
+        int32_t bk = INT32_MIN;
+        uint32_t bi = 0xffffffffu;
+        if (!u0) best_merge(bk, bi, total_key(v0), lane);
+        if (!u1) best_merge(bk, bi, total_key(v1), lane + 64);
+        wave_best(bk, bi);
+        const float amax = wave_max(fmaxf(lane < E ? fabsf(v0) : 0.f, lane + 64 < E ? fabsf(v1) : 0.f));
+        const float last = __shfl(sel, top - 1, 64);
+        if (bi != 0xffffffffu) gap = (last - __shfl(bi < 64 ? v0 : v1, bi & 63, 64)) / amax;
+    }
     // softmax in rank order, sequential like ops.rs
     const float mx = wave_max(lane < top ? sel : -INFINITY);
     const float ex = lane < top ? expf(sel - mx) : 0.f;
@@ -843,6 +856,7 @@ __global__ __launch_bounds__(kBlock) void k_pf_topk(const float* LR, uint32_t nk
         wts[(size_t)t * top + lane] = ex / sum;
         route_log[((size_t)(p0 + t) * layers + layer) * top + lane] = sid;  // routing log (diagnostics)
     }
+    if (lane == 0) gap_log[(size_t)(p0 + t) * layers + layer] = gap;
 }
 
 // Groups the S*top (token, slot) assignments by expert (one workgroup):

@@ -882,8 +882,12 @@ __global__ __launch_bounds__(kGateupThreads) void k_gateup(LayerW L, Acts a, Mod
     float* sv = lg + E1;                                    // [top]
     uint32_t* sid = reinterpret_cast<uint32_t*>(sv + top);  // [top]
     __shared__ uint32_t bad;
+    __shared__ float s9, slast;  // logits of rank top and E - 1 (the gap log)
     QH_MARK(3, 0);
-    if (threadIdx.x == 0) bad = 0;
+    if (threadIdx.x == 0) {
+        bad = 0;
+        s9 = -INFINITY;  // stays when every expert is routed
+    }
     // 1. every load of the routing phase in one round.  Logit e (and the sum
     //    of squares, column E) is folded by the four threads (e, q): thread q
     //    sums partial rows [q*pq, q*pq + pq) in order, then the quarters are
@@ -953,8 +957,11 @@ __global__ __launch_bounds__(kGateupThreads) void k_gateup(LayerW L, Acts a, Mod
             sid[rank] = i;
             sv[rank] = lg[i];
         }
+        if (q == 0 && i < E && (uint32_t)rank == top) s9 = lg[i];
+        if (q == 0 && i < E && (uint32_t)rank == E - 1) slast = lg[i];
     }
     __syncthreads();
+    const float gap = (sv[top - 1] - s9) / fmaxf(fabsf(sv[0]), fabsf(slast));  // before the softmax rewrites sv
     if (bad) {
         if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(&a.st->err, kErrRouter);
         return;
@@ -987,6 +994,7 @@ __global__ __launch_bounds__(kGateupThreads) void k_gateup(LayerW L, Acts a, Mod
             a.wts[i] = sv[i];
             if (pos < dm.ctx) a.route_log[((size_t)pos * dm.layers + L.index) * top + i] = sid[i];
         }
+        if (threadIdx.x == 0 && pos < dm.ctx) a.gap_log[(size_t)pos * dm.layers + L.index] = gap;
         if (threadIdx.x < E) a.logits_r[threadIdx.x] = lv;
     }
     // 3. this workgroup's rows of its routed expert

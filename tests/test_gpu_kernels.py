@@ -254,7 +254,9 @@ def test_gqa_kat(dev):  # tests/core.rs:20-27
 
 
 @pytest.mark.parametrize("heads,kvh,d,t", [(4, 2, 4, 1), (8, 2, 16, 7), (32, 4, 128, 1025),
-                                           (32, 4, 128, 64), (2, 2, 8, 130), (16, 1, 64, 300)])
+                                           (32, 4, 128, 64), (2, 2, 8, 130), (16, 1, 64, 300),
+                                           # several key tiles per chunk (online softmax across tiles)
+                                           (32, 4, 128, 2049), (32, 4, 128, 8192), (64, 4, 128, 5000)])
 def test_attention_vs_oracle(dev, heads, kvh, d, t):
     rng = np.random.default_rng(heads * t + d)
     q = rng.standard_normal(heads * d).astype(np.float32)

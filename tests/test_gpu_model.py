@@ -228,6 +228,33 @@ def test_persistent_step_main_formats(dev, main, out):
         assert rel_err(xg, xr) <= REL
 
 
+@pytest.mark.parametrize("persistent", [True, False])
+def test_tied_vocab_projection(dev, persistent):
+    """A model without output.weight projects onto the vocabulary with
+    token_embd.weight (src/model.rs:290-294): two 30B-shaped layers, Q4_K
+    embedding, vocab 4096, through the persistent step and the per-phase
+    kernels; logits of five tokens within 1e-4 of the oracle's, the same greedy
+    ids, and the routing of every (position, layer) equal to the oracle's."""
+    t = synth._k_types(attn=synth.Q4_K, down=synth.Q4_K, out=synth.Q6_K, embd=synth.Q4_K)
+    spec = synth.Spec(2048, 2, 32, 4, 128, 128, 8, 768, 4096, 64, types=t, more_bits_type=synth.Q6_K,
+                      tied_output=True, seed=21)
+    img = synth.build_image(spec, threads=8)
+    g = oracle.Gguf(img)
+    with pytest.raises(oracle.OracleError):
+        g.tensor("output.weight")  # the image really has no output matrix
+    om = oracle.Model(g, spec.context)
+    m = engine.Model(img, spec.context, device=dev)
+    assert m.persistent
+    m.persistent = persistent
+    toks = [5, 4095, 77, 1024, 3]
+    for i, tok in enumerate(toks):
+        ref = om.forward(tok)
+        got = m.forward(tok)
+        assert rel_err(got, ref) <= REL
+        assert m.last_argmax == oracle.greedy(ref)
+        assert np.array_equal(np.sort(m.route_log(i, 1)[0], axis=1), np.sort(om.routes(), axis=1))
+
+
 def test_greedy_30b_token_loop_matches_oracle(dev):
     """Config 4 token loop: the random-init 48-layer Qwen3-30B-A3B Q4_K_M
     model, a 32-token uniform random prompt, then 64 greedy tokens chained on

@@ -3,8 +3,12 @@ flash attention in place of the reference's one-forward-per-token prompt
 loop, src/main.rs:250-256) against the FP32 oracle's sequential forward.
 fp16 operands cannot meet the decode path's 1e-4, so the bar is the logits
 of the last prompt token within 1e-2 (infinity-norm relative) and the same
-greedy id unless the oracle's top-1/top-2 margin is inside that tolerance;
-the decode steps that follow must stay within 2e-2."""
+greedy id unless the top-1/top-2 margin is inside that tolerance; the decode
+steps that follow must stay within 2e-2.  The fp16 router may pick another
+expert where the oracle's 8th/9th router logits nearly tie: every routing
+difference is counted and each token's first one attributed to such a
+near-tie, and the logits are compared with the oracle routed to the device's
+expert ids, so the bars hold whatever flipped."""
 import importlib
 import os
 
@@ -18,6 +22,7 @@ synth = importlib.import_module("qwen-30brust_amd.synth")
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-2
+NEAR_TIE = 1e-2  # 8th/9th router logit gap, relative to the largest |logit|, that fp16 noise may flip
 
 
 @pytest.fixture(scope="module")
@@ -39,36 +44,52 @@ def model2():
     return spec, img
 
 
-def router_gap(om, spec):
-    """Smallest relative gap between the top-th and (top+1)-th router logit
-    over the layers of the oracle's last forward: a gap inside the prefill's
-    fp16 noise lets the device pick another expert for that token."""
-    gaps = []
-    for layer in range(spec.layers):
-        r = np.sort(om.last_router(layer))[::-1]
-        gaps.append(float(r[spec.top - 1] - r[spec.top]) / float(np.max(np.abs(r))))
-    return min(gaps)
+def router_gap(logits, top):
+    """Gap between the top-th and (top+1)-th router logit, relative to the
+    largest |logit|: a decision whose gap sits inside the prefill's fp16
+    noise may legitimately go the other way."""
+    r = np.sort(logits)[::-1]
+    return float(r[top - 1] - r[top]) / float(np.max(np.abs(r)))
 
 
-def oracle_logits(spec, img, prompt, extra=()):
-    """Oracle logits after the prompt (and after each extra token), and the
-    last prompt token's smallest router gap."""
-    om = oracle.Model(oracle.Gguf(img), spec.context, threads=min(16, os.cpu_count() or 1))
-    for t in prompt:
-        ref = om.forward(int(t))
-    gap = router_gap(om, spec)
-    out = [ref]
-    for t in extra:
-        out.append(om.forward(int(t)))
-    return out, gap
+def oracle_runs(spec, img, tokens, dev_routes, n_prompt):
+    """The oracle over `tokens` twice: (1) routing by itself, recording its
+    expert ids and router gaps per (token, layer); (2) routed to the device's
+    expert ids (dev_routes[t], the reference's arithmetic with the device's
+    routing, so no routing difference is left).  Returns the logits of both
+    runs after the prompt and after each later token, the oracle's own routes
+    and gaps."""
+    threads = min(16, os.cpu_count() or 1)
+    own = oracle.Model(oracle.Gguf(img), spec.context, threads=threads)
+    forced = oracle.Model(oracle.Gguf(img), spec.context, threads=threads)
+    lo, lf, routes, gaps = [], [], [], []
+    for i, t in enumerate(tokens):
+        want = i >= n_prompt - 1
+        if want:
+            lo.append(own.forward(int(t)))
+            lf.append(forced.forward(int(t), routes=dev_routes[i]))
+        else:
+            own.step(int(t))
+            forced.step(int(t), routes=dev_routes[i])
+        routes.append(own.routes())
+        gaps.append([router_gap(own.last_router(l), spec.top) for l in range(spec.layers)])
+    return lo, lf, np.stack(routes), np.array(gaps)
 
 
-def check_logits(err, gap, tol=TOL):
-    """err within tol, or the last prompt token sits on a router near-tie
-    (relative gap below 2e-3), where a different expert choice is the fp16
-    path's legitimate outcome."""
-    if err > tol:
-        assert gap < 2e-3, f"rel err {err:.2e} without a router near-tie (smallest gap {gap:.2e})"
+def check_routing(dev_routes, ref_routes, gaps, label):
+    """Counts the (token, layer) decisions where the device chose another
+    expert set than the oracle and attributes each token's first such
+    difference to a near-tie of the oracle's router (later layers of that
+    token, and later tokens through the KV cache, inherit a changed input, so
+    only the first is attributable).  Returns the number of differences."""
+    n, layers = ref_routes.shape[:2]
+    dis = np.array([[set(dev_routes[t, l]) != set(ref_routes[t, l]) for l in range(layers)] for t in range(n)])
+    first = [(t, int(np.argmax(dis[t]))) for t in range(n) if dis[t].any()]
+    worst = max((gaps[t, l] for t, l in first), default=0.0)
+    print(f"{label}: {int(dis.sum())} of {dis.size} routing decisions differ from the oracle's, "
+          f"{len(first)} tokens; largest oracle gap at a first difference {worst:.2e}")
+    assert worst <= NEAR_TIE, f"a routing difference at gap {worst:.2e}, not a near-tie"
+    return int(dis.sum())
 
 
 def check_top1(got_id, ref):
@@ -79,27 +100,41 @@ def check_top1(got_id, ref):
     return margin
 
 
+def run_and_check(m, spec, img, prompt, extra, label, prior=()):
+    """The device prefills `prompt` (after `prior` tokens already run through
+    the exact step) and decodes `extra`; every routing difference from the
+    oracle is attributed to a near-tie, and the logits after the prompt
+    (bar TOL) and after each decode step (bar 2 TOL) are compared with the
+    oracle routed as the device was, whatever flipped.  The greedy id is
+    compared with the same run."""
+    am, lg = m.prefill(prompt)
+    assert m.position == len(prior) + len(prompt)
+    dec = [m.forward(int(t)) for t in extra]
+    tokens = list(prior) + list(prompt) + list(extra)
+    dev_routes = m.route_log(0, len(tokens))
+    n_prompt = len(prior) + len(prompt)
+    lo, lf, ref_routes, gaps = oracle_runs(spec, img, tokens, dev_routes, n_prompt)
+    check_routing(dev_routes, ref_routes, gaps, label)
+    err = rel_err(lg, lf[0])
+    margin = check_top1(am, lf[0])
+    print(f"{label}: last-token logits rel err {err:.2e} (vs the oracle's own routing {rel_err(lg, lo[0]):.2e}), "
+          f"top-1 margin {margin:.3e}")
+    assert err <= TOL
+    for i, (got, ref) in enumerate(zip(dec, lf[1:])):
+        e2 = rel_err(got, ref)
+        print(f"  decode step {i} after prefill: rel err {e2:.2e}")
+        assert e2 <= 2 * TOL
+
+
 @pytest.mark.parametrize("n", [1, 31, 32, 33, 64, 65, 100, 257])
 def test_prefill_matches_oracle(dev, model2, n):
     """Prompt lengths around the 32-query attention blocks and the 64-key
     blocks; then four decode steps on the prefilled KV cache."""
     spec, img = model2
     prompt = np.random.default_rng(n).integers(0, spec.vocab, n).astype(np.uint32)
-    extra = [7, 300, 11, 499]
-    refs, gap = oracle_logits(spec, img, prompt, extra)
     m = engine.Model(img, spec.context, device=dev)
     assert m.prefill_batched
-    am, lg = m.prefill(prompt)
-    err = rel_err(lg, refs[0])
-    margin = check_top1(am, refs[0])
-    print(f"n={n}: last-token logits rel err {err:.2e}, oracle top-1 margin {margin:.3e}, router gap {gap:.2e}")
-    check_logits(err, gap)
-    assert m.position == n
-    if err <= TOL:
-        for t, ref in zip(extra, refs[1:]):
-            e2 = rel_err(m.forward(t), ref)
-            print(f"  decode after prefill: rel err {e2:.2e}")
-            assert e2 <= 2 * TOL
+    run_and_check(m, spec, img, prompt, [7, 300, 11, 499], f"n={n}")
 
 
 @pytest.mark.parametrize("main,out", [(synth.Q4_0, synth.Q4_0), (synth.Q8_0, synth.Q8_0),
@@ -112,19 +147,9 @@ def test_prefill_main_formats(dev, main, out):
     spec = synth.Spec(2048, 2, 32, 4, 128, 128, 8, 768, 512, 512, types=t, more_bits_type=synth.Q6_K, seed=12)
     img = synth.build_image(spec, threads=min(16, os.cpu_count() or 1))
     prompt = np.random.default_rng(65).integers(0, spec.vocab, 65).astype(np.uint32)
-    extra = [7, 300]
-    refs, gap = oracle_logits(spec, img, prompt, extra)
     m = engine.Model(img, spec.context, device=dev)
     assert m.prefill_batched
-    am, lg = m.prefill(prompt)
-    err = rel_err(lg, refs[0])
-    margin = check_top1(am, refs[0])
-    print(f"kind {main}: last-token logits rel err {err:.2e}, oracle top-1 margin {margin:.3e}, router gap {gap:.2e}")
-    check_logits(err, gap)
-    assert m.position == len(prompt)
-    if err <= TOL:
-        for t, ref in zip(extra, refs[1:]):
-            assert rel_err(m.forward(t), ref) <= 2 * TOL
+    run_and_check(m, spec, img, prompt, [7, 300], f"kind {main}")
 
 
 def test_prefill_chunks_match_one_pass(dev, model2, monkeypatch):
@@ -132,14 +157,9 @@ def test_prefill_chunks_match_one_pass(dev, model2, monkeypatch):
     chunks) against the oracle."""
     spec, img = model2
     prompt = np.random.default_rng(150).integers(0, spec.vocab, 150).astype(np.uint32)
-    (ref,), gap = oracle_logits(spec, img, prompt)
     monkeypatch.setenv("QH_PREFILL_CHUNK", "64")
     m = engine.Model(img, spec.context, device=dev)
-    am, lg = m.prefill(prompt)
-    err = rel_err(lg, ref)
-    print(f"150 tokens in chunks of 64: rel err {err:.2e}, router gap {gap:.2e}")
-    check_logits(err, gap)
-    check_top1(am, ref)
+    run_and_check(m, spec, img, prompt, [5], "150 tokens in chunks of 64")
 
 
 def test_prefill_continues_a_sequence(dev, model2):
@@ -147,14 +167,10 @@ def test_prefill_continues_a_sequence(dev, model2):
     path, then 40 more batched."""
     spec, img = model2
     prompt = np.random.default_rng(60).integers(0, spec.vocab, 60).astype(np.uint32)
-    (ref,), gap = oracle_logits(spec, img, prompt)
     m = engine.Model(img, spec.context, device=dev)
     m.generate(prompt[:20], 0)
     assert m.position == 20
-    am, lg = m.prefill(prompt[20:])
-    assert m.position == 60
-    check_logits(rel_err(lg, ref), gap)
-    check_top1(am, ref)
+    run_and_check(m, spec, img, prompt[20:], [9], "20 + 40 tokens", prior=prompt[:20])
 
 
 def test_prefill_uncovered_model_runs_the_exact_step(dev):
@@ -194,3 +210,32 @@ def test_prefill_odd_query_width_runs_the_exact_step(dev):
         ref_lg = ref.forward(int(t))
     assert np.array_equal(lg, ref_lg)
     assert am == int(np.argmax(ref_lg))
+
+
+def test_prefill_errors_roll_back_like_forward(dev, model2):
+    """qh_prefill fails as the reference's loop of forwards would
+    (src/model.rs:209-223): the first prompt token past the context limit
+    gives "context limit N reached", a token outside the vocabulary "token
+    outside vocabulary" (also when a later token would overflow the context),
+    and every failure leaves a clean cache at position 0, so the next prefill
+    gives the bits of a first run."""
+    spec, img = model2
+    m = engine.Model(img, spec.context, device=dev)
+    prompt = np.random.default_rng(33).integers(0, spec.vocab, 33).astype(np.uint32)
+    am0, lg0 = m.prefill(prompt)
+    with pytest.raises(engine.EngineError, match=f"context limit {spec.context} reached"):
+        m.prefill(np.zeros(spec.context, np.uint32))  # 33 + 512 tokens
+    assert m.position == 0
+    bad = prompt.copy()
+    bad[5] = spec.vocab
+    with pytest.raises(engine.EngineError, match="token outside vocabulary"):
+        m.prefill(bad)
+    assert m.position == 0
+    over = np.zeros(spec.context + 1, np.uint32)
+    over[7] = spec.vocab  # the vocabulary check of token 7 comes before the overflow at token 512
+    with pytest.raises(engine.EngineError, match="token outside vocabulary"):
+        m.prefill(over)
+    assert m.position == 0
+    am1, lg1 = m.prefill(prompt)
+    assert am1 == am0 and np.array_equal(lg1, lg0)
+    assert m.position == len(prompt)

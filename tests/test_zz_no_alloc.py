@@ -2,8 +2,9 @@
 kernel's scratch in the library's fixed device array) against qh_attention
 (src/ops.rs:57-98 over host buffers) on the same inputs, through the C ABI:
 two calls in a row, the second with a smaller shape, bit-identical outputs
-(the same kernel and chunking); a shape whose scratch exceeds the array is
-refused; and a caller-supplied stream."""
+(the same kernel and chunking) at history lengths up to 20,000 keys; a
+shape whose scratch exceeds the array (one chunk's partials larger than it)
+is refused; and a caller-supplied stream."""
 import ctypes as C
 import importlib
 
@@ -89,12 +90,25 @@ def noalloc(dev, q, k, v, heads, kvheads, d, stream=None):
             b.free()
 
 
-@pytest.mark.parametrize("T,heads,kvheads,d", [(700, 32, 4, 128), (45, 8, 2, 64)])
+@pytest.mark.parametrize("T,heads,kvheads,d", [(700, 32, 4, 128), (45, 8, 2, 64), (8192, 32, 4, 128),
+                                               (20000, 32, 4, 128)])
 def test_noalloc_attention_equals_allocating_entry(dev, T, heads, kvheads, d):
+    """Bit-identical to qh_attention at any history length (long ones take
+    several key tiles per chunk, so the scratch stays within its array), and
+    within 1e-5 of a float64 restatement of ops.rs:57-98."""
     q, k, v = inputs(T, T, heads, kvheads, d)
     ref = dev.attention(q, k, v, heads, kvheads, d)
     got = noalloc(dev, q, k, v, heads, kvheads, d)
     assert np.array_equal(got, ref)
+    G = heads // kvheads
+    kk = k.reshape(T, kvheads, d).astype(np.float64)
+    vv = v.reshape(T, kvheads, d).astype(np.float64)
+    exp = np.empty((heads, d))
+    for h in range(heads):
+        s = kk[:, h // G, :] @ q[h * d:(h + 1) * d].astype(np.float64) / np.sqrt(d)
+        e = np.exp(s - s.max())
+        exp[h] = (e / e.sum()) @ vv[:, h // G, :]
+    assert np.max(np.abs(got.reshape(heads, d) - exp)) <= 1e-5 * np.max(np.abs(exp))
 
 
 def test_noalloc_two_calls_in_a_row_second_smaller(dev):
@@ -118,9 +132,10 @@ def test_noalloc_caller_stream(dev):
 
 
 def test_noalloc_refuses_shapes_beyond_its_scratch(dev):
-    q, k, v = inputs(31, 20000, 32, 4, 128)
+    # 2048 heads of 128: one chunk's partials alone exceed the 1 MiB array
+    q, k, v = inputs(31, 2, 2048, 2048, 128)
     with pytest.raises(engine.EngineError, match="bytes of scratch"):
-        noalloc(dev, q, k, v, 32, 4, 128)
+        noalloc(dev, q, k, v, 2048, 2048, 128)
     # the array is left in a usable state
     q, k, v = inputs(32, 64, 8, 2, 64)
     assert np.array_equal(noalloc(dev, q, k, v, 8, 2, 64), dev.attention(q, k, v, 8, 2, 64))
