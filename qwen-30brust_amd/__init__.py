@@ -25,7 +25,8 @@ import weakref
 import numpy as np
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG_DIR, "libqwen_hip.so")
+# QH_LIB selects another build of the engine library (same ABI)
+LIB_PATH = os.environ.get("QH_LIB") or os.path.join(PKG_DIR, "libqwen_hip.so")
 
 KINDS = {"F32": 0, "F16": 1, "Q4_0": 2, "Q8_0": 8, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
 

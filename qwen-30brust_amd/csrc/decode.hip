@@ -3,8 +3,14 @@
 // the embedding row of tokens[pos] (model.rs:225) included.
 //
 // Placement.  MI355X has 8 XCDs of 32 CUs, each XCD with its own L2, and the
-// dispatcher places workgroup b on XCD b % 8 (checked at set-up and again by
-// every workgroup at entry).  Workgroup b is (X, j) = (b % 8, b / 8).  Values
+// dispatcher hands workgroups to the XCDs in turn: workgroup b runs on XCD
+// (b + s) % 8, where the starting XCD s carries over from earlier dispatches
+// (0 for cooperative launches; checked at set-up for one launch).  Workgroup
+// b is (X, j) = (its XCD, read from the hardware register, b / 8): every XCD
+// then holds j = 0..31 once whatever s is.  (Were the order ever broken, some
+// (X, j) would be held twice and another not at all; the waits for the
+// missing one time out and the step fails with kErrSync, no value is wrong.)
+// Values
 // handed between the 32 workgroups of one XCD go through that XCD's L2
 // (plain stores, loads that skip L1: about 0.4 us per hand-over); values that
 // cross XCDs are written through to memory and read past the caches (about
@@ -1180,7 +1186,7 @@ __global__ __launch_bounds__(kDT) void k_decode(DecodeArgs A) {
     Ctx c;
     c.b = blockIdx.x;
     c.nwg = gridDim.x;
-    c.X = c.b % kNX;
+    c.X = xcc_id();  // wave-uniform (a scalar register)
     c.j = c.b / kNX;
     c.tid = threadIdx.x;
     c.lane = c.tid & 63;
@@ -1232,9 +1238,9 @@ __global__ __launch_bounds__(kDT) void k_decode(DecodeArgs A) {
         if (c.b == 0 && c.tid == 0) atomicOr(&A.a.st->err, kErrSync);
         return;
     }
-    if (xcc_id() != c.X) {
-        // the exchanges inside an XCD rely on the placement: give up, and
-        // make every other workgroup's waits end
+    if (c.X >= kNX) {
+        // the exchanges assume 8 XCDs: give up, and make every other
+        // workgroup's waits end
         if (c.tid == 0) {
             atomicOr(&A.a.st->err, kErrSync | kErrPlace);
             st_sys_u(A.abort_flag, 1u);

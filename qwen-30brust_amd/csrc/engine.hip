@@ -219,7 +219,7 @@ struct qh_ctx {
     hipGraphExec_t exec = nullptr;
     bool use_graph = true;  // QH_NO_GRAPH=1: launch the step's kernels directly (profilers)
 
-    // persistent token step (k_decode): one cooperative launch per token
+    // persistent token step (k_decode): one launch per token
     bool persist_ok = false;  // the model's formats and shapes are covered
     bool persist = false;     // and it is enabled (qh_set_persistent(0) disables it; QH_NO_PERSIST=1 at load leaves it out)
     uint32_t nwg = 0;         // workgroups of k_decode (one per CU)
@@ -589,26 +589,28 @@ const void* decode_kernel(uint32_t km) {
     }
 }
 
-// Whether workgroup b of a 256-workgroup launch runs on XCD b % 8 (read from
-// the hardware register by a probe kernel): the persistent step's exchanges
-// inside an XCD rely on it.
+// Whether the workgroups of a 256-workgroup launch go to the XCDs in turn,
+// workgroup b on XCD (b + s) % 8 for the launch's starting XCD s (read from the
+// hardware register by a probe kernel): the persistent step takes a
+// workgroup's place in its XCD, b / 8, from that order.
 bool xcd_placement_ok(qh_ctx* c, uint32_t nwg) {
     DevBuf m;
     m.alloc(nwg * 4);
     uint32_t* out = m.as<uint32_t>();
-    void* args[] = {&out};
-    HIP_OK(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_xcd_map), dim3(nwg), dim3(512), args, 0, c->s));
+    hipLaunchKernelGGL(k_xcd_map, dim3(nwg), dim3(512), 0, c->s, out);
+    HIP_OK(hipGetLastError());
     std::vector<uint32_t> h(nwg);
     HIP_OK(hipMemcpyAsync(h.data(), m.p, nwg * 4, hipMemcpyDeviceToHost, c->s));
     HIP_OK(hipStreamSynchronize(c->s));
+    const uint32_t s = h[0] % kDecodeXcds;
     for (uint32_t b = 0; b < nwg; b++)
-        if (h[b] != b % kDecodeXcds) return false;
+        if (h[b] != (b + s) % kDecodeXcds) return false;
     return true;
 }
 
 void setup_persist(qh_ctx* c) {
     // QH_NO_PERSIST=1: no persistent step for this context (no placement
-    // probe, no router folds), so no cooperative launch at all
+    // probe, no router folds)
     const char* np = std::getenv("QH_NO_PERSIST");
     if (np && np[0] == '1') {
         c->persist_ok = c->persist = false;
@@ -622,6 +624,13 @@ void setup_persist(qh_ctx* c) {
         return;
     }
     c->decode_fn = decode_kernel(c->layers[0].q.kind);
+    // one 512-thread workgroup per CU (nwg is the CU count), all resident at
+    // once: the launch is an ordinary one (a cooperative launch adds nothing
+    // here and left every profiled process failing in the profiler's exit
+    // path), so residency is checked here -- at least one workgroup fits a
+    // CU -- and at run time every wait of the step is bounded, so a
+    // workgroup that is not resident ends the step with "device
+    // synchronisation timed out" instead of a hang
     int per_cu = 0;
     HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, c->decode_fn, 512, 0));
     c->persist_ok = per_cu >= 1 && xcd_placement_ok(c, nwg);
@@ -692,8 +701,9 @@ void clear_words(qh_ctx* c, void* p, size_t bytes) {
     HIP_OK(hipGetLastError());
 }
 
-// One cooperative launch of k_decode over layers [l0, l1); vocab: also the
-// final norm, vocab projection, argmax and position advance.
+// One launch of k_decode over layers [l0, l1) (one workgroup per CU, all
+// resident: setup_persist checks it); vocab: also the final norm, vocab
+// projection, argmax and position advance.
 void launch_decode(qh_ctx* c, uint32_t l0, uint32_t l1, bool vocab, bool embed) {
     if (!(l0 < l1 && l1 <= c->layers.size())) throw Error("decode launch needs a non-empty layer range");
     const uint32_t phases = kDecodePhases * (l1 - l0) + (vocab ? 1 : 0);
@@ -711,8 +721,7 @@ void launch_decode(qh_ctx* c, uint32_t l0, uint32_t l1, bool vocab, bool embed) 
     A.embed = embed ? 1u : 0u;
     c->flag_base += phases;
     void* args[] = {&A};
-    HIP_OK(hipLaunchCooperativeKernel(c->decode_fn, dim3(c->nwg), dim3(512), args, 0,
-                                      c->s));
+    HIP_OK(hipLaunchKernel(c->decode_fn, dim3(c->nwg), dim3(512), args, 0, c->s));
 }
 
 // One token step: the captured graph, or the same kernels launched directly.
@@ -892,7 +901,7 @@ void reset_model(qh_ctx* c) {
         clear_words(c, c->acts.attn_cnt, pad32h(c->dm.kvheads) * 4);
     }
     reset_model(c);
-    if (err & kErrPlace) throw Error("persistent step: a workgroup ran on another XCD than expected");
+    if (err & kErrPlace) throw Error("persistent step: a workgroup ran on an unexpected XCD");
     if (err & kErrToken) throw Error("token outside vocabulary");
     if (err & kErrRouter) throw Error("invalid MoE router");
     if (err & kErrLogits) throw Error("nonfinite model output");

@@ -68,7 +68,7 @@ enum : uint32_t {
     kErrToken = 4u,    // token outside vocabulary (src/model.rs:222)
     kErrContext = 8u,  // position beyond the allocated context
     kErrSync = 16u,    // a cross-workgroup wait of the persistent step timed out (or was abandoned)
-    kErrPlace = 32u,   // a workgroup of the persistent step ran on another XCD than b % 8
+    kErrPlace = 32u,   // a workgroup of the persistent step ran on an XCD beyond the eight it assumes
 };
 
 struct LayerW {

@@ -61,12 +61,14 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--tokens", type=int, default=8)
     ap.add_argument("--split", action="store_true", help="attention workgroups and the others apart")
+    ap.add_argument("--lib", default=None, help="trace library to load (default: the in-tree trace build)")
     args = ap.parse_args()
     engine = importlib.import_module("qwen-30brust_amd")
     synth = importlib.import_module("qwen-30brust_amd.synth")
     from importlib import import_module
     build = import_module("qwen-30brust_amd.build")
-    engine.LIB_PATH = build.TRACE_SO
+    trace_so = os.path.abspath(args.lib) if args.lib else build.TRACE_SO
+    engine.LIB_PATH = trace_so
     spec = synth.qwen30b(layers=args.layers, context=max(4096, args.prompt + args.tokens + 8))
     img = synth.build_image(spec, threads=min(16, os.cpu_count() or 1))
     m = engine.Model(img, spec.context)
@@ -74,7 +76,7 @@ def main():
         raise SystemExit("the persistent step is not selected for this model")
     prompt = np.random.default_rng(1).integers(0, spec.vocab, args.prompt).astype(np.uint32)
     m.generate(prompt, 2)
-    lib = C.CDLL(build.TRACE_SO)
+    lib = C.CDLL(trace_so)
     buf = np.zeros((8, 512, 8), np.uint64)
     classes = ("all", "attention", "other") if args.split else ("all",)
     rows = {(mk, cl): [] for mk, _ in MARKS for cl in classes}

@@ -171,17 +171,18 @@ def test_layer_30b_shapes_at_pos_1024(dev, more_bits, persistent):
 
 @pytest.fixture(scope="module")
 def layer30b_q4k():
-    spec = synth.layer30b(more_bits=False)
+    spec = synth.layer30b(more_bits=False, context=4096)
     img = synth.build_image(spec, threads=8)
     return spec, img
 
 
-@pytest.mark.parametrize("pos", [0, 1, 63, 64, 65, 700, 1100, 2047])
+@pytest.mark.parametrize("pos", [0, 1, 63, 64, 65, 700, 1100, 2047, 3000, 4095])
 def test_persistent_layer_attention_chunking(dev, layer30b_q4k, pos):
     """The persistent step at positions that exercise the attention split: one
     key, one chunk, chunk boundaries (64-key tiles, at least 64 keys per
-    chunk), 11 chunks per KV head (one merge round), 18 (both halves of the
-    merging wave, two rounds) and 32 (the most); against the oracle layer."""
+    chunk), 11 and then 16 chunks per XCD (the most) of one tile or two, and
+    late in the context 16 chunks of several tiles each (3,001 keys: 188
+    each; 4,096: four whole tiles each); against the oracle layer."""
     spec, img = layer30b_q4k
     om = oracle.Model(oracle.Gguf(img), spec.context)
     m = engine.Model(img, spec.context, device=dev)
