@@ -216,6 +216,13 @@ int qh_prefill(qh_ctx *ctx, const uint32_t *prompt, size_t n, float *logits, siz
  * is one forward per token): *out = 1 when qh_prefill runs the loaded model's
  * prompts through the batched GEMM path, 0 when through the exact token step. */
 int qh_prefill_batched(const qh_ctx *ctx, int *out);
+/* Diagnostics (no reference counterpart): how many prompts the batched
+ * prefill has run again through the exact token step in this context because
+ * its fp16 operands could not hold them (an activation above 65504 in
+ * magnitude after an RMSNorm, in q, k or v, or out of the SwiGLU) or its
+ * router or output logits were not finite.  The rerun's results are the exact
+ * step's (the same bits as n qh_forward calls). */
+int qh_prefill_reruns(const qh_ctx *ctx, uint64_t *out);
 
 /* One decoder layer (the loop body src/model.rs:227-287) applied to x[hidden]
  * in place at position `pos`, with this layer's KV history replaced by

@@ -106,6 +106,7 @@ _SIGS = {
     "qh_fault_inject": (C.c_int, [C.c_void_p, C.c_uint32]),
     "qh_route_log": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
     "qh_route_gap_log": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
+    "qh_prefill_reruns": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint64)]),
     "qh_read_kv": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p]),
     "qh_profile_step": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]),
     "qh_bench_read": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p]),
@@ -473,6 +474,14 @@ class Model:
         v = C.c_int()
         self.dev._check(lib().qh_prefill_batched(self.dev.h, C.byref(v)))
         return bool(v.value)
+
+    @property
+    def prefill_reruns(self):
+        """Prompts the batched prefill ran again through the exact token step
+        (an fp16 operand out of range, or non-finite router/output logits)."""
+        v = C.c_uint64()
+        self.dev._check(lib().qh_prefill_reruns(self.dev.h, C.byref(v)))
+        return v.value
 
     @persistent.setter
     def persistent(self, enable):

@@ -52,14 +52,16 @@ bool launch_mv_stream(const DevMat&, const uint8_t* const*, uint32_t, const floa
 void launch_empty(hipStream_t);
 void launch_read_stream(const void*, size_t, uint32_t*, uint32_t, hipStream_t);
 // Batched prefill (prefill.hip).
-template <uint32_t K> __global__ void k_gemm_gateup(const _Float16*, uint32_t, ExpertTiles, DevMat, DevMat, _Float16*);
+template <uint32_t K>
+__global__ void k_gemm_gateup(const _Float16*, uint32_t, ExpertTiles, DevMat, DevMat, _Float16*, uint32_t*);
 template <uint32_t K> __global__ void k_gemm_down(const _Float16*, ExpertTiles, DevMat, float*);
 __global__ void k_gemm_dense(const _Float16*, uint32_t, DenseSegs, float*, uint32_t, size_t);
 __global__ void k_pf_embed(DevMat, const uint32_t*, uint32_t, uint32_t, float*, DevState*);
 __global__ void k_tile_gemm(DevMat, uint32_t, uint8_t*);
-__global__ void k_pf_norm(float*, const float*, uint32_t, float, _Float16*, float*, const float*, size_t);
+__global__ void k_pf_norm(float*, const float*, uint32_t, float, _Float16*, float*, const float*, size_t, uint32_t*);
 __global__ void k_pf_qkrope(const float*, const float*, const float*, const float2*, uint32_t, uint32_t, uint32_t,
-                            uint32_t, uint32_t, float, _Float16*, float*, float*, _Float16*, _Float16*, uint32_t);
+                            uint32_t, uint32_t, float, _Float16*, float*, float*, _Float16*, _Float16*, uint32_t,
+                            uint32_t*);
 __global__ void k_pf_attn(const _Float16*, const _Float16*, const _Float16*, uint32_t, uint32_t, uint32_t, uint32_t,
                           uint32_t, uint32_t, _Float16*);
 __global__ void k_pf_kvh(const float*, const float*, uint32_t, uint32_t, uint32_t, uint32_t, _Float16*, _Float16*);
@@ -68,7 +70,8 @@ __global__ void k_pf_topk(const float*, uint32_t, uint32_t, uint32_t, uint32_t, 
                           float*, uint32_t, uint32_t, uint32_t);
 __global__ void k_pf_group(const uint32_t*, uint32_t, uint32_t, uint32_t, uint32_t*, uint32_t*, uint32_t*, uint32_t*,
                            uint32_t*, uint32_t*);
-__global__ void k_pf_combine(float*, const float*, const float*, uint32_t, uint32_t, const float*, float, _Float16*);
+__global__ void k_pf_combine(float*, const float*, const float*, uint32_t, uint32_t, const float*, float, _Float16*,
+                             uint32_t*);
 }  // namespace qh
 
 using namespace qh;
@@ -223,6 +226,7 @@ struct qh_ctx {
     bool persist_ok = false;  // the model's formats and shapes are covered
     bool persist = false;     // and it is enabled (qh_set_persistent(0) disables it; QH_NO_PERSIST=1 at load leaves it out)
     uint32_t nwg = 0;         // workgroups of k_decode (one per CU)
+    uint64_t prefill_reruns = 0;  // prompts the batched prefill handed to the exact step (numeric faults)
     const void* decode_fn = nullptr;  // k_decode<KM> for the model's main format KM
     uint32_t flag_base = 0;   // tag of the last phase launched
     DevBuf layers_dev, sync_buf;  // sync_buf: abort flag and tagged exchange words
@@ -1052,9 +1056,10 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
     const ModelDims& d = c->dm;
     const LayerW& L = c->layers[l];
     const uint32_t H = d.hidden, qd = d.heads * 128, kvd = d.kvheads * 128, row = qd + 2 * kvd;
+    uint32_t* err = &c->acts.st->err;  // kErrRange: an fp16 operand out of range
     if (l == 0)  // later layers: written by the previous layer's combine
         hipLaunchKernelGGL(k_pf_norm, dim3(S), dim3(kBlock), 0, c->s, P.X, L.attn_norm, H, d.eps, P.Xn16,
-                           (float*)nullptr, (const float*)nullptr, (size_t)0);
+                           (float*)nullptr, (const float*)nullptr, (size_t)0, err);
     // q | k | v: one launch over the three quantised matrices, QKV[t] = [q | k | v]
     pf_dense(c, {{&L.q, 0u}, {&L.k, qd}, {&L.v, qd + kvd}}, P.Xn16, S, P.QKV, row);
     const uint32_t vp = (d.ctx + 63) / 64 * 64;  // row pitch of the transposed V copy
@@ -1062,7 +1067,7 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
         hipLaunchKernelGGL(k_pf_kvh, dim3(p0), dim3(kBlock), 0, c->s, L.kcache, L.vcache, 0u, d.kvheads, d.ctx, vp,
                            P.Kh, P.Vth);
     hipLaunchKernelGGL(k_pf_qkrope, dim3(S), dim3(kBlock), 0, c->s, P.QKV, L.q_norm, L.k_norm, c->acts.rope, p0, S,
-                       d.heads, d.kvheads, d.ctx, d.eps, P.Q16, L.kcache, L.vcache, P.Kh, P.Vth, vp);
+                       d.heads, d.kvheads, d.ctx, d.eps, P.Q16, L.kcache, L.vcache, P.Kh, P.Vth, vp, err);
     hipLaunchKernelGGL(k_pf_attn, dim3(((S + 15) / 16 + 1) / 2, d.kvheads), dim3(256), 0, c->s, P.Q16, P.Kh, P.Vth, p0, S,
                        d.heads / d.kvheads, d.ctx, vp, qd, P.O16);
     // o in two column halves (twice the workgroups) into Y's space; the norm
@@ -1070,7 +1075,7 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
     const size_t ostride = (size_t)S * H;
     pf_dense(c, {{&L.o, 0u}}, P.O16, S, P.Y, H, 2, ostride);
     hipLaunchKernelGGL(k_pf_norm, dim3(S), dim3(kBlock), 0, c->s, P.X, L.ffn_norm, H, d.eps, P.Xn16, P.Xn32,
-                       (const float*)P.Y, ostride);
+                       (const float*)P.Y, ostride, err);
     hipLaunchKernelGGL(k_pf_router, dim3((S + 63) / 64, kPfRouterSplit), dim3(kBlock), 0, c->s, P.Xn32, L.router,
                        S, H, d.experts, P.LR);
     hipLaunchKernelGGL(k_pf_topk, dim3((S + kWaves - 1) / kWaves), dim3(kBlock), 0, c->s, P.LR, kPfRouterSplit, S,
@@ -1082,7 +1087,7 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
     const uint32_t tiles = (S * d.top + 127) / 128 + d.experts;
     dispatch_km(L.gate.kind, [&](auto K) {
         hipLaunchKernelGGL(k_gemm_gateup<decltype(K)::value>, dim3(8 * ((tiles + 7) / 8) * ((d.ff + 127) / 128)), dim3(256), 0, c->s,
-                           P.Xn16, H, T, L.gate, L.up, P.Hs);
+                           P.Xn16, H, T, L.gate, L.up, P.Hs, err);
     });
     dispatch_km(L.down.kind, [&](auto K) {
         hipLaunchKernelGGL(k_gemm_down<decltype(K)::value>, dim3(8 * ((tiles + 7) / 8) * ((H + 127) / 128)), dim3(256), 0, c->s, P.Hs, T,
@@ -1091,7 +1096,7 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
     // + the next layer's attention RMSNorm (fp16 operand of its q|k|v GEMM)
     const float* next_norm = l + 1 < c->layers.size() ? c->layers[l + 1].attn_norm : nullptr;
     hipLaunchKernelGGL(k_pf_combine, dim3(S), dim3(kBlock), 0, c->s, P.X, P.Y, P.wts, H, d.top, next_norm, d.eps,
-                       P.Xn16);
+                       P.Xn16, err);
 }
 
 double now_ms() {
@@ -1744,10 +1749,9 @@ static void prefill_body(qh_ctx* c, const uint32_t* prompt, size_t n, float* log
             if (c->pos + i >= c->context) throw Error("context limit " + std::to_string(c->context) + " reached");
             if (prompt[i] >= c->cfg.vocab) throw Error("token outside vocabulary");
         }
-        if (!prefill_gap(c).empty()) {
-            // outside the batched path's coverage (formats, head_dim, ...):
-            // the prompt runs through the exact token step, one per token, on
-            // the device, as the reference's prompt loop does (src/main.rs:250-256)
+        // the prompt through the exact token step, one per token, on the
+        // device, as the reference's prompt loop does (src/main.rs:250-256)
+        auto run_exact = [&] {
             HIP_OK(hipMemcpyAsync(c->acts.tokens + c->pos, prompt, n * 4, hipMemcpyHostToDevice, c->s));
             put_state(c, (uint32_t)c->pos, (uint32_t)(c->pos + n));
             for (size_t i = 0; i < n; i++) launch_step(c);
@@ -1759,6 +1763,9 @@ static void prefill_body(qh_ctx* c, const uint32_t* prompt, size_t n, float* log
             c->pos += n;
             c->stats.matvecs += matvecs_per_token(c) * n;
             c->stats.matvec_ms += now_ms() - t0;
+        };
+        if (!prefill_gap(c).empty()) {  // outside the batched path's coverage (formats, head_dim, ...)
+            run_exact();
             return;
         }
         prefill_tiles(c);
@@ -1787,7 +1794,16 @@ static void prefill_body(qh_ctx* c, const uint32_t* prompt, size_t n, float* log
         enqueue_tail(c);
         HIP_OK(hipGetLastError());
         DevState st = get_state(c);
-        if (st.err) fail_step(c, st.err);
+        if (st.err) {
+            // the prompt's tokens and positions were checked above, so this is
+            // numeric: an fp16 operand out of range (kErrRange), or router
+            // logits or output logits that are not finite.  The exact FP32
+            // step runs the prompt again from the same position (it rewrites
+            // every KV row the batched pass wrote); its own errors are final.
+            c->prefill_reruns++;
+            run_exact();
+            return;
+        }
         if (logits) HIP_OK(hipMemcpyAsync(logits, c->acts.logits, c->cfg.vocab * 4, hipMemcpyDeviceToHost, c->s));
         sync(c);
         if (argmax) *argmax = st.argmax;
@@ -1795,6 +1811,11 @@ static void prefill_body(qh_ctx* c, const uint32_t* prompt, size_t n, float* log
         c->stats.matvecs += matvecs_per_token(c) * n;
         c->stats.matvec_ms += now_ms() - t0;
     }
+}
+
+int qh_prefill_reruns(const qh_ctx* c, uint64_t* out) {
+    *out = c->prefill_reruns;
+    return 0;
 }
 
 int qh_reset(qh_ctx* c) {

@@ -69,6 +69,7 @@ enum : uint32_t {
     kErrContext = 8u,  // position beyond the allocated context
     kErrSync = 16u,    // a cross-workgroup wait of the persistent step timed out (or was abandoned)
     kErrPlace = 32u,   // a workgroup of the persistent step ran on an XCD beyond the eight it assumes
+    kErrRange = 64u,   // a batched-prefill activation outside the fp16 range (the prompt reruns exactly)
 };
 
 struct LayerW {

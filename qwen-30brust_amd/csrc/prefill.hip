@@ -21,6 +21,17 @@
 namespace qh {
 
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+
+// fp16 of an activation, noting a value outside the fp16 range (|v| > 65504,
+// or not finite) in bad; a thread that saw one raises kErrRange once, and
+// the engine runs that prompt again through the exact FP32 token step.
+__device__ __forceinline__ _Float16 to_h(float v, bool& bad) {
+    bad |= !(fabsf(v) <= 65504.f);
+    return (_Float16)v;
+}
+__device__ __forceinline__ void note_range(bool bad, uint32_t* err) {
+    if (bad) atomicOr(err, kErrRange);
+}
 typedef float f4v __attribute__((ext_vector_type(4)));
 
 constexpr int kGM = 128, kGN = 128, kGK = 64, kGT = 256;
@@ -377,7 +388,7 @@ __device__ __forceinline__ void xcd_tile(uint32_t nn, uint32_t& t, uint32_t& n) 
 // Hs[goff[e] + r][n] = silu(g) * u, fp16, for the sorted assignments.
 template <uint32_t KIND>
 __global__ __launch_bounds__(kGT, 2) void k_gemm_gateup(const _Float16* Xn, uint32_t H, ExpertTiles G, DevMat Wg, DevMat Wu,
-                                                     _Float16* Hs) {
+                                                     _Float16* Hs, uint32_t* err) {
     __shared__ __align__(16) _Float16 smem[kRA];
     uint32_t ty, tx;
     xcd_tile((Wg.rows + kGN - 1) / kGN, ty, tx);
@@ -402,6 +413,7 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_gateup(const _Float16* Xn, uint
     // tiles) multiplies two row blocks, not four
     gemm_tile_r<KIND, 2, 2>(arows, wblk, Wg.cols, acc, smem, 0, rows - mt0 > 64);
     const uint32_t n = n0 + racc_col();
+    bool bad = false;
 #pragma unroll
     for (int mb = 0; mb < 4; mb++)
 #pragma unroll
@@ -410,9 +422,10 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_gateup(const _Float16* Xn, uint
             if (m < rows && n < ff) {
 #pragma clang fp contract(off)
                 const float gv = acc[0][mb][i], uv = acc[1][mb][i];
-                Hs[(size_t)(base + m) * ff + n] = (_Float16)((gv / (1.f + expf(-gv))) * uv);
+                Hs[(size_t)(base + m) * ff + n] = to_h((gv / (1.f + expf(-gv))) * uv, bad);
             }
         }
+    note_range(bad, err);
 }
 
 // down of the routed experts: Y[asg][n] = Hs[goff[e] + r] . Wd_e[n].
@@ -603,7 +616,8 @@ __global__ __launch_bounds__(kBlock) void k_pf_embed(DevMat emb, const uint32_t*
 // With P: first X[t] += P[0][t] + P[1][t] (the two column halves of the
 // o-projection: the residual add of model.rs:246-248, in that order).
 __global__ __launch_bounds__(kBlock) void k_pf_norm(float* X, const float* w, uint32_t H, float eps,
-                                                    _Float16* Y16, float* Y32, const float* P, size_t pstride) {
+                                                    _Float16* Y16, float* Y32, const float* P, size_t pstride,
+                                                    uint32_t* err) {
     __shared__ float red[kWaves];
     const size_t t = blockIdx.x;
     float* x = X + t * H;
@@ -629,17 +643,19 @@ __global__ __launch_bounds__(kBlock) void k_pf_norm(float* X, const float* w, ui
         ss = fmaf(v.w, v.w, ss);
     }
     const float scale = 1.0f / sqrtf(block_sum(ss, red) / (float)H + eps);
+    bool bad = false;
     for (uint32_t i4 = threadIdx.x; 4 * i4 < H; i4 += kBlock) {
         const float4 v = reinterpret_cast<const float4*>(x)[i4], w4 = reinterpret_cast<const float4*>(w)[i4];
         const float4 y = make_float4(v.x * (scale * w4.x), v.y * (scale * w4.y), v.z * (scale * w4.z),
                                      v.w * (scale * w4.w));
         _Float16* o = Y16 + t * H + 4 * i4;
-        o[0] = (_Float16)y.x;
-        o[1] = (_Float16)y.y;
-        o[2] = (_Float16)y.z;
-        o[3] = (_Float16)y.w;
+        o[0] = to_h(y.x, bad);
+        o[1] = to_h(y.y, bad);
+        o[2] = to_h(y.z, bad);
+        o[3] = to_h(y.w, bad);
         if (Y32) reinterpret_cast<float4*>(Y32 + t * H)[i4] = y;
     }
+    note_range(bad, err);
 }
 
 // Q/K RMSNorm per head (model.rs:233-238), NeoX RoPE at position p0 + t
@@ -652,7 +668,7 @@ __global__ __launch_bounds__(kBlock) void k_pf_qkrope(const float* QKV, const fl
                                                       const float2* rope, uint32_t p0, uint32_t S, uint32_t heads,
                                                       uint32_t kvheads, uint32_t ctx, float eps, _Float16* Q16,
                                                       float* kcache, float* vcache, _Float16* Kh, _Float16* Vth,
-                                                      uint32_t vp) {
+                                                      uint32_t vp, uint32_t* err) {
     const uint32_t t = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6, pos = p0 + t;
     const uint32_t row = (heads + 2 * kvheads) * 128;
     const float* x = QKV + (size_t)t * row;
@@ -660,6 +676,7 @@ __global__ __launch_bounds__(kBlock) void k_pf_qkrope(const float* QKV, const fl
     const uint32_t nslot = heads + 2 * kvheads;
     const float qw0 = qn[lane], qw1 = qn[lane + 64], kw0 = kn[lane], kw1 = kn[lane + 64];
     constexpr uint32_t kSW = 5;  // slots per wave per round, their loads issued together
+    bool bad = false;
     for (uint32_t s0 = w; s0 < nslot; s0 += kSW * kWaves) {  // wave-uniform
         float xa_[kSW], xb_[kSW];
 #pragma unroll
@@ -678,8 +695,8 @@ __global__ __launch_bounds__(kBlock) void k_pf_qkrope(const float* QKV, const fl
                 float* dst = vcache + ((size_t)g * ctx + pos) * 128;
                 dst[lane] = xa;
                 dst[lane + 64] = xb;
-                Vth[((size_t)g * 128 + lane) * vp + pos] = (_Float16)xa;
-                Vth[((size_t)g * 128 + lane + 64) * vp + pos] = (_Float16)xb;
+                Vth[((size_t)g * 128 + lane) * vp + pos] = to_h(xa, bad);
+                Vth[((size_t)g * 128 + lane + 64) * vp + pos] = to_h(xb, bad);
                 continue;
             }
             const bool isq = slot < heads;
@@ -695,18 +712,19 @@ __global__ __launch_bounds__(kBlock) void k_pf_qkrope(const float* QKV, const fl
             }
             if (isq) {
                 _Float16* dst = Q16 + ((size_t)slot * S + t) * 128;
-                dst[lane] = (_Float16)o0;
-                dst[lane + 64] = (_Float16)o1;
+                dst[lane] = to_h(o0, bad);
+                dst[lane + 64] = to_h(o1, bad);
             } else {
                 float* dst = kcache + ((size_t)(slot - heads) * ctx + pos) * 128;
                 dst[lane] = o0;
                 dst[lane + 64] = o1;
                 _Float16* dh = Kh + ((size_t)(slot - heads) * ctx + pos) * 128;
-                dh[lane] = (_Float16)o0;
-                dh[lane + 64] = (_Float16)o1;
+                dh[lane] = to_h(o0, bad);
+                dh[lane + 64] = to_h(o1, bad);
             }
         }
     }
+    note_range(bad, err);
 }
 
 // Router logits (model.rs:249-256) in fp32 on the matrix cores
@@ -974,7 +992,8 @@ __device__ __forceinline__ float4 ld4s(const float* p) {
 }
 
 __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y, const float* wts, uint32_t H,
-                                                       uint32_t top, const float* nw, float eps, _Float16* Xn16) {
+                                                       uint32_t top, const float* nw, float eps, _Float16* Xn16,
+                                                       uint32_t* err) {
     __shared__ float red[kWaves];
     const size_t t = blockIdx.x;
     const uint32_t tk = min(top, 8u);  // ranks held in registers; more (top > 8) are read in a loop
@@ -1022,16 +1041,18 @@ __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y,
     }
     if (!nw) return;  // uniform
     const float scale = 1.0f / sqrtf(block_sum(ss, red) / (float)H + eps);
+    bool bad = false;
     for (uint32_t i4 = threadIdx.x; 4 * i4 < H; i4 += kBlock) {  // this thread's own x values
         const size_t i = 4 * (size_t)i4;
         const float4 xv = *reinterpret_cast<const float4*>(X + t * H + i);
         const float4 w4 = *reinterpret_cast<const float4*>(nw + i);
         _Float16* o = Xn16 + t * H + i;
-        o[0] = (_Float16)(xv.x * (scale * w4.x));
-        o[1] = (_Float16)(xv.y * (scale * w4.y));
-        o[2] = (_Float16)(xv.z * (scale * w4.z));
-        o[3] = (_Float16)(xv.w * (scale * w4.w));
+        o[0] = to_h(xv.x * (scale * w4.x), bad);
+        o[1] = to_h(xv.y * (scale * w4.y), bad);
+        o[2] = to_h(xv.z * (scale * w4.z), bad);
+        o[3] = to_h(xv.w * (scale * w4.w), bad);
     }
+    note_range(bad, err);
 }
 
 // ----------------------------------------------------------- attention --
@@ -1272,7 +1293,8 @@ __global__ __launch_bounds__(kBlock) void k_pf_kvh(const float* kcache, const fl
 }
 
 #define QH_INSTANTIATE_PREFILL_GEMM(K)                                                                          \
-    template __global__ void k_gemm_gateup<K>(const _Float16*, uint32_t, ExpertTiles, DevMat, DevMat, _Float16*);     \
+    template __global__ void k_gemm_gateup<K>(const _Float16*, uint32_t, ExpertTiles, DevMat, DevMat, _Float16*,      \
+                                              uint32_t*);                                                           \
     template __global__ void k_gemm_down<K>(const _Float16*, ExpertTiles, DevMat, float*);                          \
 
 QH_INSTANTIATE_PREFILL_GEMM(Q4_0)

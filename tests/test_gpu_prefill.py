@@ -109,6 +109,7 @@ def run_and_check(m, spec, img, prompt, extra, label, prior=()):
     compared with the same run."""
     am, lg = m.prefill(prompt)
     assert m.position == len(prior) + len(prompt)
+    assert m.prefill_reruns == 0  # the batched path's fp16 operands held every activation
     dec = [m.forward(int(t)) for t in extra]
     tokens = list(prior) + list(prompt) + list(extra)
     dev_routes = m.route_log(0, len(tokens))
@@ -239,3 +240,30 @@ def test_prefill_errors_roll_back_like_forward(dev, model2):
     am1, lg1 = m.prefill(prompt)
     assert am1 == am0 and np.array_equal(lg1, lg0)
     assert m.position == len(prompt)
+
+
+def test_prefill_beyond_fp16_range_reruns_exactly(dev):
+    """RMSNorm weights of 4e4 put the normalised activations far beyond the
+    fp16 range of the batched path's operands (|x| <= 65504): the prefill
+    notices (an fp16 range flag at every activation it converts), runs the
+    prompt again through the exact FP32 token step and counts it, so the
+    logits, the greedy id and the decode step that follows equal a stepwise
+    forward bit for bit."""
+    t = synth._k_types(attn=12, down=12, out=14, embd=12)
+    spec = synth.Spec(2048, 2, 32, 4, 128, 128, 8, 768, 512, 64, types=t, more_bits_type=14, seed=13,
+                      norm_mean=4e4)
+    img = synth.build_image(spec, threads=min(16, os.cpu_count() or 1))
+    prompt = np.random.default_rng(21).integers(0, spec.vocab, 21).astype(np.uint32)
+    m = engine.Model(img, spec.context, device=dev)
+    assert m.prefill_batched and m.prefill_reruns == 0
+    am, lg = m.prefill(prompt)
+    assert m.prefill_reruns == 1
+    assert m.position == len(prompt)
+    assert np.all(np.isfinite(lg)) and float(np.max(np.abs(lg))) > 0
+    nxt = m.forward(am)
+    ref = engine.Model(img, spec.context, device=dev)  # replaces m on this device
+    for tok in prompt:
+        ref_lg = ref.forward(int(tok))
+    assert np.array_equal(lg, ref_lg)
+    assert am == int(np.argmax(ref_lg))
+    assert np.array_equal(nxt, ref.forward(am))
