@@ -82,6 +82,29 @@ __device__ __forceinline__ typename Fmt<KIND>::Raw bload(__amdgpu_buffer_rsrc_t 
     }
 }
 
+// The same bytes for a wave-uniform row offset ro: ro and the field offset go
+// in the scalar offset, the lane's chunk offset in the vector offset (which
+// then stays the same from row to row).
+template <uint32_t KIND>
+__device__ __forceinline__ typename Fmt<KIND>::Raw bload_u(__amdgpu_buffer_rsrc_t r, uint32_t ro, const RowGeo& g,
+                                                           uint32_t c) {
+    const uint32_t b = c >> 3, j = c & 7;
+    if constexpr (KIND == Q4_K) {
+        return {bld16(r, b * 128 + j * 16, ro + g.off_b), bld16(r, b * 16, ro + g.off_a)};
+    } else if constexpr (KIND == Q5_K) {
+        return {bld16(r, b * 128 + j * 16, ro + g.off_c), bld16(r, b * 16, ro + g.off_a),
+                bld16(r, b * 32 + (j & 1) * 16, ro + g.off_b)};
+    } else if constexpr (KIND == Q6_K) {
+        return {bld16(r, b * 128 + j * 16, ro + g.off_a), bld16(r, b * 64 + (j >> 2) * 32 + (j & 1) * 16, ro + g.off_b),
+                bld8(r, b * 16 + (j >> 2) * 8, ro + g.off_c), bld4(r, (b >> 1) * 4, ro + g.off_d)};
+    } else if constexpr (KIND == Q4_0) {
+        return {bld16(r, c * 16, ro + g.off_a), bld4(r, (c >> 1) * 4, ro + g.off_b)};
+    } else {
+        static_assert(KIND == Q8_0, "block-quantised formats only");
+        return {bld16(r, c * 32, ro + g.off_a), bld16(r, c * 32 + 16, ro + g.off_a), bld4(r, (c >> 1) * 4, ro + g.off_b)};
+    }
+}
+
 // The two 16-float runs of chunk c of the padded LDS vector that starts at
 // element `base` (their sums come precomputed).
 template <uint32_t KIND>
@@ -96,7 +119,13 @@ __device__ __forceinline__ void x_runs_only(const float* xs, uint32_t base, uint
     }
 }
 
-template <uint32_t KIND, int C, int R, int NT>
+// FULL: one vector whose rows are exactly 64 C chunks (L = 64 lanes per
+// row): every lane takes chunks lane, lane + 64, ..., a wave's rows are
+// wave-uniform (their offsets in scalar registers), and no chunk is idle, so
+// the group, row and chunk arithmetic of the general form (the lane layout is
+// a launch argument there) leaves the vector ALU.  The vocab projection
+// (2,048 columns) and the 4,096-column o-projection take it.
+template <uint32_t KIND, int C, int R, int NT, bool FULL>
 __global__ __launch_bounds__(NT) void k_mv_stream(MvArgs a) {
     constexpr int NW = NT / 64, XV = mv_xv<NT>();
     extern __shared__ float4 smem4[];
@@ -106,36 +135,56 @@ __global__ __launch_bounds__(NT) void k_mv_stream(MvArgs a) {
     const DevMat& m = a.m;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t L = 1u << a.lshift, S = 64u >> a.lshift, sub = lane >> a.lshift, cl = lane & (L - 1);
+    const uint32_t lsh = FULL ? 6u : a.lshift;
+    const uint32_t L = 1u << lsh, S = 64u >> lsh, sub = FULL ? 0u : lane >> lsh, cl = FULL ? lane : lane & (L - 1);
     const uint32_t cpr = m.cols / 32, rpg = R * S;
-    const uint32_t ngrp = a.nb * a.gpb;
+    const uint32_t ngrp = FULL ? a.gpb : a.nb * a.gpb;
     const uint32_t g0 = min(blockIdx.x * a.per, ngrp), g1 = min(g0 + a.per, ngrp);
     if (g0 >= g1) return;  // the whole workgroup
 
     const uint32_t mbytes = m.rows * m.drb;  // < 2^32 (checked by the host)
+    // vector b and row group rg of group g (FULL: one vector)
+    auto split = [&](uint32_t g, uint32_t& b, uint32_t& rg) {
+        if constexpr (FULL) {
+            b = 0;
+            rg = g;
+        } else {
+            b = g / a.gpb;
+            rg = g - b * a.gpb;
+        }
+    };
     auto load_group = [&](Raw (&t)[R][C], uint32_t g) {
-        const uint32_t b = g / a.gpb, rg = g - b * a.gpb;
+        uint32_t b, rg;
+        split(g, b, rg);
         // a select chain, so that the argument array stays in scalar registers
         const uint8_t* base = a.mat[0];
+        if constexpr (!FULL) {
 #pragma unroll
-        for (uint32_t j = 1; j < kMvMaxVec; j++) base = b == j ? a.mat[j] : base;
+            for (uint32_t j = 1; j < kMvMaxVec; j++) base = b == j ? a.mat[j] : base;
+        }
         const __amdgpu_buffer_rsrc_t rs = buf_rsrc(base, mbytes);
 #pragma unroll
         for (int k = 0; k < R; k++) {
             const uint32_t ro = min(rg * rpg + sub + k * S, m.rows - 1) * m.drb;
 #pragma unroll
-            for (int i = 0; i < C; i++) t[k][i] = bload<KIND>(rs, ro, m.geo, min(cl + i * L, cpr - 1));
+            for (int i = 0; i < C; i++) {
+                if constexpr (FULL)
+                    t[k][i] = bload_u<KIND>(rs, __builtin_amdgcn_readfirstlane(ro), m.geo, cl + i * L);
+                else
+                    t[k][i] = bload<KIND>(rs, ro, m.geo, min(cl + i * L, cpr - 1));
+            }
         }
     };
     auto reduce_store = [&](const Raw (&t)[R][C], uint32_t g) {
-        const uint32_t b = g / a.gpb, rg = g - b * a.gpb;
+        uint32_t b, rg;
+        split(g, b, rg);
         float acc[R];
 #pragma unroll
         for (int k = 0; k < R; k++) acc[k] = 0.f;
 #pragma unroll
         for (int i = 0; i < C; i++) {
             const uint32_t ch = cl + i * L;
-            if (ch < cpr) {
+            if (FULL || ch < cpr) {
                 float xa[16], xb[16];
                 x_runs_only<KIND>(xs, b * a.xpitch, ch, xa, xb);
                 const float2 s2 = xsum[b * cpr + ch];
@@ -253,6 +302,25 @@ MvShape mv_shape(uint32_t cpr, uint64_t rows, uint32_t nb, uint32_t waves) {
 // workgroup waits for a slot behind another's whole row range.  The 64-thread
 // form: one workgroup per group up to 8 per CU, for matrices too small to
 // give every CU eight groups (the per-CU request rate, not HBM, bounds those).
+// The 512-thread form of k_mv_stream<K, C, R, FULL>: one resident wave of
+// workgroups (residency asked once per kernel, at the largest x it stages).
+template <uint32_t K, int C, int R, bool FULL>
+void launch_512(MvArgs a, uint64_t ngrp, uint32_t ncu, size_t smem, hipStream_t st) {
+    static const int per_cu = [] {
+        int n = 0;
+        const size_t most = (size_t)(kMvMaxXFloats + 4 * (kMvMaxXFloats / 64) + 2 * kMvMaxXFloats / 32) * 4;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_mv_stream<K, C, R, kMvT, FULL>, kMvT, most) !=
+            hipSuccess)
+            n = 1;
+        return std::max(n, 1);
+    }();
+    const uint64_t max_wg = (uint64_t)std::min(per_cu, 3) * ncu;
+    const uint32_t grid = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(max_wg, (ngrp + kMvW - 1) / kMvW));
+    a.per = (uint32_t)((ngrp + grid - 1) / grid);
+    a.single = a.per <= (uint32_t)kMvW;
+    hipLaunchKernelGGL((k_mv_stream<K, C, R, kMvT, FULL>), dim3(grid), dim3(kMvT), smem, st, a);
+}
+
 template <uint32_t K, int C, int R>
 void launch_one(MvArgs a, uint64_t ngrp, uint32_t num_cu, size_t smem, hipStream_t st) {
     const uint32_t ncu = std::max(num_cu, 1u);
@@ -261,22 +329,14 @@ void launch_one(MvArgs a, uint64_t ngrp, uint32_t num_cu, size_t smem, hipStream
         const uint32_t grid = (uint32_t)std::min<uint64_t>(ngrp, 8ull * ncu);
         a.per = (uint32_t)((ngrp + grid - 1) / grid);
         a.single = a.per <= 1;
-        hipLaunchKernelGGL((k_mv_stream<K, C, R, 64>), dim3(grid), dim3(64), smem, st, a);
+        hipLaunchKernelGGL((k_mv_stream<K, C, R, 64, false>), dim3(grid), dim3(64), smem, st, a);
         return;
     }
-    // residency at the largest x this kernel stages (asked once per kernel)
-    static const int per_cu = [] {
-        int n = 0;
-        const size_t most = (size_t)(kMvMaxXFloats + 4 * (kMvMaxXFloats / 64) + 2 * kMvMaxXFloats / 32) * 4;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_mv_stream<K, C, R, kMvT>, kMvT, most) != hipSuccess)
-            n = 1;
-        return std::max(n, 1);
-    }();
-    const uint64_t max_wg = (uint64_t)std::min(per_cu, 3) * ncu;
-    const uint32_t grid = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(max_wg, (ngrp + kMvW - 1) / kMvW));
-    a.per = (uint32_t)((ngrp + grid - 1) / grid);
-    a.single = a.per <= (uint32_t)kMvW;
-    hipLaunchKernelGGL((k_mv_stream<K, C, R, kMvT>), dim3(grid), dim3(kMvT), smem, st, a);
+    // one vector of rows exactly 64 C chunks wide: the full-width form
+    if (a.nb == 1 && a.lshift == 6 && a.m.cols == 64u * 32u * (uint32_t)C)
+        launch_512<K, C, R, true>(a, ngrp, ncu, smem, st);
+    else
+        launch_512<K, C, R, false>(a, ngrp, ncu, smem, st);
 }
 
 template <uint32_t K>
