@@ -143,8 +143,10 @@ int qh_attention(qh_ctx *ctx, const float *q, const float *k, const float *v, si
  * capture, tight serving loops, harnesses that forbid hipMalloc).  q, k, v
  * and out are device pointers in qh_attention's layouts; the kernel's chunk
  * partials and counters live in a fixed 1 MiB device array of the library
- * (one per GPU), so shapes needing more (heads x chunks x (head_dim + 2)
- * floats plus kvheads counters) are refused with an error.  stream NULL:
+ * (one per GPU).  Both entry points cap the key chunks per KV head at what
+ * the array holds (a chunk then takes several key tiles), so any history
+ * length runs; a shape one chunk of whose partials alone exceeds it
+ * (heads x (head_dim + 2) floats > 1 MiB) is refused with an error.  stream NULL:
  * the context's stream, and the call returns when out is written; otherwise
  * the work is enqueued on that HIP stream and the call returns at once.
  * Calls that overlap on one GPU share the array and race. */
@@ -266,9 +268,9 @@ int qh_read_kv(qh_ctx *ctx, size_t layer, size_t pos0, size_t n, float *k, float
 int qh_fault_inject(qh_ctx *ctx, uint32_t kind);
 
 /* Persistent-step timing (no counterpart in the reference): `steps` decode
- * steps continuing from the current position, with HIP events on the
- * context's stream around the step's one k_decode launch; ms_decode receives
- * its mean milliseconds per token.  ms_embed receives the time between the
+ * steps continuing from the current position, queued back to back, with HIP
+ * events on the context's stream around each step's one k_decode launch;
+ * ms_decode receives its mean milliseconds per token.  ms_embed receives the time between the
  * step's first event and that launch (the embedding row is computed inside
  * k_decode, so it is an empty interval).  Fails unless the persistent step is
  * selected. */

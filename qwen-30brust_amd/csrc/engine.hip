@@ -1955,24 +1955,28 @@ int qh_profile_decode(qh_ctx* c, size_t steps, double* ms_embed, double* ms_deco
         if (!c->persist) throw Error("profile_decode times the persistent step: it is not selected");
         if (c->pos == 0) throw Error("profile_decode continues a sequence: run a prompt first");
         if (c->pos + steps > c->context) throw Error("prompt + max-tokens exceed --ctx");
-        hipEvent_t ev[3];
+        // the steps queued back to back, as the token loop runs them (a step
+        // launched onto an idle queue would add the queue's wake-up to its
+        // time); events before and after each launch, read at the end.  The
+        // step is one launch (the embedding row included): the interval
+        // between the two events before it is empty
+        std::vector<hipEvent_t> ev(3 * steps);
         for (auto& e : ev) HIP_OK(hipEventCreate(&e));
         double acc[2] = {0.0, 0.0};
         put_state(c, (uint32_t)c->pos, (uint32_t)c->pos);
         for (size_t s = 0; s < steps; s++) {
-            // the step is one launch (the embedding row included): the first
-            // interval is empty
-            HIP_OK(hipEventRecord(ev[0], c->s));
-            HIP_OK(hipEventRecord(ev[1], c->s));
+            HIP_OK(hipEventRecord(ev[3 * s], c->s));
+            HIP_OK(hipEventRecord(ev[3 * s + 1], c->s));
             launch_decode(c, 0, (uint32_t)c->layers.size(), true, true);
-            HIP_OK(hipEventRecord(ev[2], c->s));
-            HIP_OK(hipEventSynchronize(ev[2]));
+            HIP_OK(hipEventRecord(ev[3 * s + 2], c->s));
+        }
+        HIP_OK(hipEventSynchronize(ev[3 * steps - 1]));
+        for (size_t s = 0; s < steps; s++)
             for (int k = 0; k < 2; k++) {
                 float ms = 0;
-                HIP_OK(hipEventElapsedTime(&ms, ev[k], ev[k + 1]));
+                HIP_OK(hipEventElapsedTime(&ms, ev[3 * s + k], ev[3 * s + k + 1]));
                 acc[k] += ms;
             }
-        }
         for (auto& e : ev) (void)hipEventDestroy(e);
         DevState st = get_state(c);
         if (st.err) fail_step(c, st.err);
