@@ -1050,13 +1050,18 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
     using Raw = typename Fmt<KV>::Raw;
     // unconditional loads (row and chunk clamped into the matrix; results of
     // clamped rows are dropped): the compiler then waits for exactly the group
-    // it computes, not for the prefetched one behind it
+    // it computes, not for the prefetched one behind it.  The rows are
+    // wave-uniform: a row's byte offset goes in the buffer loads' scalar
+    // offset, the lane's chunk offset (the same for every row) in the vector
+    // one, so no per-lane 64-bit address arithmetic per load (the matrix is
+    // below 4 GB: checked by persist_supported)
     const uint32_t ch = min(c.lane, cpr - 1);
+    const __amdgpu_buffer_rsrc_t vr = buf_rsrc(mv.w, (uint32_t)((size_t)V * mv.drb));
     auto load_group = [&](Raw (&t)[kVocabRows], uint32_t gi) {
 #pragma unroll
         for (uint32_t k = 0; k < kVocabRows; k++) {
             const uint32_t r = min(gi * kVocabRows + k, V - 1);
-            t[k] = Fmt<KV>::load(mv.w + (size_t)r * mv.drb, mv.geo, ch);
+            t[k] = bload_u<KV>(vr, __builtin_amdgcn_readfirstlane(r * mv.drb), mv.geo, ch);
         }
     };
     // the workgroup's groups [g0, g1): the first kDW to its waves in turn, the

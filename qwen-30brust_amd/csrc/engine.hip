@@ -571,6 +571,7 @@ bool persist_supported(const qh_ctx* c, uint32_t nwg) {
     if (!(d.hidden == 2048 && d.heads == 32 && d.kvheads == 4 && d.head_dim == 128)) return false;
     if (!(d.experts >= 8 && d.experts <= 128 && d.top == kDecodeXcds && d.ff == 768)) return false;
     if (!block(c->out.kind) || c->out.cols != d.hidden || c->layers.empty()) return false;
+    if ((uint64_t)c->out.rows * c->out.drb >= (1ull << 32)) return false;  // 32-bit buffer offsets
     const uint32_t km = c->layers[0].q.kind;  // the main format
     if (!block(km)) return false;
     auto mv = [&](uint32_t k) { return k == km || k == Q6_K; };

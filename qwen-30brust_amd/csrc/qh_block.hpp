@@ -203,6 +203,69 @@ __device__ __forceinline__ void block_best(int32_t& k, uint32_t& i) {
     __syncthreads();
 }
 
+// Chunk loads of a row through a buffer resource: the row's byte offset is
+// one 32-bit add per lane, the field offsets (RowGeo) go in the scalar offset.
+// The loads carry the non-temporal hint (cache policy nt): every weight byte
+// is read once per launch, and streams that do not allocate as reusable
+// lines in the vector L1 measured 5-7 % faster on the 256 MB vocab matrix.
+constexpr int kMvAux = 2;  // cache policy nt (non-temporal)
+__device__ __forceinline__ uint4 bld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kMvAux);
+    return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+__device__ __forceinline__ uint2 bld8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, kMvAux);
+    return make_uint2((uint32_t)v[0], (uint32_t)v[1]);
+}
+__device__ __forceinline__ uint32_t bld4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, kMvAux);
+}
+
+// The same bytes as Fmt<KIND>::load (qh_device.hpp), for the row at byte
+// offset ro of the buffer.
+template <uint32_t KIND>
+__device__ __forceinline__ typename Fmt<KIND>::Raw bload(__amdgpu_buffer_rsrc_t r, uint32_t ro, const RowGeo& g,
+                                                         uint32_t c) {
+    const uint32_t b = c >> 3, j = c & 7;
+    if constexpr (KIND == Q4_K) {
+        return {bld16(r, ro + b * 128 + j * 16, g.off_b), bld16(r, ro + b * 16, g.off_a)};
+    } else if constexpr (KIND == Q5_K) {
+        return {bld16(r, ro + b * 128 + j * 16, g.off_c), bld16(r, ro + b * 16, g.off_a),
+                bld16(r, ro + b * 32 + (j & 1) * 16, g.off_b)};
+    } else if constexpr (KIND == Q6_K) {
+        return {bld16(r, ro + b * 128 + j * 16, g.off_a), bld16(r, ro + b * 64 + (j >> 2) * 32 + (j & 1) * 16, g.off_b),
+                bld8(r, ro + b * 16 + (j >> 2) * 8, g.off_c), bld4(r, ro + (b >> 1) * 4, g.off_d)};
+    } else if constexpr (KIND == Q4_0) {
+        return {bld16(r, ro + c * 16, g.off_a), bld4(r, ro + (c >> 1) * 4, g.off_b)};
+    } else {
+        static_assert(KIND == Q8_0, "block-quantised formats only");
+        return {bld16(r, ro + c * 32, g.off_a), bld16(r, ro + c * 32 + 16, g.off_a), bld4(r, ro + (c >> 1) * 4, g.off_b)};
+    }
+}
+
+// The same bytes for a wave-uniform row offset ro: ro and the field offset go
+// in the scalar offset, the lane's chunk offset in the vector offset (which
+// then stays the same from row to row).
+template <uint32_t KIND>
+__device__ __forceinline__ typename Fmt<KIND>::Raw bload_u(__amdgpu_buffer_rsrc_t r, uint32_t ro, const RowGeo& g,
+                                                           uint32_t c) {
+    const uint32_t b = c >> 3, j = c & 7;
+    if constexpr (KIND == Q4_K) {
+        return {bld16(r, b * 128 + j * 16, ro + g.off_b), bld16(r, b * 16, ro + g.off_a)};
+    } else if constexpr (KIND == Q5_K) {
+        return {bld16(r, b * 128 + j * 16, ro + g.off_c), bld16(r, b * 16, ro + g.off_a),
+                bld16(r, b * 32 + (j & 1) * 16, ro + g.off_b)};
+    } else if constexpr (KIND == Q6_K) {
+        return {bld16(r, b * 128 + j * 16, ro + g.off_a), bld16(r, b * 64 + (j >> 2) * 32 + (j & 1) * 16, ro + g.off_b),
+                bld8(r, b * 16 + (j >> 2) * 8, ro + g.off_c), bld4(r, (b >> 1) * 4, ro + g.off_d)};
+    } else if constexpr (KIND == Q4_0) {
+        return {bld16(r, c * 16, ro + g.off_a), bld4(r, (c >> 1) * 4, ro + g.off_b)};
+    } else {
+        static_assert(KIND == Q8_0, "block-quantised formats only");
+        return {bld16(r, c * 32, ro + g.off_a), bld16(r, c * 32 + 16, ro + g.off_a), bld4(r, (c >> 1) * 4, ro + g.off_b)};
+    }
+}
+
 // ------------------------------------------- cross-workgroup data exchange --
 // Workgroups on different XCDs do not share an L2, so data handed from one
 // workgroup to another inside a kernel is written through to memory with
