@@ -1069,7 +1069,7 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
                            P.Kh, P.Vth);
     hipLaunchKernelGGL(k_pf_qkrope, dim3(S), dim3(kBlock), 0, c->s, P.QKV, L.q_norm, L.k_norm, c->acts.rope, p0, S,
                        d.heads, d.kvheads, d.ctx, d.eps, P.Q16, L.kcache, L.vcache, P.Kh, P.Vth, vp, err);
-    hipLaunchKernelGGL(k_pf_attn, dim3(((S + 15) / 16 + 1) / 2, d.kvheads), dim3(256), 0, c->s, P.Q16, P.Kh, P.Vth, p0, S,
+    hipLaunchKernelGGL(k_pf_attn, dim3((S + 15) / 16 * d.kvheads), dim3(256), 0, c->s, P.Q16, P.Kh, P.Vth, p0, S,
                        d.heads / d.kvheads, d.ctx, vp, qd, P.O16);
     // o in two column halves (twice the workgroups) into Y's space; the norm
     // adds both to the residual (model.rs:246-248) before normalising

@@ -1069,10 +1069,12 @@ __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y,
 //                 order inside a 32-key step being the same permutation for
 //                 P and V),
 //   O  += P V    (queries x 128 dims).
-// Workgroup (b, g) takes query blocks nqb-1-b and then b: the causal triangle
-// gives block q about q key blocks, so every workgroup has the same work
-// (about nqb/2 + 1 key blocks per pass pair).  Two heads per wave halve the
-// LDS reads per product against one head per wave (twice the workgroups).
+// One query block per workgroup, nqb x kvheads workgroups: the longer half of
+// the blocks (the causal triangle gives block q about q key blocks) first in
+// dispatch order, the shorter half after them, so that the two workgroups a
+// CU holds at once pair a long block with a short one (two waves per SIMD;
+// one workgroup taking blocks nqb-1-b and b in turn ran one).  Two heads per
+// wave halve the LDS reads per product against one head per wave.
 constexpr uint32_t kAQ = 16, kAK = 64;
 constexpr uint32_t kQT = 2;  // query heads per wave (index qt), each over the block's 16 queries
 // LDS pitches (halfs).  K rows of 272 bytes, their 16-byte column chunks
@@ -1098,12 +1100,21 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
                                                  uint32_t qd, _Float16* O16) {
     __shared__ __align__(16) _Float16 Kl[kAK * kKL];
     __shared__ __align__(16) _Float16 Vt[128 * kVL];
-    const uint32_t nqb = (S + kAQ - 1) / kAQ;
-    for (uint32_t pass = 0; pass < 2; pass++) {
-        const uint32_t qb = pass == 0 ? nqb - 1 - blockIdx.x : blockIdx.x;
-        if (pass == 1 && qb >= nqb - 1 - blockIdx.x) break;
+    // one query block per workgroup: the longer half of the blocks of every
+    // KV head first in dispatch order, then the shorter half, so that the
+    // two workgroups a CU holds at once pair a long block with a short one
+    const uint32_t nqb = (S + kAQ - 1) / kAQ, kvh = gridDim.x / nqb, nl = (nqb + 1) / 2;
+    {
+        uint32_t qb, g;
+        if (blockIdx.x < nl * kvh) {
+            g = blockIdx.x / nl;
+            qb = nqb - 1 - blockIdx.x % nl;
+        } else {
+            const uint32_t L2 = blockIdx.x - nl * kvh;
+            g = L2 / (nqb - nl);
+            qb = L2 % (nqb - nl);
+        }
         const uint32_t q0 = qb * kAQ;
-        const uint32_t g = blockIdx.y;
         const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, grp = lane >> 4, col = lane & 15;
         const bool hok = kQT * w < G;  // the wave's first head exists (wave-uniform)
         // scores / sqrt(128) (ops.rs:87), exponentiated base 2
@@ -1198,20 +1209,33 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
                             st[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[ks][kt], qf[qt][ks], st[kt][qt], 0, 0, 0);
                     }
                 }
-                // causal mask, online softmax per query
+                // causal mask (only blocks that reach past the block's first
+                // query or past kend have masked keys), online softmax per query
+                const bool edge = k0 + kAK > p0 + q0 + 1 || k0 + kAK > kend;  // block-uniform
 #pragma unroll
                 for (uint32_t qt = 0; qt < kQT; qt++) {
                     const uint32_t qpos = p0 + q0 + col;
                     float mx = -INFINITY;
+                    if (edge) {
 #pragma unroll
-                    for (uint32_t kt = 0; kt < 4; kt++)
+                        for (uint32_t kt = 0; kt < 4; kt++)
 #pragma unroll
-                        for (uint32_t i = 0; i < 4; i++) {
-                            const uint32_t kpos = k0 + 16 * kt + 4 * grp + i;
-                            const float v = (kpos <= qpos && kpos < kend) ? st[kt][qt][i] * sc2 : -INFINITY;
-                            st[kt][qt][i] = v;
-                            mx = fmaxf(mx, v);
-                        }
+                            for (uint32_t i = 0; i < 4; i++) {
+                                const uint32_t kpos = k0 + 16 * kt + 4 * grp + i;
+                                const float v = (kpos <= qpos && kpos < kend) ? st[kt][qt][i] * sc2 : -INFINITY;
+                                st[kt][qt][i] = v;
+                                mx = fmaxf(mx, v);
+                            }
+                    } else {
+#pragma unroll
+                        for (uint32_t kt = 0; kt < 4; kt++)
+#pragma unroll
+                            for (uint32_t i = 0; i < 4; i++) {
+                                const float v = st[kt][qt][i] * sc2;
+                                st[kt][qt][i] = v;
+                                mx = fmaxf(mx, v);
+                            }
+                    }
                     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
                     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
                     const float mn = fmaxf(m[qt], mx);
