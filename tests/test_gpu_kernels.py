@@ -13,7 +13,7 @@ engine = importlib.import_module("qwen-30brust_amd")
 synth = importlib.import_module("qwen-30brust_amd.synth")
 
 pytestmark = pytest.mark.gpu
-REL = 1e-4  # matvec / logits tolerance
+REL = 1e-4  # matvec / logits tolerance (relative to the largest |value|)
 
 
 @pytest.fixture(scope="module")

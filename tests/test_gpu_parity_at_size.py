@@ -39,7 +39,7 @@ synth = importlib.import_module("qwen-30brust_amd.synth")
 
 pytestmark = pytest.mark.gpu
 THREADS = min(16, os.cpu_count() or 1)
-REL = 1e-4           # decode path vs the FP32 oracle (north-star bar)
+REL = 1e-4           # decode path vs the FP32 oracle
 PF_TOL = 1e-2        # batched prefill (fp16 operands) vs an FP32 path
 PF_TOL_FLIPPED = 2e-2  # the same when the last token's own routing flipped in some layer
 DECODE_NEAR_TIE = 1e-4  # router gap under which FP32 reassociation may flip the exact decode path
