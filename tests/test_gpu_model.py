@@ -197,6 +197,31 @@ def test_persistent_layer_attention_chunking(dev, layer30b_q4k, pos):
     assert rel_err(xg, xr) <= REL
 
 
+@pytest.fixture(scope="module")
+def layer30b_long():
+    spec = synth.layer30b(more_bits=False, context=16384)
+    img = synth.build_image(spec, threads=8)
+    return spec, img
+
+
+@pytest.mark.parametrize("pos", [8191, 16383])
+def test_persistent_layer_long_context(dev, layer30b_long, pos):
+    """The persistent step beyond 4,096 positions: 16 chunks per XCD of 512
+    and of 1,024 keys (8 and 16 key tiles each), against the oracle layer."""
+    spec, img = layer30b_long
+    om = oracle.Model(oracle.Gguf(img), spec.context)
+    m = engine.Model(img, spec.context, device=dev)
+    assert m.persistent
+    kvd = spec.kvheads * spec.head_dim
+    x = synth.normal(41 + pos, spec.hidden)
+    kp = synth.normal(42 + pos, pos * kvd)
+    vp = synth.normal(43 + pos, pos * kvd)
+    xr, ids_r, _ = om.layer_forward(0, x, pos, kp, vp)
+    xg, ids_g, _ = m.layer_forward(0, x, pos, kp, vp)
+    assert np.array_equal(ids_g, ids_r)
+    assert rel_err(xg, xr) <= REL
+
+
 @pytest.mark.parametrize("main,out", [(synth.Q4_0, synth.Q4_0), (synth.Q8_0, synth.Q8_0),
                                       (synth.Q5_K, synth.Q5_K), (synth.Q6_K, synth.Q4_K)])
 def test_persistent_step_main_formats(dev, main, out):
