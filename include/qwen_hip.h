@@ -225,6 +225,16 @@ int qh_prefill_batched(const qh_ctx *ctx, int *out);
  * router or output logits were not finite.  The rerun's results are the exact
  * step's (the same bits as n qh_forward calls). */
 int qh_prefill_reruns(const qh_ctx *ctx, uint64_t *out);
+/* Memory control (no counterpart in the reference, which holds one copy of
+ * the weights): frees the batched prefill's device memory, the tile-layout
+ * copy of every layer's projection matrices (as many bytes again as their
+ * row layout) and the chunk buffers.  The KV cache, the position and the
+ * token step's weights stay; the next batched prefill builds both again.
+ * For callers that prefill once and then decode with the memory given back. */
+int qh_prefill_release(qh_ctx *ctx);
+/* Device bytes the batched prefill holds now (tile copies + chunk buffers);
+ * 0 before the first batched prefill and after qh_prefill_release. */
+int qh_prefill_bytes(const qh_ctx *ctx, uint64_t *out);
 
 /* One decoder layer (the loop body src/model.rs:227-287) applied to x[hidden]
  * in place at position `pos`, with this layer's KV history replaced by

@@ -107,6 +107,8 @@ _SIGS = {
     "qh_route_log": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
     "qh_route_gap_log": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
     "qh_prefill_reruns": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint64)]),
+    "qh_prefill_release": (C.c_int, [C.c_void_p]),
+    "qh_prefill_bytes": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint64)]),
     "qh_read_kv": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p]),
     "qh_profile_step": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]),
     "qh_bench_read": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p]),
@@ -482,6 +484,21 @@ class Model:
         v = C.c_uint64()
         self.dev._check(lib().qh_prefill_reruns(self.dev.h, C.byref(v)))
         return v.value
+
+    @property
+    def prefill_bytes(self):
+        """Device bytes the batched prefill holds now: the tile-layout copy of
+        the projection matrices plus its chunk buffers (0 before the first
+        batched prefill and after prefill_release())."""
+        v = C.c_uint64()
+        self.dev._check(lib().qh_prefill_bytes(self.dev.h, C.byref(v)))
+        return v.value
+
+    def prefill_release(self):
+        """Frees the batched prefill's device memory (the tile-layout weight
+        copy and the chunk buffers); the KV cache and the position stay, and
+        the next batched prefill builds both again."""
+        self.dev._check(lib().qh_prefill_release(self.dev.h))
 
     @persistent.setter
     def persistent(self, enable):

@@ -1819,6 +1819,29 @@ int qh_prefill_reruns(const qh_ctx* c, uint64_t* out) {
     return 0;
 }
 
+// Frees the batched prefill's device memory: the tile-layout copies of the
+// projection matrices and the chunk buffers.  The next batched prefill builds
+// both again (its fp16 K/V copies come from the KV cache, which stays).
+int qh_prefill_release(qh_ctx* c) {
+    return guarded(c, [&] {
+        need_model(c);
+        HIP_OK(hipStreamSynchronize(c->s));
+        auto& P = c->pf;
+        for (LayerW& L : c->layers)
+            for (DevMat* m : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down}) m->wt = nullptr;
+        P.tiles.release();
+        P.tiled = false;
+        P.buf.release();
+        P.cap = 0;
+        P.max_tiles = 0;
+    });
+}
+
+int qh_prefill_bytes(const qh_ctx* c, uint64_t* out) {
+    *out = (uint64_t)c->pf.tiles.n + (uint64_t)c->pf.buf.n;
+    return 0;
+}
+
 int qh_reset(qh_ctx* c) {
     return guarded(c, [&] {
         need_model(c);

@@ -174,6 +174,38 @@ def test_prefill_continues_a_sequence(dev, model2):
     run_and_check(m, spec, img, prompt[20:], [9], "20 + 40 tokens", prior=prompt[:20])
 
 
+def test_prefill_release_rebuilds_the_same_bits(dev, model2):
+    """qh_prefill_release frees the tile-layout weight copy and the chunk
+    buffers; a prefill after it (from position 0, and continuing a sequence
+    whose earlier 65 positions sit only in the KV cache) gives the bits of a
+    run that never released, and so does the decode step that follows."""
+    spec, img = model2
+    prompt = np.random.default_rng(100).integers(0, spec.vocab, 100).astype(np.uint32)
+    ref = engine.Model(img, spec.context, device=dev)
+    ra0, rl0 = ref.prefill(prompt[:65])
+    ra1, rl1 = ref.prefill(prompt[65:])
+    rnext = ref.forward(ra1)
+
+    m = engine.Model(img, spec.context, device=dev)
+    assert m.prefill_bytes == 0
+    m.prefill(prompt[:65])
+    held = m.prefill_bytes
+    assert held > 0
+    m.prefill_release()
+    assert m.prefill_bytes == 0 and m.position == 65
+    m.reset()
+    a0, l0 = m.prefill(prompt[:65])
+    assert m.prefill_bytes == held
+    m.prefill_release()
+    m.prefill_release()  # idempotent
+    a1, l1 = m.prefill(prompt[65:])
+    assert (a0, a1) == (ra0, ra1)
+    assert np.array_equal(l0, rl0) and np.array_equal(l1, rl1)
+    m.prefill_release()
+    assert np.array_equal(m.forward(a1), rnext)
+    assert m.position == 101
+
+
 def test_prefill_uncovered_model_runs_the_exact_step(dev):
     """head_dim 16 with F32 weights (the reference's fixture model) is outside
     the batched path: the prompt then runs through the exact token step on the
