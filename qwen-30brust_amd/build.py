@@ -3,7 +3,7 @@ command-line driver (qwen-hip) and the synthetic-model generator
 (libqwen_synth.so, host-only g++).
 
 Usage: python qwen-30brust_amd/build.py         (compiles every time it is called)
-       python qwen-30brust_amd/build.py trace   (the phase-trace variant, after a build)
+       python qwen-30brust_amd/build.py trace   (the phase-trace variant; reuses the objects of a build)
 """
 import os
 import subprocess
@@ -37,17 +37,18 @@ def _run(cmd):
     return r
 
 
+def _compile_one(src):
+    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+    if src.endswith(".hip"):
+        _run([HIPCC, *HIP_FLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj])
+    else:  # host-only C++
+        _run(["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-c", os.path.join(CSRC, src), "-o", obj])
+    return obj
+
+
 def build_engine():
     os.makedirs(BUILD, exist_ok=True)
-
-    def compile_one(src):
-        obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-        if src.endswith(".hip"):
-            _run([HIPCC, *HIP_FLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj])
-        else:  # host-only C++
-            _run(["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-c", os.path.join(CSRC, src), "-o", obj])
-        return obj
-
+    compile_one = _compile_one
     with ThreadPoolExecutor(max_workers=len(ENGINE_SOURCES)) as ex:
         objs = list(ex.map(compile_one, ENGINE_SOURCES))
     tmp = ENGINE_SO + ".tmp"
@@ -62,15 +63,17 @@ def build_trace():
     persistent step (decode_trace.hip) in place of decode.hip, for
     phase_trace.py.  Built on request only (`python build.py trace`)."""
     os.makedirs(BUILD, exist_ok=True)
-    objs = []
-    for src in ENGINE_SOURCES:
-        obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+
+    def one(src):
         if src == "decode.hip":
             obj = os.path.join(BUILD, "decode_trace.o")
             _run([HIPCC, *HIP_FLAGS, "-x", "hip", "-c", os.path.join(CSRC, "decode_trace.hip"), "-o", obj])
-        elif not os.path.exists(obj):
-            raise RuntimeError(f"{obj} is missing: build the engine first")
-        objs.append(obj)
+            return obj
+        obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+        return obj if os.path.exists(obj) else _compile_one(src)  # objects of an earlier build are reused
+
+    with ThreadPoolExecutor(max_workers=len(ENGINE_SOURCES)) as ex:
+        objs = list(ex.map(one, ENGINE_SOURCES))
     tmp = TRACE_SO + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, TRACE_SO)

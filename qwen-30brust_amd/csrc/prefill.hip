@@ -1127,8 +1127,10 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
             const _Float16* src = Q16 + ((size_t)(g * G + hh) * S + q) * 128 + 8 * grp;
 #pragma unroll
             for (uint32_t ks = 0; ks < 4; ks++) {
-                if (ok) {
-                    qf[qt][ks] = gld<h8v>(src + 32 * ks);
+                if (ok) {  // q scaled once, so the scores come out in base-2 units
+                    const h8v t = gld<h8v>(src + 32 * ks);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) qf[qt][ks][i] = (_Float16)((float)t[i] * sc2);
                 } else {
 #pragma unroll
                     for (int i = 0; i < 8; i++) qf[qt][ks][i] = (_Float16)0.f;
@@ -1222,7 +1224,7 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
 #pragma unroll
                             for (uint32_t i = 0; i < 4; i++) {
                                 const uint32_t kpos = k0 + 16 * kt + 4 * grp + i;
-                                const float v = (kpos <= qpos && kpos < kend) ? st[kt][qt][i] * sc2 : -INFINITY;
+                                const float v = (kpos <= qpos && kpos < kend) ? st[kt][qt][i] : -INFINITY;
                                 st[kt][qt][i] = v;
                                 mx = fmaxf(mx, v);
                             }
@@ -1230,29 +1232,34 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
 #pragma unroll
                         for (uint32_t kt = 0; kt < 4; kt++)
 #pragma unroll
-                            for (uint32_t i = 0; i < 4; i++) {
-                                const float v = st[kt][qt][i] * sc2;
-                                st[kt][qt][i] = v;
-                                mx = fmaxf(mx, v);
-                            }
+                            for (uint32_t i = 0; i < 4; i++) mx = fmaxf(mx, st[kt][qt][i]);
                     }
                     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
                     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                    const float mn = fmaxf(m[qt], mx);
-                    const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);  // 0 on the first block
+                    // Lazy rescale: the reference maximum m moves (and O, l
+                    // are rescaled) only when some query of the wave saw a
+                    // score above m + 8, so the probabilities stay <= 2^8 (fp16
+                    // holds them at full precision) and most blocks skip the
+                    // rescale; O / l is the same ratio whichever m it used.
+                    // Block 0 always moves it (m = -inf; key 0 is never masked).
+                    if (__any(mx > m[qt] + 8.f)) {  // wave-uniform
+                        const float mn = fmaxf(m[qt], mx);
+                        const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);  // 0 on the first block
+                        l[qt] *= alpha;
+#pragma unroll
+                        for (uint32_t dt = 0; dt < 8; dt++) o[qt][dt] *= alpha;
+                        m[qt] = mn;
+                    }
                     float ls = 0.f;
 #pragma unroll
                     for (uint32_t kt = 0; kt < 4; kt++)
 #pragma unroll
                         for (uint32_t i = 0; i < 4; i++) {
-                            const float pv = __builtin_amdgcn_exp2f(st[kt][qt][i] - mn);
+                            const float pv = __builtin_amdgcn_exp2f(st[kt][qt][i] - m[qt]);
                             st[kt][qt][i] = pv;
                             ls += pv;
                         }
-                    l[qt] = fmaf(l[qt], alpha, ls);
-                    m[qt] = mn;
-#pragma unroll
-                    for (uint32_t dt = 0; dt < 8; dt++) o[qt][dt] *= alpha;
+                    l[qt] += ls;
                 }
                 // O^T += V^T P^T: A = V^T rows (dims) with keys in the same
                 // permuted order as this lane's probabilities, B = P^T
