@@ -307,6 +307,64 @@ __device__ __forceinline__ bool gather_l(const DecodeArgs& A, DecodeLds& S, cons
     return S.abort == 0;
 }
 
+// gather_l of an RMSNorm input x (n elements, n even) with its weights w:
+// dst[px(i)] = x_i w_i and, with raw, raw[px(i)] = x_i; red[wave] receives the
+// wave's sum of x_i^2.  The RMS scale (rms_scale, after the closing barrier)
+// then multiplies what a caller computes from dst: s (W . (x w)) instead of
+// W . (x (s w)), which takes the normalisation's own reduction and barrier
+// out of the way between the gather and the dot products.  (Used where the
+// gathered vector arrives last, x'' from across the XCDs; on x', whose
+// hand-over inside the XCD is short, the same form measured slower.)
+__device__ __forceinline__ bool gather_l_norm(const DecodeArgs& A, DecodeLds& S, const uint64_t* src, uint32_t n,
+                                              uint32_t tag, const float* w, float* dst, float* raw, uint32_t tid) {
+    const uint32_t np = n / 2;
+    const __amdgpu_buffer_rsrc_t r = buf_rsrc(src, np * 16);
+    bool ab = false;
+    float ss = 0.f;
+    __syncthreads();  // every wave is done with what the previous phase kept in dst's region
+    for (uint32_t p0 = tid; p0 < np; p0 += kGatherPairs * kDT) {
+        uint32_t word[kGatherPairs], need = 0;
+        float2 wp[kGatherPairs];
+#pragma unroll
+        for (uint32_t k = 0; k < kGatherPairs; k++) {
+            const uint32_t p = p0 + k * kDT;
+            word[k] = 2 * p;
+            if (p < np) need |= 1u << k;
+            wp[k] = p < np ? gld<float2>(w + 2 * p) : make_float2(0.f, 0.f);
+        }
+        float v[2 * kGatherPairs];
+        poll_pairs<kAuxL, kGatherPairs>(A, r, word, need, need, tag, v, ab);
+        if (ab) break;
+#pragma unroll
+        for (uint32_t k = 0; k < kGatherPairs; k++) {
+            const uint32_t p = p0 + k * kDT, d = px(2 * p);  // a pair stays adjacent
+            if (p < np) {
+                dst[d] = v[2 * k] * wp[k].x;
+                dst[d + 1] = v[2 * k + 1] * wp[k].y;
+                if (raw) {
+                    raw[d] = v[2 * k];
+                    raw[d + 1] = v[2 * k + 1];
+                }
+                ss = fmaf(v[2 * k + 1], v[2 * k + 1], fmaf(v[2 * k], v[2 * k], ss));
+            }
+        }
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) S.red[tid >> 6] = ss;
+    if (ab) S.abort = 1;
+    __syncthreads();
+    return S.abort == 0;
+}
+
+// RMSNorm scale 1/sqrt(mean(x^2) + eps) (ops.rs:3-15) from gather_l_norm's
+// per-wave sums (the same order in every thread).
+__device__ __forceinline__ float rms_scale(const DecodeLds& S, uint32_t n, float eps) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < kDW; i++) t += S.red[i];
+    return 1.0f / sqrtf(t / (float)n + eps);
+}
+
 // Block sum.  It ends without a barrier: every caller reaches another
 // barrier before anything writes red again.
 __device__ __forceinline__ float dsum(float v, float* red) {
@@ -440,6 +498,11 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
     }
     attn_prefetch(A, L, c, P);
     float* xs = S.big;
+    // the raw x of layers after the first (xs holds x * attn_norm there, and
+    // `post` the RMS scale that multiplies the dot products); px(2047) = 2171
+    float* const xraw = S.big + 2304;
+    const float* xr = xs;
+    float post = 1.f;
     QH_MARK(0, 0);
     if (l == A.l0) {
         if (A.embed) {
@@ -457,24 +520,27 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
             *reinterpret_cast<float4*>(xs + px(4 * c.tid)) = ld_sys4(buf_rsrc(A.a.x, c.H * 4), c.tid * 16);
         }
         __syncthreads();
-    } else if (!gather_l(A, S, lbuf(A.lx2, kDecodeStrideX2, c.X), c.H, ptag(A, l - 1, 7), xs, c.tid)) {
-        return false;  // x'' of the previous layer (phase R)
+    } else {
+        if (!gather_l_norm(A, S, lbuf(A.lx2, kDecodeStrideX2, c.X), c.H, ptag(A, l - 1, 7), L.attn_norm, xs, xraw,
+                           c.tid))
+            return false;  // x'' of the previous layer (phase R)
+        xr = xraw;
+        post = rms_scale(S, c.H, A.dm.eps);
     }
     QH_MARK(0, 1);
-    // raw values before the in-place norm: this workgroup's rows of x and
-    // the router columns
+    // raw values: this workgroup's rows of x and the router columns
     if (c.tid < kRowsWg / 4)
-        *reinterpret_cast<float4*>(S.xo + 4 * c.tid) = *reinterpret_cast<const float4*>(xs + px(kRowsWg * c.j + 4 * c.tid));
+        *reinterpret_cast<float4*>(S.xo + 4 * c.tid) = *reinterpret_cast<const float4*>(xr + px(kRowsWg * c.j + 4 * c.tid));
     if (c.wv < kExpWg) {
-        const float4 xr = *reinterpret_cast<const float4*>(xs + px(rcol));
-        float rd = (wr.x * fw.x) * xr.x;
-        rd = fmaf(wr.y * fw.y, xr.y, rd);
-        rd = fmaf(wr.z * fw.z, xr.z, rd);
-        rd = fmaf(wr.w * fw.w, xr.w, rd);
+        const float4 xv = *reinterpret_cast<const float4*>(xr + px(rcol));
+        float rd = (wr.x * fw.x) * xv.x;
+        rd = fmaf(wr.y * fw.y, xv.y, rd);
+        rd = fmaf(wr.z * fw.z, xv.z, rd);
+        rd = fmaf(wr.w * fw.w, xv.w, rd);
         rd = wave_sum(rd);
         if (c.lane == 0) S.ra[c.wv] = rd;
     }
-    norm_in_lds(c, xs, nw, A.dm.eps, S.red);
+    if (l == A.l0) norm_in_lds(c, xs, nw, A.dm.eps, S.red);  // in place, scale included
     float xa[16], xb[16], sa, sb;
     x_runs_p<KQ>(xs, 0, c.lane, xa, xb, sa, sb);
 #pragma unroll
@@ -490,7 +556,7 @@ __device__ __forceinline__ bool phase_qkv(const DecodeArgs& A, DecodeLds& S, con
         } else {
             acc = Fmt<KQ>::dot(wvv[k].template get<KQ>(), c.lane, xa, xb, sa, sb);  // the q|k rows' x runs
         }
-        acc = wave_sum(acc);
+        acc = wave_sum(acc) * post;
         if (c.lane == 0) S.hv[c.wv + kDW * k] = acc;
     }
     QH_MARK(0, 2);
@@ -1075,13 +1141,13 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
     load_group(cur, min(gi, ngrp - 1));
     // read now, used by workgroup 0 after the argmax hand-over
     const uint32_t n_given = a.st->n_given;
-    const float4 on = gld<float4>(A.onorm + 4 * c.tid);
     QH_MARK(6, 0);
     float* xs = S.big;
-    if (!gather_l(A, S, lbuf(A.lx2, kDecodeStrideX2, c.X), c.H, ptag(A, A.l1 - 1, 7), xs, c.tid))
-        return;  // x after the last layer
+    if (!gather_l_norm(A, S, lbuf(A.lx2, kDecodeStrideX2, c.X), c.H, ptag(A, A.l1 - 1, 7), A.onorm, xs, nullptr,
+                       c.tid))
+        return;  // x after the last layer, times the output norm's weights
+    const float post = rms_scale(S, c.H, A.dm.eps);
     QH_MARK(6, 1);
-    norm_in_lds(c, xs, on, A.dm.eps, S.red);
     float xa[16], xb[16], sa, sb;
     if (c.lane < cpr) x_runs_p<KV>(xs, 0, c.lane, xa, xb, sa, sb);
     int32_t bk = INT32_MIN;
@@ -1096,7 +1162,7 @@ __device__ __forceinline__ void phase_vocab(const DecodeArgs& A, DecodeLds& S, c
 #pragma unroll
         for (uint32_t k = 0; k < kVocabRows; k++) {
             acc[k] = c.lane < cpr ? Fmt<KV>::dot(cur[k], c.lane, xa, xb, sa, sb) : 0.f;
-            acc[k] = wave_sum(acc[k]);
+            acc[k] = wave_sum(acc[k]) * post;
         }
         if (c.lane == 0) {
 #pragma unroll
