@@ -27,7 +27,7 @@
 //      router term sum_c router[e][c] ffn_norm[c] x[c] over this XCD's
 //      256 columns for experts 4j..4j+3                        -> L qkv
 //   B  Q/K RMSNorm, RoPE, KV append, GQA attention of the XCD's 4 heads over
-//      key chunk j (online softmax, P.V on MFMA; at most 16 chunks)
+//      key chunk j (online softmax, P.V on MFMA; at most 32 chunks)
 //                                                              -> L partials
 //   C  merge of the chunk partials (every workgroup); o-projection partial
 //      over this XCD's 512 attention columns for rows [64j, 64j+64), and the
@@ -86,10 +86,10 @@ constexpr uint32_t kRowsWg = 64;            // rows of x per workgroup slice (20
 constexpr uint32_t kExpWg = 4;              // router experts per workgroup slice (128 / 32)
 constexpr uint32_t kDTile = 64;             // keys per attention tile
 constexpr uint32_t kMinKeys = 64;           // fewest keys per attention chunk (one tile)
-constexpr uint32_t kMaxChunks = 16;         // most attention chunks per XCD
+constexpr uint32_t kMaxChunks = 32;         // most attention chunks per XCD (one per workgroup)
 constexpr uint32_t kTP = 132;               // LDS pitch of the value tile (floats)
 constexpr uint32_t kPP = 68;                // LDS pitch of the per-head scores (floats)
-constexpr uint32_t kDSmem = 10240;          // floats of phase scratch
+constexpr uint32_t kDSmem = 18560;          // floats of phase scratch (phase C: 32 chunk partials + the merged output)
 constexpr uint32_t kFfWg = 24;              // gate/up rows per workgroup (768 / 32), 3 per wave
 constexpr uint32_t kDownUnits = 3;          // chunks per lane in F (8 rows x 24 chunks per wave)
 constexpr uint32_t kVocabRows = 4;          // vocab rows per wave group
@@ -159,7 +159,6 @@ template <uint32_t KM> struct ChunkBox {
 };
 
 struct DecodeLds {
-    float big[kDSmem];        // phase scratch (x, attention tiles, h, reductions)
     float xo[kRowsWg];        // rows [64j, 64j+64) of the residual stream x (then x'')
     float x1[kRowsWg];        // the same rows of x'
     float po[kRowsWg];        // o-projection partial / weighted down partial of those rows
@@ -179,6 +178,9 @@ struct DecodeLds {
     uint32_t abort;
     uint32_t bad;
     uint32_t vq;              // next vocab row group of this workgroup to hand out
+    // phase scratch (x, attention tiles, h, reductions) last: the small
+    // fields above stay within the 64-KB reach of an LDS instruction's offset
+    alignas(16) float big[kDSmem];
 };
 
 // Per-workgroup constants of one launch.
@@ -400,16 +402,18 @@ __device__ __forceinline__ uint32_t ptag(const DecodeArgs& A, uint32_t l, uint32
 // Per-XCD and cross-XCD exchange buffers of this workgroup's XCD.
 __device__ __forceinline__ uint64_t* lbuf(uint64_t* base, uint32_t stride, uint32_t X) { return base + (size_t)X * stride; }
 
-// Chunk geometry of the attention: chunk j of T keys, at least kMinKeys keys
-// per chunk, at most kMaxChunks chunks (a chunk's time hardly depends on how
-// many of its tile's 64 keys are used, and fewer chunks are cheaper to merge).
+// Chunk geometry of the attention: chunk j of T keys.  A chunk's time grows
+// with its 64-key tiles (each waits for its K/V slice) and hardly with how
+// many of a tile's keys are used, and fewer chunks are cheaper to merge: up to
+// 16 chunks of at least one tile (T <= 2048: one or two tiles each), then up
+// to 32 chunks of two tiles (T <= 4096), then 32 chunks of T/32 keys.
 struct AttnChunk {
     uint32_t nch, t0, t1;
     bool active;
 };
 __device__ __forceinline__ AttnChunk attn_chunk(const Ctx& c) {
     AttnChunk k;
-    const uint32_t tc = max((c.T + kMaxChunks - 1) / kMaxChunks, kMinKeys);
+    const uint32_t tc = max((c.T + kMaxChunks - 1) / kMaxChunks, min(max((c.T + 15) / 16, kMinKeys), 2 * kDTile));
     k.nch = (c.T + tc - 1) / tc;
     k.active = c.j < k.nch;
     k.t0 = min(c.T, c.j * tc);
@@ -796,30 +800,55 @@ __device__ __forceinline__ bool phase_oproj(const DecodeArgs& A, DecodeLds& S, c
     // the next layer's descriptor, while this phase waits for the partials
     if (l + 1 < A.l1) warm_layer(A.layers + l + 1);
     QH_MARK(2, 0);
-    float* ps = S.big;             // [nch][4][130] chunk partials (padded layout)
-    float* xs = S.big + 9216;      // [512] merged attention output (padded layout)
+    float* ps = S.big;             // [nch][4][130] chunk partials (padded layout; px(32*4*130 - 1) = 17679)
+    float* xs = S.big + 17920;     // [512] merged attention output (padded layout)
+    static_assert(17920 >= kMaxChunks * kHX * kPartWords + kMaxChunks * kHX * kPartWords / 64 * 4 &&
+                      17920 + 512 + 512 / 64 * 4 <= kDSmem,
+                  "the partials and the merged output in the phase scratch");
     const uint32_t nch = attn_chunk(c).nch;
     if (!gather_l(A, S, lbuf(A.lpart, kDecodeStridePart, c.X), nch * kHX * kPartWords, ptag(A, l, 2), ps, c.tid))
         return false;  // the chunk partials (phase B)
     QH_MARK(2, 1);
     {
-        // every wave computes the 64 merge weights (lane = (head, chunk)) and
-        // reads its head's from its own lanes: no hand-over through LDS
-        const uint32_t h = c.lane >> 4, ck = c.lane & 15, pb = (ck * kHX + h) * kPartWords;
-        const bool on = ck < nch;
-        const float m = on ? ps[px(pb + 128)] : -INFINITY;
-        float M = fmaxf(m, dpp_f<kDppXor1>(m));
-        M = fmaxf(M, dpp_f<kDppXor2>(M));
-        M = fmaxf(M, dpp_f<kDppHalfMirror>(M));
-        M = fmaxf(M, dpp_f<kDppMirror>(M));  // max over the head's 16 lanes
-        const float e = on ? expf(m - M) : 0.f;
-        const float Ls = seg_sum(on ? ps[px(pb + 129)] * e : 0.f, 16);
-        const float mw = e / Ls;
+        // every wave computes the merge weights (lane = (head, chunk ck), and
+        // chunk ck + 16 in the same lane past 16 chunks) and reads its head's
+        // from its own lanes: no hand-over through LDS
+        const uint32_t h = c.lane >> 4, ck = c.lane & 15, pb0 = (ck * kHX + h) * kPartWords;
         const uint32_t hw = __builtin_amdgcn_readfirstlane(c.tid >> 7), d = c.tid & 127;  // head of this wave
         float a = 0.f;
-        for (uint32_t k = 0; k < nch; k++)
-            a = fmaf(ps[px((k * kHX + hw) * kPartWords + d)],
-                     __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(mw), hw * 16 + k)), a);
+        if (nch <= 16) {  // uniform
+            const bool on = ck < nch;
+            const float m = on ? ps[px(pb0 + 128)] : -INFINITY;
+            float M = fmaxf(m, dpp_f<kDppXor1>(m));
+            M = fmaxf(M, dpp_f<kDppXor2>(M));
+            M = fmaxf(M, dpp_f<kDppHalfMirror>(M));
+            M = fmaxf(M, dpp_f<kDppMirror>(M));  // max over the head's 16 lanes
+            const float e = on ? expf(m - M) : 0.f;
+            const float Ls = seg_sum(on ? ps[px(pb0 + 129)] * e : 0.f, 16);
+            const float mw = e / Ls;
+            for (uint32_t k = 0; k < nch; k++)
+                a = fmaf(ps[px((k * kHX + hw) * kPartWords + d)],
+                         __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(mw), hw * 16 + k)), a);
+        } else {
+            const uint32_t pb1 = ((ck + 16) * kHX + h) * kPartWords;
+            const bool on1 = ck + 16 < nch;
+            const float m0 = ps[px(pb0 + 128)], m1 = on1 ? ps[px(pb1 + 128)] : -INFINITY;
+            float M = fmaxf(m0, m1);
+            M = fmaxf(M, dpp_f<kDppXor1>(M));
+            M = fmaxf(M, dpp_f<kDppXor2>(M));
+            M = fmaxf(M, dpp_f<kDppHalfMirror>(M));
+            M = fmaxf(M, dpp_f<kDppMirror>(M));  // max over the head's 16 lanes
+            const float e0 = expf(m0 - M), e1 = on1 ? expf(m1 - M) : 0.f;
+            const float Ls = seg_sum(ps[px(pb0 + 129)] * e0 + (on1 ? ps[px(pb1 + 129)] * e1 : 0.f), 16);
+            const float mw0 = e0 / Ls, mw1 = e1 / Ls;
+            for (uint32_t k = 0; k < 16; k++)
+                a = fmaf(ps[px((k * kHX + hw) * kPartWords + d)],
+                         __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(mw0), hw * 16 + k)), a);
+            for (uint32_t k = 16; k < nch; k++)
+                a = fmaf(ps[px((k * kHX + hw) * kPartWords + d)],
+                         __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(mw1), hw * 16 + k - 16)),
+                         a);
+        }
         xs[px(c.tid)] = a;
     }
     __syncthreads();

@@ -144,7 +144,7 @@ constexpr uint32_t kDecodeXcds = 8;         // XCDs of the device (workgroup b o
 constexpr uint32_t kDecodeWgPerXcd = 32;    // workgroups per XCD
 constexpr uint32_t kDecodeQkvX = 768;       // q|k|v rows per XCD: 4 query heads + one KV head
 constexpr uint32_t kDecodeStrideQkv = 768;
-constexpr uint32_t kDecodeStridePart = 16 * 4 * kPartWords;  // [chunk][head] partials
+constexpr uint32_t kDecodeStridePart = 32 * 4 * kPartWords;  // [chunk][head] partials, up to 32 chunks
 constexpr uint32_t kDecodeStrideX1 = 2048 + 128;  // x' and the unscaled router logits
 constexpr uint32_t kDecodeStrideH = 768;
 constexpr uint32_t kDecodeStrideX2 = 2048;
@@ -158,7 +158,7 @@ struct DecodeArgs {
     ModelDims dm;
     uint32_t* abort_flag;  // set when a wait times out; every wait then returns
     uint64_t* lqkv;        // [8][768]   q|k|v rows of the XCD
-    uint64_t* lpart;       // [8][16][4][130] attention chunk partials (o, m, l)
+    uint64_t* lpart;       // [8][32][4][130] attention chunk partials (o, m, l)
     uint64_t* lx1;         // [8][2176]  x' and the unscaled router logits
     uint64_t* lh;          // [8][768]   SwiGLU outputs of the XCD's expert
     uint64_t* lx2;         // [8][2048]  x''

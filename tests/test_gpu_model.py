@@ -176,13 +176,14 @@ def layer30b_q4k():
     return spec, img
 
 
-@pytest.mark.parametrize("pos", [0, 1, 63, 64, 65, 700, 1100, 2047, 3000, 4095])
+@pytest.mark.parametrize("pos", [0, 1, 63, 64, 65, 700, 1100, 2047, 2500, 3000, 3583, 4095])
 def test_persistent_layer_attention_chunking(dev, layer30b_q4k, pos):
     """The persistent step at positions that exercise the attention split: one
     key, one chunk, chunk boundaries (64-key tiles, at least 64 keys per
-    chunk), 11 and then 16 chunks per XCD (the most) of one tile or two, and
-    late in the context 16 chunks of several tiles each (3,001 keys: 188
-    each; 4,096: four whole tiles each); against the oracle layer."""
+    chunk), 11 and then 16 chunks per XCD of one tile or two (up to 2,048
+    keys), then chunks of two tiles, up to 32 per XCD: 2,501 keys in 20
+    (the last of 69 keys), 3,001 in 24, 3,584 in 28 and 4,096 in 32;
+    against the oracle layer."""
     spec, img = layer30b_q4k
     om = oracle.Model(oracle.Gguf(img), spec.context)
     m = engine.Model(img, spec.context, device=dev)
@@ -206,8 +207,8 @@ def layer30b_long():
 
 @pytest.mark.parametrize("pos", [8191, 16383])
 def test_persistent_layer_long_context(dev, layer30b_long, pos):
-    """The persistent step beyond 4,096 positions: 16 chunks per XCD of 512
-    and of 1,024 keys (8 and 16 key tiles each), against the oracle layer."""
+    """The persistent step beyond 4,096 positions: 32 chunks per XCD of 256
+    and of 512 keys (4 and 8 key tiles each), against the oracle layer."""
     spec, img = layer30b_long
     om = oracle.Model(oracle.Gguf(img), spec.context)
     m = engine.Model(img, spec.context, device=dev)
