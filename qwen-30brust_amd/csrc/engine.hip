@@ -63,7 +63,7 @@ __global__ void k_pf_qkrope(const float*, const float*, const float*, const floa
                             uint32_t, uint32_t, float, _Float16*, float*, float*, _Float16*, _Float16*, uint32_t,
                             uint32_t*);
 __global__ void k_pf_attn(const _Float16*, const _Float16*, const _Float16*, uint32_t, uint32_t, uint32_t, uint32_t,
-                          uint32_t, uint32_t, _Float16*);
+                          uint32_t, uint32_t, _Float16*, float*, uint32_t*);
 __global__ void k_pf_kvh(const float*, const float*, uint32_t, uint32_t, uint32_t, uint32_t, _Float16*, _Float16*);
 __global__ void k_pf_router(const float*, DevMat, uint32_t, uint32_t, uint32_t, float*);
 __global__ void k_pf_topk(const float*, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t*, float*, DevState*, uint32_t*,
@@ -249,6 +249,8 @@ struct qh_ctx {
         _Float16 *Xn16 = nullptr, *Q16 = nullptr, *O16 = nullptr, *Hs = nullptr, *Kh = nullptr, *Vth = nullptr;
         uint32_t *ids = nullptr, *goff = nullptr, *tok = nullptr, *asg = nullptr, *te = nullptr, *tm = nullptr,
                  *ntile = nullptr;
+        float* axw = nullptr;      // attention hand-over slots (kPfAttnSlot floats each)
+        uint32_t* axc = nullptr;   // their arrival counters (zero between launches)
         uint32_t max_tiles = 0;
         // tile-layout copies of the GEMMs' matrices (DevMat::wt of q, k, v,
         // o, gate, up, down of every layer), built on the first batched
@@ -987,6 +989,7 @@ void prefill_alloc(qh_ctx* c, uint32_t cap) {
     const uint64_t n_asg = (uint64_t)cap * d.top;
     const uint32_t max_tiles = (uint32_t)((n_asg + 127) / 128 + d.experts);
     auto up = [](uint64_t b) { return (b + 255) / 256 * 256; };
+    const uint64_t npair = ((cap + 15) / 16 + 1) / 2 * d.kvheads;  // attention block pairs
     struct R {
         uint64_t bytes;
         void** dst;
@@ -1002,6 +1005,7 @@ void prefill_alloc(qh_ctx* c, uint32_t cap) {
         {4, (void**)&P.ntile},
         {(uint64_t)d.kvheads * d.ctx * 128 * 2, (void**)&P.Kh},
         {(uint64_t)d.kvheads * 128 * ((d.ctx + 63) / 64 * 64) * 2, (void**)&P.Vth},
+        {npair * 2 * kPfAttnSlot * 4, (void**)&P.axw}, {npair * 4, (void**)&P.axc},
     };
     uint64_t total = 0;
     for (const R& r : regs) total += up(r.bytes);
@@ -1069,8 +1073,10 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
                            P.Kh, P.Vth);
     hipLaunchKernelGGL(k_pf_qkrope, dim3(S), dim3(kBlock), 0, c->s, P.QKV, L.q_norm, L.k_norm, c->acts.rope, p0, S,
                        d.heads, d.kvheads, d.ctx, d.eps, P.Q16, L.kcache, L.vcache, P.Kh, P.Vth, vp, err);
-    hipLaunchKernelGGL(k_pf_attn, dim3((S + 15) / 16 * d.kvheads), dim3(256), 0, c->s, P.Q16, P.Kh, P.Vth, p0, S,
-                       d.heads / d.kvheads, d.ctx, vp, qd, P.O16);
+    // two workgroups per pair of query blocks (the n-1-i-th and the i-th of n)
+    const uint32_t npair = ((S + 15) / 16 + 1) / 2;
+    hipLaunchKernelGGL(k_pf_attn, dim3(2 * npair * d.kvheads), dim3(256), 0, c->s, P.Q16, P.Kh, P.Vth, p0, S,
+                       d.heads / d.kvheads, d.ctx, vp, qd, P.O16, P.axw, P.axc);
     // o in two column halves (twice the workgroups) into Y's space; the norm
     // adds both to the residual (model.rs:246-248) before normalising
     const size_t ostride = (size_t)S * H;

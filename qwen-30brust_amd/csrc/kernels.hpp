@@ -202,6 +202,12 @@ void launch_sample_sort(unsigned long long* cand, uint32_t np, hipStream_t s);
 void launch_sample_fold(const SampleArgs& a, const unsigned long long* cand, float* prob, uint32_t P, uint32_t K,
                         hipStream_t s);
 
+// Batched-prefill attention (prefill.hip: k_pf_attn): floats of the (O, m, l)
+// hand-over slot of one workgroup (4 waves x 68 values x 64 lanes) when two
+// workgroups share a query block's keys; two slots and a zeroed counter per
+// block pair and KV head.
+constexpr uint32_t kPfAttnSlot = 4 * 68 * 64;
+
 // Expert work list of the batched-prefill grouped GEMMs (prefill.hip): tile
 // y covers rows [tm, tm + 128) of expert te; the rows of expert e are
 // [goff[e], goff[e+1]) of the assignments sorted by expert.

@@ -1069,12 +1069,16 @@ __global__ __launch_bounds__(kBlock) void k_pf_combine(float* X, const float* Y,
 //                 order inside a 32-key step being the same permutation for
 //                 P and V),
 //   O  += P V    (queries x 128 dims).
-// One query block per workgroup, nqb x kvheads workgroups: the longer half of
-// the blocks (the causal triangle gives block q about q key blocks) first in
-// dispatch order, the shorter half after them, so that the two workgroups a
-// CU holds at once pair a long block with a short one (two waves per SIMD;
-// one workgroup taking blocks nqb-1-b and b in turn ran one).  Two heads per
-// wave halve the LDS reads per product against one head per wave.
+// The causal triangle gives block q about q key blocks.  Blocks nqb-1-i and
+// i form pair i, which two workgroups share with about half of its key blocks
+// each: workgroup 0 takes the first key blocks of the long block, workgroup
+// 1 the rest of them and then the short block, and the two parts of the long
+// block are merged by the workgroup that finishes second (through memory, no
+// waiting).  So every workgroup of the launch has the same work, and the two
+// a CU holds at once (two waves per SIMD) both run to the end; with one long
+// and one short block per CU, the long block ran alone for most of the launch
+// at one wave per SIMD, about 1.2x as long.  Two heads per wave halve the LDS
+// reads per product against one head per wave.
 constexpr uint32_t kAQ = 16, kAK = 64;
 constexpr uint32_t kQT = 2;  // query heads per wave (index qt), each over the block's 16 queries
 // LDS pitches (halfs).  K rows of 272 bytes, their 16-byte column chunks
@@ -1095,30 +1099,40 @@ __device__ __forceinline__ uint2 pack4h(float a, float b, float c, float d) {
     return make_uint2(u.x, u.y);
 }
 
+// Hand-over of a split query block: one slot per workgroup, [wave][value][lane]
+// floats, values 32 qt + 4 dt + i = o[qt][dt][i], then m and l of head qt at
+// 64 + 2 qt and 65 + 2 qt.
+constexpr uint32_t kXv = kQT * 32 + 2 * kQT;
+static_assert(4 * kXv * 64 == kPfAttnSlot, "hand-over slot size");
+
 __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _Float16* Kh, const _Float16* Vth,
                                                  uint32_t p0, uint32_t S, uint32_t G, uint32_t ctx, uint32_t vp,
-                                                 uint32_t qd, _Float16* O16) {
+                                                 uint32_t qd, _Float16* O16, float* xw, uint32_t* xcnt) {
     __shared__ __align__(16) _Float16 Kl[kAK * kKL];
     __shared__ __align__(16) _Float16 Vt[128 * kVL];
-    // one query block per workgroup: the longer half of the blocks of every
-    // KV head first in dispatch order, then the shorter half, so that the
-    // two workgroups a CU holds at once pair a long block with a short one
-    const uint32_t nqb = (S + kAQ - 1) / kAQ, kvh = gridDim.x / nqb, nl = (nqb + 1) / 2;
-    {
-        uint32_t qb, g;
-        if (blockIdx.x < nl * kvh) {
-            g = blockIdx.x / nl;
-            qb = nqb - 1 - blockIdx.x % nl;
-        } else {
-            const uint32_t L2 = blockIdx.x - nl * kvh;
-            g = L2 / (nqb - nl);
-            qb = L2 % (nqb - nl);
-        }
+    __shared__ uint32_t xlast;  // arrivals before this workgroup's at a split block
+    // pair pi of KV head g: long block qL = nqb-1-pi and short block qS = pi
+    // (the same block for the middle one of an odd count), two workgroups
+    const uint32_t nqb = (S + kAQ - 1) / kAQ, npair = (nqb + 1) / 2, kvh = gridDim.x / (2 * npair);
+    const uint32_t role = blockIdx.x & 1, unit = blockIdx.x >> 1, g = unit % kvh, pi = unit / kvh;
+    const uint32_t qL = nqb - 1 - pi, qS = pi;
+    const uint32_t ntL = (p0 + min(qL * kAQ + kAQ, S) + kAK - 1) / kAK;
+    const uint32_t ntS = qS != qL ? (p0 + min(qS * kAQ + kAQ, S) + kAK - 1) / kAK : 0;
+    // split of qL: workgroup 0 takes key blocks [0, hs), workgroup 1 [hs, ntL)
+    // and then all of qS, hs about half the pair's key blocks and 64 hs <= qL's
+    // first query position (each query sees a key of both parts)
+    const uint32_t hs = min(min((ntL + ntS + 1) / 2, ntL), (p0 + qL * kAQ) / kAK);
+    const bool split = hs > 0 && hs < ntL;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, grp = lane >> 4, col = lane & 15;
+    const bool hok = kQT * w < G;  // the wave's first head exists (wave-uniform)
+    // scores / sqrt(128) (ops.rs:87), exponentiated base 2
+    const float sc2 = 1.4426950408889634f / sqrtf(128.0f);
+    const _Float16* kg = Kh + (size_t)g * ctx * 128;
+    const _Float16* vg = Vth + (size_t)g * 128 * vp;
+    // staging: K thread (key tid/4, 32 dims); V^T thread (dim tid/2, 32 keys)
+    const uint32_t skey = tid >> 2, sd0 = (tid & 3) * 32, sdim = tid >> 1, skk0 = (tid & 1) * 32;
+    auto run = [&](const uint32_t qb, const uint32_t ta, const uint32_t tb, const bool part) {
         const uint32_t q0 = qb * kAQ;
-        const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, grp = lane >> 4, col = lane & 15;
-        const bool hok = kQT * w < G;  // the wave's first head exists (wave-uniform)
-        // scores / sqrt(128) (ops.rs:87), exponentiated base 2
-        const float sc2 = 1.4426950408889634f / sqrtf(128.0f);
         h8v qf[kQT][4];
 #pragma unroll
         for (uint32_t qt = 0; qt < kQT; qt++) {
@@ -1151,10 +1165,6 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
             l[qt] = 0.f;
         }
         const uint32_t kend = p0 + min(q0 + kAQ, S);  // keys [0, kend) can be attended
-        const _Float16* kg = Kh + (size_t)g * ctx * 128;
-        const _Float16* vg = Vth + (size_t)g * 128 * vp;
-        // staging: K thread (key tid/4, 32 dims); V^T thread (dim tid/2, 32 keys)
-        const uint32_t skey = tid >> 2, sd0 = (tid & 3) * 32, sdim = tid >> 1, skk0 = (tid & 1) * 32;
         uint4 kr[4], vr[4];
         auto kvload = [&](uint32_t k0) {
 #pragma unroll
@@ -1176,8 +1186,9 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
                 }
             }
         };
-        kvload(0);
-        for (uint32_t k0 = 0; k0 < kend; k0 += kAK) {
+        const uint32_t kstop = tb * kAK;
+        kvload(ta * kAK);
+        for (uint32_t k0 = ta * kAK; k0 < kstop; k0 += kAK) {
 #pragma unroll
             for (uint32_t i = 0; i < 4; i++) {
                 *reinterpret_cast<uint4*>(Kl + skey * kKL + 8 * kchunk(sd0 / 8 + i)) = kr[i];
@@ -1186,7 +1197,7 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
                 vd[1] = make_uint2(vr[i].z, vr[i].w);
             }
             __syncthreads();
-            if (k0 + kAK < kend) kvload(k0 + kAK);  // next block, during this one
+            if (k0 + kAK < kstop) kvload(k0 + kAK);  // next block, during this one
             if (hok) {  // wave-uniform
                 f4v st[4][kQT];
 #pragma unroll
@@ -1241,7 +1252,8 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
                     // score above m + 8, so the probabilities stay <= 2^8 (fp16
                     // holds them at full precision) and most blocks skip the
                     // rescale; O / l is the same ratio whichever m it used.
-                    // Block 0 always moves it (m = -inf; key 0 is never masked).
+                    // A segment's first block always moves it (m = -inf; every
+                    // query sees a key of it).
                     if (__any(mx > m[qt] + 8.f)) {  // wave-uniform
                         const float mn = fmaxf(m[qt], mx);
                         const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);  // 0 on the first block
@@ -1291,22 +1303,73 @@ __global__ __launch_bounds__(kGT, 2) void k_pf_attn(const _Float16* Q16, const _
             }
             __syncthreads();
         }
+        if (part) {
+            // Both parts of a split block store (O, m, l) to their slot,
+            // written through to memory; the second to arrive merges them
+            // with weights 2^(m_part - max m), part 0 first whichever
+            // workgroup computes it, so the bits do not depend on the order.
+            float* mine = xw + ((size_t)(unit * 2 + role) * 4 + w) * kXv * 64 + lane;
+            if (hok)
+#pragma unroll
+                for (uint32_t qt = 0; qt < kQT; qt++) {
+#pragma unroll
+                    for (uint32_t dt = 0; dt < 8; dt++)
+#pragma unroll
+                        for (uint32_t i = 0; i < 4; i++) st_sys(mine + (qt * 32 + dt * 4 + i) * 64, o[qt][dt][i]);
+                    st_sys(mine + (kQT * 32 + 2 * qt) * 64, m[qt]);
+                    st_sys(mine + (kQT * 32 + 2 * qt + 1) * 64, l[qt]);
+                }
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's write-through stores have completed
+            __syncthreads();
+            if (tid == 0) {
+                const uint32_t old = __hip_atomic_fetch_add(xcnt + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                xlast = old;
+                if (old == 1) __hip_atomic_store(xcnt + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+            __syncthreads();
+            if (xlast != 1) return;  // the other part merges
+            const float* other = xw + ((size_t)(unit * 2 + (role ^ 1)) * 4 + w) * kXv * 64 + lane;
+            if (hok)
+#pragma unroll
+                for (uint32_t qt = 0; qt < kQT; qt++) {
+                    const float mo = ld_sys(other + (kQT * 32 + 2 * qt) * 64), lo = ld_sys(other + (kQT * 32 + 2 * qt + 1) * 64);
+                    const float m0 = role ? mo : m[qt], m1 = role ? m[qt] : mo;
+                    const float l0 = role ? lo : l[qt], l1 = role ? l[qt] : lo;
+                    const float mm = fmaxf(m0, m1);
+                    const float a0 = __builtin_amdgcn_exp2f(m0 - mm), a1 = __builtin_amdgcn_exp2f(m1 - mm);
+                    l[qt] = __builtin_fmaf(a0, l0, a1 * l1);
+#pragma unroll
+                    for (uint32_t dt = 0; dt < 8; dt++)
+#pragma unroll
+                        for (uint32_t i = 0; i < 4; i++) {
+                            const float oo = ld_sys(other + (qt * 32 + dt * 4 + i) * 64);
+                            const float o0 = role ? oo : o[qt][dt][i], o1 = role ? o[qt][dt][i] : oo;
+                            o[qt][dt][i] = __builtin_fmaf(a0, o0, a1 * o1);
+                        }
+                }
+        }
         if (hok)
 #pragma unroll
-        for (uint32_t qt = 0; qt < kQT; qt++) {
-            float lt = l[qt] + __shfl_xor(l[qt], 16, 64);
-            lt += __shfl_xor(lt, 32, 64);
-            const float inv = 1.0f / lt;
-            const uint32_t q = q0 + col, hh = kQT * w + qt;
-            if (q < S && hh < G) {
-                _Float16* dst = O16 + (size_t)q * qd + (g * G + hh) * 128 + 4 * grp;
+            for (uint32_t qt = 0; qt < kQT; qt++) {
+                float lt = l[qt] + __shfl_xor(l[qt], 16, 64);
+                lt += __shfl_xor(lt, 32, 64);
+                const float inv = 1.0f / lt;
+                const uint32_t q = q0 + col, hh = kQT * w + qt;
+                if (q < S && hh < G) {
+                    _Float16* dst = O16 + (size_t)q * qd + (g * G + hh) * 128 + 4 * grp;
 #pragma unroll
-                for (uint32_t dt = 0; dt < 8; dt++)
-                    *reinterpret_cast<uint2*>(dst + 16 * dt) =
-                        pack4h(o[qt][dt][0] * inv, o[qt][dt][1] * inv, o[qt][dt][2] * inv, o[qt][dt][3] * inv);
+                    for (uint32_t dt = 0; dt < 8; dt++)
+                        *reinterpret_cast<uint2*>(dst + 16 * dt) =
+                            pack4h(o[qt][dt][0] * inv, o[qt][dt][1] * inv, o[qt][dt][2] * inv, o[qt][dt][3] * inv);
+                }
             }
-        }
-    }
+    };
+    // the workgroup's segments, as two call sites (a loop over them kept
+    // values live across its back edge and spilled): workgroup 0 the long
+    // block (its first part when split), workgroup 1 the long block's second
+    // part (when split), then the short block
+    if (role == 0 || split) run(qL, role ? hs : 0, role || !split ? ntL : hs, split);
+    if (role == 1 && qS != qL) run(qS, 0, ntS, false);
 }
 
 // fp16 copies of the KV cache positions [r0, r0 + gridDim.x) of one layer for
