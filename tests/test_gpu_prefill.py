@@ -129,7 +129,7 @@ def run_and_check(m, spec, img, prompt, extra, label, prior=()):
 
 @pytest.mark.parametrize("n", [1, 31, 32, 33, 64, 65, 100, 257])
 def test_prefill_matches_oracle(dev, model2, n):
-    """Prompt lengths around the 32-query attention blocks and the 64-key
+    """Prompt lengths around the 16-query attention blocks and the 64-key
     blocks; then four decode steps on the prefilled KV cache."""
     spec, img = model2
     prompt = np.random.default_rng(n).integers(0, spec.vocab, n).astype(np.uint32)
