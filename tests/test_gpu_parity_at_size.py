@@ -23,7 +23,9 @@ the reference side, the flip rates are bounded, and the logits and KV bars
 apply to what no flip reached.  A second oracle pass forced to the device's
 own expert ids (the reference's arithmetic with the device's routing) then
 leaves no flip: its logits and every KV row must meet the fp16 bar
-whatever flipped.
+whatever flipped.  A 2-layer model at the same shapes also runs a 2,600-token
+prompt (a 2,048-token chunk, then 552 tokens from position 2,048) against
+the oracle forced to the device's expert ids.
 """
 import importlib
 import os
@@ -218,6 +220,49 @@ def test_config5_prefill_2048_vs_oracle_4_layers(dev, model4):
         f"largest {max(kv_f):.2e}, worst single token {max(kv_t):.2e}")
     assert ferr <= PF_TOL
     assert max(kv_f) <= PF_TOL
+    assert max(kv_t) <= 5 * PF_TOL  # a gross-error guard on single tokens (small-norm K/V rows)
+    s = np.sort(fref)
+    if float(s[-1] - s[-2]) > PF_TOL * float(np.max(np.abs(fref))):
+        assert am == oracle.greedy(fref)
+
+
+@pytest.mark.timeout(900)
+def test_prefill_continuation_chunk_vs_forced_oracle_2_layers(dev):
+    """A 2,600-token prompt at 30B shapes (2 layers, full vocabulary) runs as a
+    2,048-token chunk and a 552-token chunk from position 2,048.  The second
+    chunk's 35 query blocks (an odd count: the middle block pairs with itself)
+    attend to 2,049-2,600 keys each, so every pair splits its long block's keys
+    between two workgroups.  The oracle, routed to the device's expert ids,
+    must match the last token's logits and every KV row of both layers (rows
+    2,048-2,599 written by the continuation chunk) to the fp16 bar."""
+    spec = synth.qwen30b(layers=2, context=2600 + 8)
+    img = synth.build_image(spec, threads=THREADS)
+    n = 2600
+    prompt = np.random.default_rng(2600).integers(0, spec.vocab, n).astype(np.uint32)
+    m = engine.Model(img, spec.context, device=dev)
+    am, lg = m.prefill(prompt)
+    assert m.position == n and m.prefill_reruns == 0
+    dev_routes = m.route_log(0, n)
+    fm = oracle.Model(oracle.Gguf(img), spec.context, threads=THREADS)
+    t0 = time.time()
+    for t in range(n - 1):
+        fm.step(int(prompt[t]), routes=dev_routes[t])
+    fref = fm.forward(int(prompt[-1]), routes=dev_routes[-1])
+    log(f"forced-routing oracle pass, {n} tokens: {time.time() - t0:.0f}s")
+    ferr = rel_err(lg, fref)
+    kv_f, kv_t, kv_c = [], [], []
+    for l in range(spec.layers):
+        k, v = m.read_kv(l, 0, n)
+        fk, fv = fm.kv(l)
+        fk, fv = fk.reshape(k.shape), fv.reshape(v.shape)
+        kv_f.append(max(frob_rel_err(k, fk), frob_rel_err(v, fv)))
+        kv_t.append(max(token_rel_err(k, fk), token_rel_err(v, fv)))
+        kv_c.append(max(frob_rel_err(k[2048:], fk[2048:]), frob_rel_err(v[2048:], fv[2048:])))
+    log(f"2600-token prefill in two chunks, 2 layers: last-token logits rel err {ferr:.2e}; KV rel err "
+        f"(2-norm) per layer largest {max(kv_f):.2e}, over the second chunk's rows {max(kv_c):.2e}, worst "
+        f"single token {max(kv_t):.2e}")
+    assert ferr <= PF_TOL
+    assert max(kv_f) <= PF_TOL and max(kv_c) <= PF_TOL
     assert max(kv_t) <= 5 * PF_TOL  # a gross-error guard on single tokens (small-norm K/V rows)
     s = np.sort(fref)
     if float(s[-1] - s[-2]) > PF_TOL * float(np.max(np.abs(fref))):
