@@ -138,6 +138,22 @@ def test_prefill_matches_oracle(dev, model2, n):
     run_and_check(m, spec, img, prompt, [7, 300, 11, 499], f"n={n}")
 
 
+@pytest.mark.parametrize("heads,kvheads", [(20, 4), (12, 2), (4, 1)])
+def test_prefill_fewer_query_heads_per_kv_head(dev, heads, kvheads):
+    """Batched attention with 5, 6 and 4 query heads per KV head (the
+    kernel's waves take two heads each, so some hold one head or none) and
+    query widths of 2,560, 1,536 and 512: a 257-token prompt (17 query
+    blocks, the long blocks' keys split between two workgroups), then two
+    decode steps, against the oracle."""
+    t = synth._k_types(attn=12, down=12, out=14, embd=12)
+    spec = synth.Spec(2048, 2, heads, kvheads, 128, 128, 8, 768, 512, 512, types=t, more_bits_type=14, seed=heads)
+    img = synth.build_image(spec, threads=min(16, os.cpu_count() or 1))
+    prompt = np.random.default_rng(heads).integers(0, spec.vocab, 257).astype(np.uint32)
+    m = engine.Model(img, spec.context, device=dev)
+    assert m.prefill_batched
+    run_and_check(m, spec, img, prompt, [7, 300], f"{heads} query heads over {kvheads} KV heads")
+
+
 @pytest.mark.parametrize("main,out", [(synth.Q4_0, synth.Q4_0), (synth.Q8_0, synth.Q8_0),
                                       (synth.Q5_K, synth.Q5_K), (synth.Q6_K, synth.Q4_K)])
 def test_prefill_main_formats(dev, main, out):
