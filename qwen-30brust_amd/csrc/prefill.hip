@@ -893,16 +893,17 @@ __global__ __launch_bounds__(1024) void k_pf_group(const uint32_t* ids, uint32_t
     // this thread's assignments a = threadIdx.x + 1024 i, all loaded before
     // any is used (one memory round trip instead of one per assignment)
     constexpr uint32_t kPer = 16;  // 1024 x 16 = 16,384 = a 2,048-token chunk's top-8 assignments
-    uint32_t myid[kPer];
+    uint32_t myid[kPer], mys[kPer];
 #pragma unroll
     for (uint32_t i = 0; i < kPer; i++) {
         const uint32_t a = threadIdx.x + 1024 * i;
         myid[i] = a < n ? ids[a] : 0xffffffffu;
     }
     __syncthreads();
+    // the count's old value is the assignment's slot within its expert
 #pragma unroll
     for (uint32_t i = 0; i < kPer; i++)
-        if (myid[i] < E) atomicAdd(&cnt[myid[i]], 1u);  // ids < E unless routing failed (reported)
+        if (myid[i] < E) mys[i] = atomicAdd(&cnt[myid[i]], 1u);  // ids < E unless routing failed (reported)
     for (uint32_t a = threadIdx.x + 1024 * kPer; a < n; a += 1024)  // chunks beyond 16,384 assignments
         if (ids[a] < E) atomicAdd(&cnt[ids[a]], 1u);
     __syncthreads();
@@ -953,10 +954,10 @@ __global__ __launch_bounds__(1024) void k_pf_group(const uint32_t* ids, uint32_t
     for (uint32_t i = 0; i < kPer; i++) {
         const uint32_t a = threadIdx.x + 1024 * i;
         if (myid[i] >= E) continue;
-        const uint32_t p = atomicAdd(&cur[myid[i]], 1u);
         if (staged) {
-            srt[p] = a;
+            srt[cur[myid[i]] + mys[i]] = a;  // cur = the expert's offset
         } else {
+            const uint32_t p = atomicAdd(&cur[myid[i]], 1u);
             tok[p] = a / top;
             asg[p] = a;
         }
