@@ -66,8 +66,8 @@ __global__ void k_pf_attn(const _Float16*, const _Float16*, const _Float16*, uin
                           uint32_t, uint32_t, _Float16*, float*, uint32_t*);
 __global__ void k_pf_kvh(const float*, const float*, uint32_t, uint32_t, uint32_t, uint32_t, _Float16*, _Float16*);
 __global__ void k_pf_router(const float*, DevMat, uint32_t, uint32_t, uint32_t, float*);
-__global__ void k_pf_topk(const float*, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t*, float*, DevState*, uint32_t*,
-                          float*, uint32_t, uint32_t, uint32_t);
+__global__ void k_pf_topk(const float*, uint32_t, uint32_t, uint32_t, uint32_t*, float*, DevState*, uint32_t*, float*,
+                          uint32_t, uint32_t, uint32_t);
 __global__ void k_pf_group(const uint32_t*, uint32_t, uint32_t, uint32_t, uint32_t*, uint32_t*, uint32_t*, uint32_t*,
                            uint32_t*, uint32_t*);
 __global__ void k_pf_combine(float*, const float*, const float*, uint32_t, uint32_t, const float*, float, _Float16*,
@@ -978,8 +978,6 @@ void prefill_tiles(qh_ctx* c) {
     P.tiled = true;
 }
 
-// column splits of the prefill router logits (partial sums added in order)
-constexpr uint32_t kPfRouterSplit = 8;
 
 void prefill_alloc(qh_ctx* c, uint32_t cap) {
     auto& P = c->pf;
@@ -1085,7 +1083,7 @@ void prefill_layer(qh_ctx* c, size_t l, uint32_t S, uint32_t p0) {
                        (const float*)P.Y, ostride, err);
     hipLaunchKernelGGL(k_pf_router, dim3((S + 63) / 64, kPfRouterSplit), dim3(kBlock), 0, c->s, P.Xn32, L.router,
                        S, H, d.experts, P.LR);
-    hipLaunchKernelGGL(k_pf_topk, dim3((S + kWaves - 1) / kWaves), dim3(kBlock), 0, c->s, P.LR, kPfRouterSplit, S,
+    hipLaunchKernelGGL(k_pf_topk, dim3((S + kWaves - 1) / kWaves), dim3(kBlock), 0, c->s, P.LR, S,
                        d.experts, d.top, P.ids, P.wts, c->acts.st, c->acts.route_log, c->acts.gap_log, d.layers,
                        (uint32_t)l, p0);
     hipLaunchKernelGGL(k_pf_group, dim3(1), dim3(1024), 0, c->s, P.ids, S * d.top, d.top, d.experts, P.goff, P.tok,

@@ -202,6 +202,11 @@ void launch_sample_sort(unsigned long long* cand, uint32_t np, hipStream_t s);
 void launch_sample_fold(const SampleArgs& a, const unsigned long long* cand, float* prob, uint32_t P, uint32_t K,
                         hipStream_t s);
 
+// Column splits of the batched prefill's router logits (prefill.hip:
+// k_pf_router writes one partial sum per split, k_pf_topk adds them in split
+// order).
+constexpr uint32_t kPfRouterSplit = 8;
+
 // Batched-prefill attention (prefill.hip: k_pf_attn): floats of the (O, m, l)
 // hand-over slot of one workgroup (4 waves x 68 values x 64 lanes) when two
 // workgroups share a query block's keys; two slots and a zeroed counter per

@@ -813,18 +813,29 @@ __global__ __launch_bounds__(kBlock) void k_pf_router(const float* Xn, DevMat R,
 // Top-k routing of one token per wave (ops.rs:45-56): the k largest logits
 // under the total order, lower index on ties; softmax over the chosen logits
 // in rank order (ops.rs:29-44).  E <= 128.  The logits are the sum of the
-// router's nks partial sums, added in split order.
-__global__ __launch_bounds__(kBlock) void k_pf_topk(const float* LR, uint32_t nks, uint32_t S, uint32_t E,
+// router's kPfRouterSplit partial sums, added in split order; every partial
+// is requested before the first is added (one memory round trip, not one
+// per split).
+__global__ __launch_bounds__(kBlock) void k_pf_topk(const float* LR, uint32_t S, uint32_t E,
                                                     uint32_t top, uint32_t* ids, float* wts, DevState* st,
                                                     uint32_t* route_log, float* gap_log, uint32_t layers,
                                                     uint32_t layer, uint32_t p0) {
     const uint32_t lane = threadIdx.x & 63, t = blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (t >= S) return;  // wave-uniform
-    float v0 = lane < E ? LR[(size_t)t * E + lane] : 0.f, v1 = lane + 64 < E ? LR[(size_t)t * E + lane + 64] : 0.f;
-    for (uint32_t ks = 1; ks < nks; ks++) {
+    // lanes past E read column E - 1 (in the row) and drop it
+    const uint32_t c0 = min(lane, E - 1), c1 = min(lane + 64, E - 1);
+    float pa[kPfRouterSplit], pb[kPfRouterSplit];
+#pragma unroll
+    for (uint32_t ks = 0; ks < kPfRouterSplit; ks++) {
         const float* lg = LR + ((size_t)ks * S + t) * E;
-        v0 += lane < E ? lg[lane] : 0.f;
-        v1 += lane + 64 < E ? lg[lane + 64] : 0.f;
+        pa[ks] = lg[c0];
+        pb[ks] = lg[c1];
+    }
+    float v0 = lane < E ? pa[0] : 0.f, v1 = lane + 64 < E ? pb[0] : 0.f;
+#pragma unroll
+    for (uint32_t ks = 1; ks < kPfRouterSplit; ks++) {
+        v0 += lane < E ? pa[ks] : 0.f;
+        v1 += lane + 64 < E ? pb[ks] : 0.f;
     }
     const bool bad = (lane < E && !finite_f(v0)) || (lane + 64 < E && !finite_f(v1));
     if (__any(bad)) {
