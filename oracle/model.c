@@ -411,7 +411,7 @@ static int layer_body(or_model *m, size_t i, float *x, size_t pos, kvbuf *kv, si
     MV("ffn_gate_inp", -1, xn, H, logits);
     memcpy(m->last_router + i * c->experts, logits, c->experts * sizeof(float));
     if (m->forced) {
-        /* checker hook: the caller's expert ids in the caller's rank order,
+        /* test hook: the caller's expert ids in the caller's rank order,
          * weighted by the softmax over this path's own logits at those ids
          * (the arithmetic of ops.rs:45-56 after its selection) */
         for (size_t s = 0; s < c->top; s++) {
@@ -441,7 +441,7 @@ out:
     return rc;
 }
 
-/* model.rs:217-302.  vocab = 0 stops after the last layer (a checker's
+/* model.rs:217-302.  vocab = 0 stops after the last layer (a test's
  * shortcut for long prompts whose intermediate logits are not compared: no
  * final norm, vocab projection or finite check; the position still advances). */
 static int forward_inner(or_model *m, uint32_t token, float *logits_out, int threads, int vocab) {

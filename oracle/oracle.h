@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference
  * CPU path (src/quant.rs, src/ops.rs, src/gguf.rs, src/model.rs,
- * src/backend.rs `Cpu`, src/sampling.rs with rand's StdRng restated).  It is the checker
+ * src/backend.rs `Cpu`, src/sampling.rs with rand's StdRng restated).  It is what
  * the HIP engine is compared against; it is never linked into the engine and
  * nothing in the engine calls it.  Only tests/, __graft_entry__.smoke() and
  * bench.py's CPU-baseline leg load it.
@@ -99,7 +99,7 @@ void or_model_reset(or_model *m);                                    /* model.rs
 size_t or_model_position(const or_model *m);
 /* Threads as in or_packed_matvec.  logits may be NULL. */
 int or_model_forward(or_model *m, uint32_t token, float *logits, int threads); /* model.rs:209-302 */
-/* The same step without the final norm and vocab projection (checker shortcut
+/* The same step without the final norm and vocab projection (a test shortcut
  * for long prompts whose intermediate logits are not compared). */
 int or_model_step(or_model *m, uint32_t token, int threads);
 /* Backend::matvec surface: (name, expert) resolved as backend.rs:57-75. */
@@ -115,7 +115,7 @@ int or_layer_forward(or_model *m, size_t layer, float *x, size_t pos,
                      int threads);
 /* Read the model's KV cache for one layer (time-major), for tests. */
 int or_model_kv(const or_model *m, size_t layer, float *k, float *v, size_t cap);
-/* Checker hook (no reference counterpart): the next forward/step routes
+/* Test hook (no reference counterpart): the next forward/step routes
  * layer i to ids[i*top .. i*top+top) in that rank order instead of its own
  * top-k, with weights = softmax of its own router logits at those ids (the
  * arithmetic of ops.rs:45-56 after the selection).  Holds for one step. */

@@ -1,6 +1,6 @@
 """ctypes binding of the CPU oracle (liboracle.so).
 
-TEST INFRASTRUCTURE ONLY: the oracle is the checker the HIP engine is compared
+TEST INFRASTRUCTURE ONLY: the oracle is what the HIP engine is compared
 against.  Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg
 import this module; the engine never does.
 """

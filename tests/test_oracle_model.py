@@ -171,7 +171,7 @@ def _np_forward(g, c, tokens, routes):
 
 
 def test_forced_routes_hook():
-    """The checker's forced-routing hook (or_model_force_routes).  Forcing the
+    """The oracle's forced-routing hook (or_model_force_routes).  Forcing the
     oracle's own expert ids reproduces its forward bit for bit; forcing other
     ids matches a float64 NumPy restatement of model.rs:217-302 that takes
     those ids (so the hook uses the given ids, in the given rank order, with
